@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Decode throughput of the inferox token loop on one MI355X.
+
+Workload (one "step" = one greedy decode token at batch 1): the Llama-3-8B-shape
+synthetic Q4_K_M model (dim 4096, 32 layers, 32/8 heads, ffn 14336, vocab
+128256; Q4_K attn_q/k/o + ffn_gate/up + embedding, Q6_K attn_v/ffn_down/output),
+a 2048-token KV context filled by a GPU prefill of 2048 seeded token ids, then
+`--steps` greedy decode tokens timed end to end (weights and context resident
+in HBM when timing starts).
+
+Prints ONE JSON line (metric, value, roofline of the dominant kernel measured
+with HIP events, cpu_baseline of the CPU oracle on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
+CTX = 2048
+METRIC = "decode tok/s, 8B Q4_K_M bs=1, 1×MI355X; % of HBM-BW roofline"
+KCLASS = ["embed", "qkv_gemv", "attention", "attn_output_gemv", "ffn_gate_up_gemv", "ffn_down_gemv",
+          "output_head_gemv", "finalize"]
+KERNEL_NAMES = {4: "k_gemv<EpiSwiglu>", 5: "k_gemv<EpiResidual>", 6: "k_gemv<EpiLogits>",
+                1: "k_gemv<EpiQkv>", 2: "k_attn_decode"}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=CTX)
+    ap.add_argument("--model-dir", default=os.environ.get("IFX_BENCH_DIR", os.path.join(tempfile.gettempdir(), "inferox_bench")))
+    ap.add_argument("--cpu-steps", type=int, default=1, help="oracle decode steps for cpu_baseline (0: skip)")
+    ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--no-profile", action="store_true")
+    return ap.parse_args()
+
+
+def bytes_per_token(spec, ctx_avg):
+    """Stored weight bytes read per decode token (one embedding row, all layers,
+    final norm, output) + KV at a canonical 2 B/element."""
+    from inferox_amd.synth import byte_size
+    total = 0
+    for name, _, t, r, c in spec.shapes():
+        if name == "token_embd.weight":
+            total += byte_size(t, c)          # one row
+        else:
+            total += byte_size(t, r * c)
+    kv = 2 * spec.n_layers * ctx_avg * spec.kv_dim * 2
+    return total, kv
+
+
+def cpu_baseline(model_path, kv_k, kv_v, ctx, token, n_steps):
+    """The reference algorithm (faithful CPU restatement: per-step full dequant
+    into fresh buffers, AVX2 matmul_t, scalar ops), 1 thread, n_steps decode
+    steps from the same KV state the GPU decoded from."""
+    from oracle import binding as orc
+    orc.set_threads(1)
+    m = orc.Model(model_path)
+    kv = m.kv(ctx + n_steps + 1)
+    assert kv.import_(kv_k, kv_v, ctx) == 0
+    times, toks = [], []
+    t = token
+    for _ in range(n_steps):
+        t0 = time.perf_counter()
+        rc, logits = m.decode_step(kv, t, mode=orc.MODE_FAITHFUL)
+        times.append(time.perf_counter() - t0)
+        assert rc == 0
+        t = orc.argmax(logits)[1]
+        toks.append(t)
+    m.close()
+    med = float(np.median(times))
+    return med, toks
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the token loop runs on a single MI355X; "
+                          "multi-GPU sharding is described in DESIGN.md but not built", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    from inferox_amd import _native, synth
+    from inferox_amd._native import check
+    L = _native.lib()
+
+    spec = synth.LLAMA3_8B
+    os.makedirs(args.model_dir, exist_ok=True)
+    path = os.path.join(args.model_dir, f"{spec.name}-seed1234.gguf")
+    if not os.path.exists(path) or os.path.getsize(path) < spec.gguf_bytes():
+        log(f"writing synthetic {spec.name} ({spec.gguf_bytes() / 1e9:.2f} GB) to {path}")
+        t0 = time.time()
+        synth.write_llama(path, spec, seed=1234)
+        log(f"  written in {time.time() - t0:.1f} s")
+
+    name = C.create_string_buffer(128)
+    ncu, hbm = C.c_int(), C.c_uint64()
+    check(L.ifx_device_info(name, 128, C.byref(ncu), C.byref(hbm)), "device_info")
+    log(f"device: {name.value.decode()} CUs={ncu.value} HBM={hbm.value / 2**30:.0f} GiB")
+
+    t0 = time.time()
+    model = C.c_void_p()
+    check(L.ifx_model_open(path.encode(), C.byref(model)), "model_open")
+    dev_b, gguf_b = C.c_uint64(), C.c_uint64()
+    L.ifx_model_weight_bytes(model, C.byref(dev_b), C.byref(gguf_b))
+    log(f"model uploaded in {time.time() - t0:.1f} s: {dev_b.value / 1e9:.3f} GB in HBM "
+        f"({gguf_b.value / 1e9:.3f} GB stored)")
+
+    K, W = args.steps, args.warmup
+    max_seq = args.ctx + max(K, W) + args.profile_steps + 8
+    sess = C.c_void_p()
+    check(L.ifx_session_create(model, max_seq, C.byref(sess)), "session_create")
+    vocab = spec.vocab
+
+    # warmup on an empty cache (graph capture, clocks), then the real context
+    out = np.zeros(max(K, W, 1), np.uint32)
+    check(L.ifx_decode_greedy(sess, 1, W, out.ctypes.data_as(C.c_void_p)), "warmup")
+    check(L.ifx_session_clear(sess), "clear")
+    ids = synth.token_ids(args.ctx, vocab, seed=2048)
+    t0 = time.perf_counter()
+    check(L.ifx_prefill(sess, ids.ctypes.data_as(C.c_void_p), ids.size, None), "prefill")
+    prefill_s = time.perf_counter() - t0
+    ms = C.c_float()
+    L.ifx_session_last_elapsed_ms(sess, C.byref(ms))
+    log(f"prefill of {args.ctx} tokens: {prefill_s:.2f} s ({args.ctx / prefill_s:.0f} tok/s)")
+
+    # the first generated token = greedy pick of the last prefill row (Model::generate)
+    first = C.c_uint32()
+    check(L.ifx_session_last_token(sess, C.byref(first)), "last_token")
+    start_tok = first.value
+    kv_len = C.c_uint64()
+    L.ifx_session_len(sess, C.byref(kv_len))
+    assert kv_len.value == args.ctx
+    # the context is exported for the CPU baseline before decoding further
+    n_kv = spec.n_layers * args.ctx * spec.kv_dim
+    do_cpu = args.cpu_steps > 0
+    kv_k = np.zeros(n_kv if do_cpu else 1, np.float32)
+    kv_v = np.zeros_like(kv_k)
+    if do_cpu:
+        check(L.ifx_kv_export(sess, kv_k.ctypes.data_as(C.c_void_p), kv_v.ctypes.data_as(C.c_void_p), args.ctx),
+              "kv_export")
+
+    # ---- timed region: K greedy decode steps, synchronized on both sides ----
+    check(L.ifx_stream_synchronize(None), "sync")
+    t0 = time.perf_counter()
+    check(L.ifx_decode_greedy(sess, start_tok, K, out.ctypes.data_as(C.c_void_p)), "decode")
+    wall = time.perf_counter() - t0
+    L.ifx_session_last_elapsed_ms(sess, C.byref(ms))
+    dev_s = ms.value / 1e3
+    tok_s = K / wall
+    log(f"decode {K} tokens: wall {wall * 1e3:.1f} ms ({tok_s:.1f} tok/s), device {dev_s * 1e3:.1f} ms "
+        f"({K / dev_s:.1f} tok/s)")
+
+    w_bytes, kv_bytes = bytes_per_token(spec, args.ctx + (K + 1) / 2)
+    b_tok = w_bytes + kv_bytes
+    frac_tok = tok_s * b_tok / HBM_PEAK
+
+    # ---- dominant kernel: HIP events around every kernel of a decode step ----
+    roofline = None
+    prof = {}
+    if not args.no_profile:
+        avg = (C.c_float * 8)()
+        launches = (C.c_uint64 * 8)()
+        wbytes = (C.c_uint64 * 8)()
+        check(L.ifx_session_profile(sess, int(out[K - 1]), args.profile_steps, avg, launches, wbytes), "profile")
+        per_step = {KCLASS[k]: avg[k] * launches[k] for k in range(8)}
+        dom = max(range(8), key=lambda k: avg[k] * launches[k])
+        # algorithmic bytes of one launch of the dominant kernel: its weight bytes
+        # + the f32 input vector (+ the f32 norm weight when the norm is fused)
+        extra = {1: 2, 4: 2, 6: 2}.get(dom, 1) * spec.dim * 4 if dom != 5 else spec.ffn * 4
+        alg = wbytes[dom] + extra
+        achieved = alg / (avg[dom] * 1e-3)
+        roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                    "kernel": KERNEL_NAMES.get(dom, KCLASS[dom]), "kernel_class": KCLASS[dom],
+                    "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2)}
+        prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "launches_per_step": int(launches[k]),
+                            "weight_bytes": int(wbytes[k]),
+                            "GB_s": round(wbytes[k] / (avg[k] * 1e-3) / 1e9, 1) if avg[k] > 0 and wbytes[k] else None}
+                for k in range(8)}
+        log("per-kernel (events): " + json.dumps(prof))
+        log(f"sum of kernel time per step: {sum(per_step.values()):.3f} ms vs {wall / K * 1e3:.3f} ms per step")
+
+    cpu = None
+    if do_cpu:
+        log(f"cpu baseline: {args.cpu_steps} faithful oracle step(s) at ctx {args.ctx}, 1 thread ...")
+        med, toks = cpu_baseline(path, kv_k, kv_v, args.ctx, start_tok, args.cpu_steps)
+        cpu = {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"{args.cpu_steps} decode step(s) of the same 8B model from the same {args.ctx}-row KV "
+                         f"state, faithful CPU restatement (per-step full dequant, AVX2 matmul_t), median "
+                         f"{med:.2f} s/step; greedy pick {toks[0]} vs GPU {int(out[0])}"}
+        log(f"cpu: {med:.2f} s/step; first pick cpu={toks[0]} gpu={int(out[0])}")
+
+    L.ifx_session_destroy(sess)
+    L.ifx_model_close(model)
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"llama3-8b-shape Q4_K_M greedy decode, bs=1, {args.ctx}-token context from a GPU "
+                               f"prefill of seeded ids, {K} tokens", "ctx": args.ctx, "decode_tokens": K,
+                   "batch": 1},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "roofline_tok": {"bytes_per_token": int(b_tok), "weight_bytes": int(w_bytes), "kv_bytes_f16": int(kv_bytes),
+                         "roofline_tok_s": round(HBM_PEAK / b_tok, 1), "frac": round(frac_tok, 4)},
+        "device_tok_s": round(K / dev_s, 2),
+        "prefill_tok_s": round(args.ctx / prefill_s, 1),
+        "kernels": prof or None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,232 @@
+/*
+ * inferox.h — C ABI of the MI355X (gfx950) inferox token loop.
+ *
+ * This is the drop-in boundary: every entry point replaces one reference
+ * interface (phraakture/inferox, cited as path:line) that a Rust crate would
+ * bind through `extern "C"`.  Plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every call returns an int status (IFX_OK = 0).  Nothing aborts: the
+ *    conditions for which the reference panics (shape asserts, a full KV cache,
+ *    a NaN met by argmax) come back as IFX_E_INVALID_ARG / IFX_E_KV_FULL /
+ *    IFX_E_NAN_LOGIT.  ifx_last_error() gives a message for the calling thread.
+ *  - `ifx_model` is immutable after open and may be shared by threads.  An
+ *    `ifx_session` (KV cache + scratch + one HIP stream) is used by one thread
+ *    at a time, like the reference's `&mut KvCache` / `&mut DecodeBuffers`.
+ *  - Host-pointer outputs are complete when the call returns.
+ *  - Kernel-level entry points (ifx_dequantize_f32, ifx_gemv, ifx_ops_*) take
+ *    device pointers and a stream (NULL = the library's own stream) and are
+ *    asynchronous; ifx_stream_synchronize() waits.
+ */
+#ifndef INFEROX_H
+#define INFEROX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Status codes.  1..12 map one-to-one onto the variants of the reference's
+ * gguf::Error (src/gguf/error.rs:6-42); 20.. replace reference panics.
+ * ------------------------------------------------------------------------- */
+enum {
+  IFX_OK = 0,
+  IFX_E_IO = 1,                   /* Error::Io */
+  IFX_E_INVALID_MAGIC = 2,        /* Error::InvalidMagic */
+  IFX_E_UNSUPPORTED_VERSION = 3,  /* Error::UnsupportedVersion */
+  IFX_E_UNKNOWN_VALUE_TYPE = 4,   /* Error::UnknownValueType */
+  IFX_E_UNKNOWN_TENSOR_TYPE = 5,  /* Error::UnknownTensorType */
+  IFX_E_INVALID_UTF8 = 6,         /* Error::InvalidUtf8 */
+  IFX_E_INVALID_SHAPE = 7,        /* Error::InvalidShape */
+  IFX_E_UNEXPECTED_EOF = 8,       /* Error::UnexpectedEof */
+  IFX_E_TENSOR_NOT_FOUND = 9,     /* Error::TensorNotFound */
+  IFX_E_INVALID_TENSOR_INDEX = 10,/* Error::InvalidTensorIndex */
+  IFX_E_TENSOR_OFFSET_OVERFLOW = 11, /* Error::TensorOffsetOverflow */
+  IFX_E_UNSUPPORTED_ARCH = 12,    /* Error::UnsupportedArchitecture */
+  IFX_E_INVALID_ARG = 20,         /* a reference assert!/slice panic */
+  IFX_E_KV_FULL = 21,             /* KV append past max_seq_len (src/model/forward.rs:376) */
+  IFX_E_HIP = 22,                 /* a HIP runtime call failed */
+  IFX_E_OOM = 23,                 /* device or host allocation failed */
+  IFX_E_NAN_LOGIT = 24,           /* argmax met a NaN (src/model/forward.rs:619 unwrap) */
+  IFX_E_NO_DEVICE = 25            /* no usable gfx950 device */
+};
+
+/* GGML tensor type ids (src/gguf/types.rs:70-100). */
+enum {
+  IFX_TYPE_F32 = 0, IFX_TYPE_F16 = 1, IFX_TYPE_Q4_0 = 2, IFX_TYPE_Q8_0 = 7,
+  IFX_TYPE_Q4_K = 12, IFX_TYPE_Q6_K = 14, IFX_TYPE_Q8_K = 15
+};
+
+/* RoPE position rule of a session.
+ * REFERENCE (default) reproduces the reference exactly: decode rotates q/k at
+ * position 0 (src/model/forward.rs:371-372 with src/ops.rs:270) and prefill at
+ * positions 0..n relative to the chunk (src/model/forward.rs:243-244).
+ * ABSOLUTE rotates at the cache index (len + t). */
+enum { IFX_ROPE_REFERENCE = 0, IFX_ROPE_ABSOLUTE = 1 };
+
+const char* ifx_last_error(void);
+const char* ifx_status_string(int status);
+
+/* ---------------------------------------------------------------------------
+ * Model and session — replaces src/model/{mod,cache,forward}.rs
+ * ------------------------------------------------------------------------- */
+typedef struct ifx_model ifx_model;
+typedef struct ifx_session ifx_session;
+
+/* Config (src/model/config.rs:5-30). */
+typedef struct {
+  uint32_t vocab_size;
+  uint64_t hidden_size;
+  uint64_t n_layers;
+  uint64_t n_heads;
+  uint64_t n_kv_heads;
+  uint64_t head_dim;
+  uint64_t intermediate_size;
+  float norm_eps;
+  float rope_base;
+  uint64_t rope_dim;
+  uint64_t context_length;
+  char architecture[32];
+} ifx_config;
+
+/* Model::open (src/model/mod.rs:64-92): mmap + parse (src/gguf/weights.rs:24-32,
+ * src/gguf/file.rs:57-116), Config::from_gguf (src/model/config.rs:34-84), name
+ * resolution (src/model/mod.rs:34-48).  In addition every weight is uploaded to
+ * HBM once, in its quantized form; nothing is dequantized to f32 in HBM. */
+int ifx_model_open(const char* path, ifx_model** out);
+void ifx_model_close(ifx_model* model);
+int ifx_model_config(const ifx_model* model, ifx_config* out);
+/* Bytes of weights resident in HBM, and the stored GGUF bytes they came from. */
+int ifx_model_weight_bytes(const ifx_model* model, uint64_t* device_bytes, uint64_t* gguf_bytes);
+
+/* KvCache::new + DecodeBuffers::new (src/model/cache.rs:16-24,62-83): a device
+ * KV cache of max_seq_len rows per layer, scratch and one HIP stream. */
+int ifx_session_create(ifx_model* model, uint64_t max_seq_len, ifx_session** out);
+void ifx_session_destroy(ifx_session* s);
+int ifx_session_clear(ifx_session* s);                 /* KvCache::clear (cache.rs:26-28) */
+int ifx_session_len(const ifx_session* s, uint64_t* len);  /* KvCache::len (cache.rs:31-33) */
+int ifx_session_set_rope_mode(ifx_session* s, int mode);
+
+/* Model::decode_step (src/model/forward.rs:543-586).  logits_out: host buffer of
+ * vocab_size floats, or NULL to leave the logits on the device. */
+int ifx_decode_step(ifx_session* s, uint32_t token, float* logits_out);
+
+/* Model::prefill (src/model/forward.rs:496-538): causal over the chunk, writes
+ * K/V at len..len+n, len += n.  logits_out: host [n x vocab], or NULL. */
+int ifx_prefill(ifx_session* s, const uint32_t* ids, uint64_t n, float* logits_out);
+
+/* Model::forward (src/model/forward.rs:448-482): non-causal, no cache; logits
+ * for every row into host logits_out [n x vocab]. */
+int ifx_forward(ifx_model* model, const uint32_t* ids, uint64_t n, float* logits_out);
+
+/* Model::generate (src/model/forward.rs:592-612): clear, prefill, then
+ * max_tokens greedy steps (argmax ties -> last index, src/model/forward.rs:615-622).
+ * The argmax runs on the device; the loop runs without host round trips. */
+int ifx_generate(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t max_tokens,
+                 uint32_t* out_tokens);
+
+/* The decode half of generate: feeds `token`, then n_steps-1 of its own greedy
+ * picks; out_tokens[i] = argmax of step i's logits.  len grows by n_steps. */
+int ifx_decode_greedy(ifx_session* s, uint32_t token, uint64_t n_steps, uint32_t* out_tokens);
+
+/* KV state in the reference layout: k,v = [n_layers][len][n_kv_heads*head_dim]
+ * f32 (src/model/cache.rs:8-24), host memory.  Import sets len. */
+int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len);
+int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len);
+
+/* argmax (src/model/forward.rs:615-622) of the logits of the most recent
+ * step — for a prefill, of its last row: the token generate feeds next. */
+int ifx_session_last_token(ifx_session* s, uint32_t* token);
+
+/* Device time of the last ifx_decode_greedy / ifx_prefill call, measured with
+ * HIP events on the session stream (milliseconds). */
+int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms);
+
+/* Measurement hook (no reference counterpart; the reference has no timers):
+ * n_steps greedy decode steps launched directly with a HIP event pair around
+ * every kernel on the session stream.  Arrays of 8, one per kernel class:
+ * 0 embedding gather, 1 QKV GEMV (+RMSNorm, RoPE, KV append), 2 attention,
+ * 3 attn_output GEMV (+residual), 4 ffn gate/up GEMV (+RMSNorm, SwiGLU),
+ * 5 ffn_down GEMV (+residual), 6 output head GEMV (+RMSNorm, argmax),
+ * 7 finalize.  avg_ms: mean duration per launch; launches: per step;
+ * bytes: stored weight bytes each launch streams.  len grows by n_steps. */
+int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
+                        uint64_t* launches, uint64_t* bytes);
+
+/* ---------------------------------------------------------------------------
+ * Device memory and streams (plumbing for the kernel-level entry points)
+ * ------------------------------------------------------------------------- */
+int ifx_device_info(char* name, uint64_t name_cap, int* n_cu, uint64_t* hbm_bytes);
+int ifx_malloc(void** dptr, uint64_t bytes);
+int ifx_free(void* dptr);
+int ifx_memcpy_h2d(void* dst, const void* src, uint64_t bytes);
+int ifx_memcpy_d2h(void* dst, const void* src, uint64_t bytes);
+int ifx_memcpy_d2d(void* dst, const void* src, uint64_t bytes);
+int ifx_stream_synchronize(void* stream);
+/* HIP event timing on a stream (NULL = library stream). */
+int ifx_timer_start(void* stream);
+int ifx_timer_stop(void* stream, float* ms);
+
+/* ---------------------------------------------------------------------------
+ * Dequantization — replaces gguf::dequantize_f32 (src/gguf/dequant.rs:10-31)
+ * Bit-exact with the reference for F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K; the
+ * same checks in the same order (UnknownTensorType, UnexpectedEof,
+ * InvalidTensorIndex).  `bytes` is the raw GGUF block stream on the device.
+ * ------------------------------------------------------------------------- */
+int ifx_dequantize_f32(uint32_t type, uint64_t n_elements, const void* bytes, uint64_t n_bytes,
+                       float* out, uint64_t n_out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Quantized weight matrices on the device and the fused dequant-GEMV — the
+ * decode (m = 1) case of ops::matmul_t (src/ops.rs:33-44) fed by
+ * Weights::tensor_f32_by_index (src/gguf/weights.rs:66-74), without the f32
+ * copy: y[rows] = W[rows x cols] . x[cols].
+ * ------------------------------------------------------------------------- */
+typedef struct ifx_tensor ifx_tensor;
+
+/* Upload a host GGUF block stream holding a [rows x cols] matrix (row-major,
+ * cols contiguous) into the device layout the GEMV kernels read. */
+int ifx_tensor_upload(uint32_t type, const void* host_bytes, uint64_t n_bytes, uint64_t rows,
+                      uint64_t cols, ifx_tensor** out);
+void ifx_tensor_free(ifx_tensor* t);
+int ifx_tensor_bytes(const ifx_tensor* t, uint64_t* device_bytes, uint64_t* gguf_bytes);
+/* Dequantize an uploaded matrix to f32 [rows x cols] on the device (bit-exact). */
+int ifx_tensor_dequant(const ifx_tensor* t, float* out, void* stream);
+/* y = W x  (x: device f32 [cols], y: device f32 [rows]). */
+int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream);
+/* C[m x rows] = A[m x cols] . W^T for m >= 1 (the prefill form of matmul_t). */
+int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * f32 operators on device buffers — replaces src/ops.rs
+ * ------------------------------------------------------------------------- */
+/* ops::matmul_t (src/ops.rs:33-44): C[m x n] = A[m x k] . B[n x k]^T. */
+int ifx_ops_matmul_t(const float* a, const float* b, float* c, uint64_t m, uint64_t n, uint64_t k,
+                     void* stream);
+/* ops::rms_norm_rows (src/ops.rs:155-180), in place, x = [rows x n]. */
+int ifx_ops_rms_norm_rows(float* x, const float* w, uint64_t n, uint64_t rows, float eps,
+                          void* stream);
+/* ops::swiglu (src/ops.rs:190-197). */
+int ifx_ops_swiglu(const float* gate, const float* up, float* out, uint64_t n, void* stream);
+/* ops::add_in_place (src/ops.rs:212-217). */
+int ifx_ops_add_in_place(float* out, const float* b, uint64_t n, void* stream);
+/* ops::softmax_rows (src/ops.rs:223-239), in place. */
+int ifx_ops_softmax_rows(float* x, uint64_t rows, uint64_t cols, void* stream);
+/* ops::rope (src/ops.rs:265-287), x = [seq x heads x head_dim], positions pos0..pos0+seq. */
+int ifx_ops_rope(float* x, uint64_t seq, uint64_t heads, uint64_t head_dim, uint64_t rope_dim,
+                 float base, uint64_t pos0, void* stream);
+/* ops::embedding_lookup (src/ops.rs:246-258) over an uploaded (quantized) table:
+ * out[n_ids x cols] = dequantized rows ids[i] (bit-exact). ids: device u32. */
+int ifx_ops_embedding_lookup(const ifx_tensor* table, const uint32_t* ids, uint64_t n_ids,
+                             float* out, void* stream);
+/* argmax (src/model/forward.rs:615-622): last index of the maximum; *status_out
+ * (device int) becomes IFX_E_NAN_LOGIT if a NaN is present. out: device u32. */
+int ifx_ops_argmax(const float* x, uint64_t n, uint32_t* out, int* status_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFEROX_H */

@@ -1,0 +1,326 @@
+// capi_ops.cpp — device plumbing, dequantization, uploaded matrices, GEMV and
+// the f32 operators of include/inferox.h.
+#include <string.h>
+
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "ifx_common.h"
+#include "kernels.h"
+
+using namespace ifx;
+
+namespace ifx {
+
+static std::once_flag g_init_once;
+static int g_init_status = IFX_OK;
+static hipStream_t g_stream = nullptr;
+static hipEvent_t g_ev0 = nullptr, g_ev1 = nullptr;
+
+// The library targets gfx950 only: refuse any other device loudly.
+int device_init() {
+  std::call_once(g_init_once, [] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+      g_init_status = IFX_E_NO_DEVICE;
+      return;
+    }
+    hipDeviceProp_t prop;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+      g_init_status = IFX_E_NO_DEVICE;
+      return;
+    }
+    if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&g_ev0) != hipSuccess || hipEventCreate(&g_ev1) != hipSuccess)
+      g_init_status = IFX_E_HIP;
+  });
+  if (g_init_status != IFX_OK)
+    return set_error(g_init_status, "no usable gfx950 device (HIP device count / arch check failed)");
+  return IFX_OK;
+}
+
+static hipStream_t stream_of(void* s) { return s ? (hipStream_t)s : g_stream; }
+
+DevW devw(const ifx_tensor* t) {
+  return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal};
+}
+
+// Parallel host repack (one worker per core share) into a staging buffer.
+static void repack_parallel(uint32_t type, const uint8_t* src, uint64_t nb, uint64_t src_bb,
+                            uint8_t* body, uint64_t body_bb, uint8_t* scal, uint64_t scal_bb) {
+  unsigned nt = std::thread::hardware_concurrency();
+  nt = nt == 0 ? 1 : (nt > 16 ? 16 : nt);
+  if (nb < 65536) nt = 1;
+  std::vector<std::thread> th;
+  const uint64_t per = (nb + nt - 1) / nt;
+  for (unsigned i = 0; i < nt; i++) {
+    const uint64_t b0 = i * per, b1 = b0 + per < nb ? b0 + per : nb;
+    if (b0 >= b1) break;
+    th.emplace_back([=] {
+      repack_to_device_layout(type, src + b0 * src_bb, b1 - b0, body + b0 * body_bb,
+                              scal ? scal + b0 * scal_bb : nullptr);
+    });
+  }
+  for (auto& t : th) t.join();
+}
+
+int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t rows, uint64_t cols,
+                  ifx_tensor** out) {
+  *out = nullptr;
+  if (!gemv_supported(type))
+    return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "tensor type %u has no device layout", type);
+  uint64_t expect;
+  if (!byte_size(type, rows * cols, &expect))
+    return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "tensor type %u", type);
+  if (expect != nbytes)
+    return set_error(IFX_E_UNEXPECTED_EOF, "%llu bytes for a %s [%llu x %llu] matrix, %llu expected",
+                     (unsigned long long)nbytes, type_name(type), (unsigned long long)rows,
+                     (unsigned long long)cols, (unsigned long long)expect);
+  uint64_t body, scal;
+  if (!layout_sizes(type, rows, cols, &body, &scal))
+    return set_error(IFX_E_INVALID_ARG, "%s rows of %llu columns are not whole blocks", type_name(type),
+                     (unsigned long long)cols);
+  ifx_tensor* t = new ifx_tensor();
+  const uint64_t body_al = (body + 255) / 256 * 256;
+  if (hipMalloc(&t->alloc, body_al + scal + 16) != hipSuccess) {
+    delete t;
+    return set_error(IFX_E_OOM, "hipMalloc of %llu bytes failed", (unsigned long long)(body_al + scal));
+  }
+  t->L.type = type;
+  t->L.rows = rows;
+  t->L.cols = cols;
+  t->L.body = (uint8_t*)t->alloc;
+  t->L.scal = scal ? (uint8_t*)t->alloc + body_al : nullptr;
+  t->L.body_bytes = body;
+  t->L.scal_bytes = scal;
+  t->L.gguf_bytes = nbytes;
+  uint64_t be = 1, bb = 0;
+  if (type == T_F32 || type == T_F16) { be = 1; bb = element_size(type); }
+  else block_layout(type, &be, &bb);
+  t->L.n_blocks = rows * cols / be;
+  t->L.blocks_per_row = cols / be;
+  hipError_t e;
+  if (type == T_F32 || type == T_F16 || type == T_Q4K) {
+    e = hipMemcpy(t->L.body, src, nbytes, hipMemcpyHostToDevice);
+  } else {
+    std::vector<uint8_t> stage(body + scal);
+    const uint64_t nb = t->L.n_blocks;
+    repack_parallel(type, src, nb, bb, stage.data(), body / nb, scal ? stage.data() + body : nullptr,
+                    scal / nb);
+    e = hipMemcpy(t->L.body, stage.data(), body, hipMemcpyHostToDevice);
+    if (e == hipSuccess && scal) e = hipMemcpy(t->L.scal, stage.data() + body, scal, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) {
+    (void)hipFree(t->alloc);
+    delete t;
+    return set_error(IFX_E_HIP, "upload failed: %s", hipGetErrorString(e));
+  }
+  *out = t;
+  return IFX_OK;
+}
+
+}  // namespace ifx
+
+extern "C" {
+
+const char* ifx_last_error(void) { return last_error(); }
+
+const char* ifx_status_string(int s) {
+  switch (s) {
+    case IFX_OK: return "ok";
+    case IFX_E_IO: return "io error";
+    case IFX_E_INVALID_MAGIC: return "invalid magic";
+    case IFX_E_UNSUPPORTED_VERSION: return "unsupported GGUF version";
+    case IFX_E_UNKNOWN_VALUE_TYPE: return "unknown metadata value type";
+    case IFX_E_UNKNOWN_TENSOR_TYPE: return "unknown tensor type";
+    case IFX_E_INVALID_UTF8: return "invalid utf-8 string";
+    case IFX_E_INVALID_SHAPE: return "invalid tensor shape";
+    case IFX_E_UNEXPECTED_EOF: return "unexpected end of file";
+    case IFX_E_TENSOR_NOT_FOUND: return "tensor not found";
+    case IFX_E_INVALID_TENSOR_INDEX: return "tensor index out of bounds";
+    case IFX_E_TENSOR_OFFSET_OVERFLOW: return "tensor byte range overflows file bounds";
+    case IFX_E_UNSUPPORTED_ARCH: return "unsupported model architecture";
+    case IFX_E_INVALID_ARG: return "invalid argument";
+    case IFX_E_KV_FULL: return "KV cache full";
+    case IFX_E_HIP: return "HIP runtime error";
+    case IFX_E_OOM: return "out of memory";
+    case IFX_E_NAN_LOGIT: return "NaN logit in argmax";
+    case IFX_E_NO_DEVICE: return "no gfx950 device";
+    default: return "unknown status";
+  }
+}
+
+int ifx_device_info(char* name, uint64_t cap, int* n_cu, uint64_t* hbm) {
+  IFX_TRY(device_init());
+  int dev = 0;
+  IFX_HIP(hipGetDevice(&dev));
+  hipDeviceProp_t p;
+  IFX_HIP(hipGetDeviceProperties(&p, dev));
+  if (name && cap) snprintf(name, cap, "%s (%s)", p.name, p.gcnArchName);
+  if (n_cu) *n_cu = p.multiProcessorCount;
+  if (hbm) *hbm = p.totalGlobalMem;
+  return IFX_OK;
+}
+
+int ifx_malloc(void** p, uint64_t bytes) {
+  IFX_TRY(device_init());
+  if (!p) return set_error(IFX_E_INVALID_ARG, "null pointer");
+  if (hipMalloc(p, bytes ? bytes : 4) != hipSuccess) return set_error(IFX_E_OOM, "hipMalloc(%llu)", (unsigned long long)bytes);
+  return IFX_OK;
+}
+
+int ifx_free(void* p) {
+  if (p) IFX_HIP(hipFree(p));
+  return IFX_OK;
+}
+
+int ifx_memcpy_h2d(void* d, const void* s, uint64_t n) { IFX_TRY(device_init()); IFX_HIP(hipMemcpy(d, s, n, hipMemcpyHostToDevice)); return IFX_OK; }
+int ifx_memcpy_d2h(void* d, const void* s, uint64_t n) { IFX_TRY(device_init()); IFX_HIP(hipStreamSynchronize(g_stream)); IFX_HIP(hipMemcpy(d, s, n, hipMemcpyDeviceToHost)); return IFX_OK; }
+int ifx_memcpy_d2d(void* d, const void* s, uint64_t n) { IFX_TRY(device_init()); IFX_HIP(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToDevice, g_stream)); return IFX_OK; }
+int ifx_stream_synchronize(void* s) { IFX_TRY(device_init()); IFX_HIP(hipStreamSynchronize(stream_of(s))); return IFX_OK; }
+
+int ifx_timer_start(void* s) {
+  IFX_TRY(device_init());
+  IFX_HIP(hipEventRecord(g_ev0, stream_of(s)));
+  return IFX_OK;
+}
+
+int ifx_timer_stop(void* s, float* ms) {
+  IFX_TRY(device_init());
+  IFX_HIP(hipEventRecord(g_ev1, stream_of(s)));
+  IFX_HIP(hipEventSynchronize(g_ev1));
+  IFX_HIP(hipEventElapsedTime(ms, g_ev0, g_ev1));
+  return IFX_OK;
+}
+
+// gguf::dequantize_f32 (src/gguf/dequant.rs:10-31), same check order.
+int ifx_dequantize_f32(uint32_t type, uint64_t n_elements, const void* bytes, uint64_t n_bytes,
+                       float* out, uint64_t n_out, void* stream) {
+  clear_error();
+  IFX_TRY(device_init());
+  uint64_t expected;
+  if (!byte_size(type, n_elements, &expected))
+    return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "unknown tensor type id: %u", type);
+  if (n_bytes != expected) return set_error(IFX_E_UNEXPECTED_EOF, "unexpected end of file");
+  if (n_out != n_elements) return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: %llu", (unsigned long long)n_out);
+  if (!dequant_supported(type)) return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "unknown tensor type id: %u", type);
+  uint64_t be = 1, bb;
+  if (type != T_F32 && type != T_F16) block_layout(type, &be, &bb);
+  if (n_elements % be) return set_error(IFX_E_INVALID_ARG, "%llu elements is not a whole number of blocks", (unsigned long long)n_elements);
+  if (n_elements == 0) return IFX_OK;
+  IFX_HIP(launch_dequant_raw(type, (const uint8_t*)bytes, n_elements, out, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_tensor_upload(uint32_t type, const void* host, uint64_t n_bytes, uint64_t rows, uint64_t cols,
+                      ifx_tensor** out) {
+  clear_error();
+  IFX_TRY(device_init());
+  if (!out || (!host && n_bytes)) return set_error(IFX_E_INVALID_ARG, "null argument");
+  return upload_matrix(type, (const uint8_t*)host, n_bytes, rows, cols, out);
+}
+
+void ifx_tensor_free(ifx_tensor* t) {
+  if (!t) return;
+  if (t->alloc) (void)hipFree(t->alloc);
+  delete t;
+}
+
+int ifx_tensor_bytes(const ifx_tensor* t, uint64_t* dev, uint64_t* gguf) {
+  if (!t) return set_error(IFX_E_INVALID_ARG, "null tensor");
+  if (dev) *dev = t->L.body_bytes + t->L.scal_bytes;
+  if (gguf) *gguf = t->L.gguf_bytes;
+  return IFX_OK;
+}
+
+int ifx_tensor_dequant(const ifx_tensor* t, float* out, void* stream) {
+  IFX_TRY(device_init());
+  if (!t || !out) return set_error(IFX_E_INVALID_ARG, "null argument");
+  IFX_HIP(launch_dequant_dev(devw(t), t->L.rows * t->L.cols, out, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream) {
+  IFX_TRY(device_init());
+  if (!w || !x || !y) return set_error(IFX_E_INVALID_ARG, "null argument");
+  GemvLaunch L;
+  L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows};
+  L.nseg = 1;
+  L.cols = (uint32_t)w->L.cols;
+  L.x = x;
+  IFX_HIP(gemv_store(L, y, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream) {
+  IFX_TRY(device_init());
+  if (!w || (m && (!a || !c))) return set_error(IFX_E_INVALID_ARG, "null argument");
+  for (uint64_t i = 0; i < m; i++) {
+    GemvLaunch L;
+    L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows};
+    L.nseg = 1;
+    L.cols = (uint32_t)w->L.cols;
+    L.x = a + i * w->L.cols;
+    IFX_HIP(gemv_store(L, c + i * w->L.rows, stream_of(stream)));
+  }
+  return IFX_OK;
+}
+
+int ifx_ops_matmul_t(const float* a, const float* b, float* c, uint64_t m, uint64_t n, uint64_t k,
+                     void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_matmul_t_f32(a, b, c, m, n, k, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_rms_norm_rows(float* x, const float* w, uint64_t n, uint64_t rows, float eps, void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_rms_norm_rows(x, w, n, rows, eps, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_swiglu(const float* g, const float* u, float* o, uint64_t n, void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_swiglu(g, u, o, n, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_add_in_place(float* o, const float* b, uint64_t n, void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_add(o, b, n, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_softmax_rows(float* x, uint64_t rows, uint64_t cols, void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_softmax_rows(x, rows, cols, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_rope(float* x, uint64_t seq, uint64_t heads, uint64_t hd, uint64_t rope_dim, float base,
+                 uint64_t pos0, void* stream) {
+  IFX_TRY(device_init());
+  if (rope_dim > hd || (rope_dim & 1)) return set_error(IFX_E_INVALID_ARG, "rope_dim must be even and <= head_dim");
+  if (seq * heads * (rope_dim / 2) == 0) return IFX_OK;
+  IFX_HIP(launch_rope(x, seq, heads, hd, rope_dim, base, pos0, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_embedding_lookup(const ifx_tensor* table, const uint32_t* ids, uint64_t n_ids, float* out,
+                             void* stream) {
+  IFX_TRY(device_init());
+  if (!table) return set_error(IFX_E_INVALID_ARG, "null table");
+  IFX_HIP(launch_embed_rows(devw(table), ids, n_ids, out, stream_of(stream)));
+  return IFX_OK;
+}
+
+int ifx_ops_argmax(const float* x, uint64_t n, uint32_t* out, int* status, void* stream) {
+  IFX_TRY(device_init());
+  IFX_HIP(launch_argmax(x, n, out, status, stream_of(stream)));
+  return IFX_OK;
+}
+
+}  // extern "C"

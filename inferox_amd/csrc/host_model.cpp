@@ -1,0 +1,753 @@
+// host_model.cpp — model upload, sessions and the token loop behind the model
+// half of include/inferox.h.
+//
+// Model::open (src/model/mod.rs:64-92) + Config::from_gguf
+// (src/model/config.rs:34-84), with every weight uploaded to HBM once in its
+// quantized form.  A session owns the device KV cache (the reference's
+// KvCache, src/model/cache.rs:8-24, same [t][kv_dim] f32 rows per layer), the
+// scratch of DecodeBuffers, a HIP stream and one captured decode step that is
+// replayed for every token (positions live in device memory).
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "host_gguf.h"
+#include "ifx_common.h"
+#include "kernels.h"
+
+using namespace ifx;
+
+namespace ifx {
+int device_init();
+int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t rows, uint64_t cols,
+                  ifx_tensor** out);
+DevW devw(const ifx_tensor* t);
+}  // namespace ifx
+
+struct LayerDev {
+  ifx_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+  ifx_tensor *gate = nullptr, *up = nullptr, *down = nullptr;
+  float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+struct ifx_model {
+  MappedFile map;
+  GgufFile gguf;
+  ifx_config cfg{};
+  std::vector<LayerDev> layers;
+  ifx_tensor* embd = nullptr;
+  ifx_tensor* output = nullptr;  // equals embd when output.weight is absent (forward.rs:573)
+  float* out_norm = nullptr;
+  std::vector<void*> norm_allocs;
+  uint64_t dev_bytes = 0, gguf_bytes = 0;
+  bool dims_ok = false;
+};
+
+struct ifx_session {
+  ifx_model* m = nullptr;
+  uint64_t max_seq = 0, len = 0, steps = 0;
+  int rope_mode = IFX_ROPE_REFERENCE;
+  hipStream_t stream = nullptr;
+  float *kc = nullptr, *vc = nullptr;
+  float *hidden = nullptr, *q = nullptr, *attn = nullptr, *mid = nullptr, *logits = nullptr;
+  float* partial = nullptr;
+  uint32_t* counters = nullptr;
+  float2* rope_cs = nullptr;
+  DevState* state = nullptr;
+  uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
+  uint32_t attn_chunk = 64, max_chunks = 0;
+  hipGraphExec_t exec = nullptr;
+  bool graph_tried = false;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  float last_ms = 0.f;
+  std::vector<void*> allocs;
+};
+
+namespace {
+
+const char* kRoleNames[9] = {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+                             "ffn_norm",  "ffn_gate", "ffn_up", "ffn_down"};
+
+int dev_alloc(std::vector<void*>& owner, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 4;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return set_error(IFX_E_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+  owner.push_back(*p);
+  return IFX_OK;
+}
+
+// A norm vector: raw tensor bytes dequantized on the device to f32
+// (Weights::tensor_f32_by_index of the norm weight, src/model/forward.rs:359).
+int upload_norm(ifx_model* m, int64_t idx, uint64_t n, float** out) {
+  const uint8_t* data;
+  uint64_t sz;
+  IFX_TRY(gguf_tensor_bytes(m->gguf, m->map, idx, &data, &sz));
+  const GgufTensor& t = m->gguf.tensors[idx];
+  if (!dequant_supported(t.type))
+    return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "%s: type %u", t.name.c_str(), t.type);
+  if (t.n_elements() != n)
+    return set_error(IFX_E_INVALID_ARG, "%s has %llu elements, expected %llu", t.name.c_str(),
+                     (unsigned long long)t.n_elements(), (unsigned long long)n);
+  void* raw = nullptr;
+  IFX_HIP(hipMalloc(&raw, sz));
+  void* f = nullptr;
+  IFX_TRY(dev_alloc(m->norm_allocs, &f, n * 4));
+  IFX_HIP(hipMemcpy(raw, data, sz, hipMemcpyHostToDevice));
+  IFX_HIP(launch_dequant_raw(t.type, (const uint8_t*)raw, n, (float*)f, nullptr));
+  IFX_HIP(hipDeviceSynchronize());
+  IFX_HIP(hipFree(raw));
+  m->dev_bytes += n * 4;
+  m->gguf_bytes += sz;
+  *out = (float*)f;
+  return IFX_OK;
+}
+
+int upload_weight(ifx_model* m, int64_t idx, uint64_t rows, uint64_t cols, ifx_tensor** out) {
+  const uint8_t* data;
+  uint64_t sz;
+  IFX_TRY(gguf_tensor_bytes(m->gguf, m->map, idx, &data, &sz));
+  const GgufTensor& t = m->gguf.tensors[idx];
+  if (t.n_elements() != rows * cols)
+    return set_error(IFX_E_INVALID_ARG, "%s has %llu elements, expected %llu x %llu", t.name.c_str(),
+                     (unsigned long long)t.n_elements(), (unsigned long long)rows,
+                     (unsigned long long)cols);
+  int rc = upload_matrix(t.type, data, sz, rows, cols, out);
+  if (rc != IFX_OK) return rc;
+  uint64_t db = (*out)->L.body_bytes + (*out)->L.scal_bytes;
+  m->dev_bytes += db;
+  m->gguf_bytes += sz;
+  return IFX_OK;
+}
+
+void model_free(ifx_model* m) {
+  if (!m) return;
+  for (LayerDev& L : m->layers)
+    for (ifx_tensor* t : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) ifx_tensor_free(t);
+  if (m->output && m->output != m->embd) ifx_tensor_free(m->output);
+  ifx_tensor_free(m->embd);
+  for (void* p : m->norm_allocs) (void)hipFree(p);
+  delete m;
+}
+
+int check_dims(const ifx_model* m) {
+  const ifx_config& c = m->cfg;
+  if (c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.n_heads * c.head_dim != c.hidden_size ||
+      c.rope_dim > c.head_dim || (c.rope_dim & 1) || (c.head_dim & 1))
+    return set_error(IFX_E_INVALID_ARG, "inconsistent attention shape (heads %llu/%llu, head_dim %llu, rope_dim %llu)",
+                     (unsigned long long)c.n_heads, (unsigned long long)c.n_kv_heads,
+                     (unsigned long long)c.head_dim, (unsigned long long)c.rope_dim);
+  return IFX_OK;
+}
+
+GemvSeg seg_of(const ifx_tensor* t) {
+  return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows};
+}
+
+// Per-kernel event timing of one step (ifx_session_profile); null when not profiling.
+struct StepProbe {
+  std::vector<hipEvent_t>* ev;  // ev[i] recorded before kernel i, ev[n] after the last
+  std::vector<int>* cls;        // kernel class of kernel i
+  void mark(hipStream_t st, int k) {
+    if (!ev) return;
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    (void)hipEventRecord(e, st);
+    ev->push_back(e);
+    cls->push_back(k);
+  }
+};
+
+// One token through the whole model: embed -> layers -> final norm + head ->
+// greedy bookkeeping.  Every kernel reads positions from s->state.
+int enqueue_step(ifx_session* s, StepProbe probe = StepProbe{nullptr, nullptr}) {
+  ifx_model* m = s->m;
+  const ifx_config& c = m->cfg;
+  hipStream_t st = s->stream;
+  const uint32_t D = (uint32_t)c.hidden_size, F = (uint32_t)c.intermediate_size;
+  const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim);
+  probe.mark(st, 0);
+  IFX_HIP(launch_embed_state(devw(m->embd), s->state, s->hidden, st));
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    const LayerDev& L = m->layers[l];
+    float* kc = s->kc + l * s->max_seq * kvd;
+    float* vc = s->vc + l * s->max_seq * kvd;
+    probe.mark(st, 1);
+    GemvLaunch g;
+    g.seg[0] = seg_of(L.q);
+    g.seg[1] = seg_of(L.k);
+    g.seg[2] = seg_of(L.v);
+    g.nseg = 3;
+    g.cols = D;
+    g.x = s->hidden;
+    g.norm_w = L.attn_norm;
+    g.eps = c.norm_eps;
+    QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd};
+    IFX_HIP(gemv_qkv(g, e, st));
+    probe.mark(st, 2);
+    AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
+               (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
+    IFX_HIP(launch_attn_decode(a, st));
+    probe.mark(st, 3);
+    GemvLaunch go;
+    go.seg[0] = seg_of(L.o);
+    go.nseg = 1;
+    go.cols = D;
+    go.x = s->attn;
+    IFX_HIP(gemv_residual(go, s->hidden, st));
+    probe.mark(st, 4);
+    GemvLaunch gf;
+    gf.seg[0] = seg_of(L.gate);
+    gf.seg[1] = seg_of(L.up);
+    gf.nseg = 2;
+    gf.paired = true;
+    gf.cols = D;
+    gf.x = s->hidden;
+    gf.norm_w = L.ffn_norm;
+    gf.eps = c.norm_eps;
+    IFX_HIP(gemv_swiglu(gf, s->mid, st));
+    probe.mark(st, 5);
+    GemvLaunch gd;
+    gd.seg[0] = seg_of(L.down);
+    gd.nseg = 1;
+    gd.cols = F;
+    gd.x = s->mid;
+    IFX_HIP(gemv_residual(gd, s->hidden, st));
+  }
+  probe.mark(st, 6);
+  GemvLaunch gh;
+  gh.seg[0] = seg_of(m->output);
+  gh.nseg = 1;
+  gh.cols = D;
+  gh.x = s->hidden;
+  gh.norm_w = m->out_norm;
+  gh.eps = c.norm_eps;
+  IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
+  probe.mark(st, 7);
+  IFX_HIP(launch_finalize(s->state, st));
+  probe.mark(st, -1);
+  return IFX_OK;
+}
+
+uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->L.scal_bytes; }
+
+// Replay the captured step (capturing it on first use); direct launches if the
+// runtime refuses capture.
+int run_step(ifx_session* s) {
+  if (!s->graph_tried) {
+    s->graph_tried = true;
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeRelaxed) == hipSuccess) {
+      int rc = enqueue_step(s);
+      hipError_t e = hipStreamEndCapture(s->stream, &g);
+      if (rc == IFX_OK && e == hipSuccess && g) {
+        if (hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0) != hipSuccess) s->exec = nullptr;
+      }
+      if (g) (void)hipGraphDestroy(g);
+      (void)hipGetLastError();
+    }
+  }
+  s->steps++;
+  if (s->exec) {
+    IFX_HIP(hipGraphLaunch(s->exec, s->stream));
+    return IFX_OK;
+  }
+  return enqueue_step(s);
+}
+
+int state_op(ifx_session* s, uint32_t kind, uint32_t value, uint32_t len) {
+  StateOp op{kind, value, len};
+  IFX_HIP(launch_state(s->state, op, s->stream));
+  return IFX_OK;
+}
+
+int check_vocab(const ifx_model* m) {
+  const ifx_config& c = m->cfg;
+  if (m->embd->L.rows < c.vocab_size || m->output->L.rows != c.vocab_size)
+    return set_error(IFX_E_INVALID_ARG, "vocab_size %u does not match the embedding/output rows",
+                     c.vocab_size);
+  return IFX_OK;
+}
+
+void session_free(ifx_session* s) {
+  if (!s) return;
+  if (s->stream) (void)hipStreamSynchronize(s->stream);
+  if (s->exec) (void)hipGraphExecDestroy(s->exec);
+  if (s->ev0) (void)hipEventDestroy(s->ev0);
+  if (s->ev1) (void)hipEventDestroy(s->ev1);
+  for (void* p : s->allocs) (void)hipFree(p);
+  if (s->stream) (void)hipStreamDestroy(s->stream);
+  delete s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ifx_model_open(const char* path, ifx_model** out) {
+  clear_error();
+  if (!out) return set_error(IFX_E_INVALID_ARG, "null output");
+  *out = nullptr;
+  ifx_model* m = new ifx_model();
+  int rc = m->map.open(path);
+  if (rc == IFX_OK) rc = gguf_parse(m->map.data, m->map.size, &m->gguf);
+  if (rc != IFX_OK) { model_free(m); return rc; }
+  const GgufFile& f = m->gguf;
+  ifx_config& c = m->cfg;
+  std::string arch;
+  if (!f.get_string("general.architecture", &arch)) {
+    model_free(m);
+    return set_error(IFX_E_TENSOR_NOT_FOUND, "general.architecture");
+  }
+  if (arch != "llama") {
+    model_free(m);
+    return set_error(IFX_E_UNSUPPORTED_ARCH, "unsupported model architecture: %s", arch.c_str());
+  }
+  snprintf(c.architecture, sizeof c.architecture, "%s", arch.c_str());
+  const char* req[3] = {"llama.embedding_length", "llama.block_count", "llama.attention.head_count"};
+  uint64_t* dst[3] = {&c.hidden_size, &c.n_layers, &c.n_heads};
+  for (int i = 0; i < 3; i++)
+    if (!f.get_u64(req[i], dst[i])) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "%s", req[i]); }
+  uint32_t u;
+  c.n_kv_heads = f.get_u32("llama.attention.head_count_kv", &u) ? u : c.n_heads;
+  if (c.n_heads == 0) { model_free(m); return set_error(IFX_E_INVALID_ARG, "head_count is 0"); }
+  c.head_dim = f.get_u32("llama.attention.key_length", &u) ? u : c.hidden_size / c.n_heads;
+  if (!f.get_u64("llama.feed_forward_length", &c.intermediate_size)) {
+    model_free(m);
+    return set_error(IFX_E_TENSOR_NOT_FOUND, "llama.feed_forward_length");
+  }
+  if (!f.get_f32("llama.attention.layer_norm_rms_epsilon", &c.norm_eps)) c.norm_eps = 1e-5f;
+  if (!f.get_f32("llama.rope.freq_base", &c.rope_base)) c.rope_base = 10000.0f;
+  c.rope_dim = f.get_u32("llama.rope.dimension_count", &u) ? u : c.head_dim;
+  c.context_length = f.get_u32("llama.context_length", &u) ? u : 4096;
+  c.vocab_size = f.get_u32("llama.vocab_size", &u) ? u : 0;
+
+  // name resolution (src/model/mod.rs:34-48,64-92)
+  std::vector<int64_t> idx(c.n_layers * 9);
+  for (uint64_t l = 0; l < c.n_layers; l++)
+    for (int r = 0; r < 9; r++) {
+      char nm[128];
+      snprintf(nm, sizeof nm, "blk.%llu.%s.weight", (unsigned long long)l, kRoleNames[r]);
+      idx[l * 9 + r] = f.tensor_index(nm);
+      if (idx[l * 9 + r] < 0) {
+        model_free(m);
+        return set_error(IFX_E_TENSOR_NOT_FOUND, "blk.%llu.*", (unsigned long long)l);
+      }
+    }
+  int64_t i_embd = f.tensor_index("token_embd.weight");
+  if (i_embd < 0) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "token_embd.weight"); }
+  int64_t i_onorm = f.tensor_index("output_norm.weight");
+  if (i_onorm < 0) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "output_norm.weight"); }
+  int64_t i_out = f.tensor_index("output.weight");
+
+  // upload once (parse errors above are reported without touching a device)
+  rc = device_init();
+  if (rc != IFX_OK) { model_free(m); return rc; }
+  const uint64_t D = c.hidden_size, F = c.intermediate_size, KV = c.n_kv_heads * c.head_dim;
+  m->dims_ok = check_dims(m) == IFX_OK;
+  clear_error();
+  const uint64_t embd_n = f.tensors[i_embd].n_elements();
+  if (D == 0 || embd_n % D) {
+    model_free(m);
+    return set_error(IFX_E_INVALID_ARG, "token_embd.weight is not [*, %llu]", (unsigned long long)D);
+  }
+  rc = upload_weight(m, i_embd, embd_n / D, D, &m->embd);
+  if (rc == IFX_OK && i_out >= 0) {
+    const uint64_t n = f.tensors[i_out].n_elements();
+    rc = n % D ? set_error(IFX_E_INVALID_ARG, "output.weight is not [*, %llu]", (unsigned long long)D)
+               : upload_weight(m, i_out, n / D, D, &m->output);
+  } else if (rc == IFX_OK) {
+    m->output = m->embd;
+  }
+  if (rc == IFX_OK) rc = upload_norm(m, i_onorm, D, &m->out_norm);
+  m->layers.resize(c.n_layers);
+  for (uint64_t l = 0; l < c.n_layers && rc == IFX_OK; l++) {
+    LayerDev& L = m->layers[l];
+    const int64_t* x = &idx[l * 9];
+    if (rc == IFX_OK) rc = upload_norm(m, x[0], D, &L.attn_norm);
+    if (rc == IFX_OK) rc = upload_weight(m, x[1], D, D, &L.q);
+    if (rc == IFX_OK) rc = upload_weight(m, x[2], KV, D, &L.k);
+    if (rc == IFX_OK) rc = upload_weight(m, x[3], KV, D, &L.v);
+    if (rc == IFX_OK) rc = upload_weight(m, x[4], D, D, &L.o);
+    if (rc == IFX_OK) rc = upload_norm(m, x[5], D, &L.ffn_norm);
+    if (rc == IFX_OK) rc = upload_weight(m, x[6], F, D, &L.gate);
+    if (rc == IFX_OK) rc = upload_weight(m, x[7], F, D, &L.up);
+    if (rc == IFX_OK) rc = upload_weight(m, x[8], D, F, &L.down);
+    if (rc == IFX_OK && (L.q->L.type != L.k->L.type || L.gate->L.type != L.up->L.type))
+      rc = set_error(IFX_E_INVALID_ARG, "layer %llu: attn_q/attn_k or ffn_gate/ffn_up types differ",
+                     (unsigned long long)l);
+  }
+  if (rc != IFX_OK) { model_free(m); return rc; }
+  *out = m;
+  return IFX_OK;
+}
+
+void ifx_model_close(ifx_model* m) { model_free(m); }
+
+int ifx_model_config(const ifx_model* m, ifx_config* out) {
+  if (!m || !out) return set_error(IFX_E_INVALID_ARG, "null argument");
+  *out = m->cfg;
+  return IFX_OK;
+}
+
+int ifx_model_weight_bytes(const ifx_model* m, uint64_t* dev, uint64_t* gguf) {
+  if (!m) return set_error(IFX_E_INVALID_ARG, "null model");
+  if (dev) *dev = m->dev_bytes;
+  if (gguf) *gguf = m->gguf_bytes;
+  return IFX_OK;
+}
+
+int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
+  clear_error();
+  if (!m || !out || max_seq_len == 0 || max_seq_len > 0x7fffffffull)
+    return set_error(IFX_E_INVALID_ARG, "bad session arguments");
+  *out = nullptr;
+  IFX_TRY(check_dims(m));
+  const ifx_config& c = m->cfg;
+  ifx_session* s = new ifx_session();
+  s->m = m;
+  s->max_seq = max_seq_len;
+  const uint64_t D = c.hidden_size, F = c.intermediate_size, kvd = c.n_kv_heads * c.head_dim;
+  const uint64_t G = c.n_heads / c.n_kv_heads;
+  s->max_chunks = (uint32_t)((max_seq_len + s->attn_chunk - 1) / s->attn_chunk);
+  int rc = IFX_OK;
+  auto A = [&](void** p, size_t b) { if (rc == IFX_OK) rc = dev_alloc(s->allocs, p, b); };
+  A((void**)&s->kc, c.n_layers * max_seq_len * kvd * 4);
+  A((void**)&s->vc, c.n_layers * max_seq_len * kvd * 4);
+  A((void**)&s->hidden, D * 4);
+  A((void**)&s->q, D * 4);
+  A((void**)&s->attn, D * 4);
+  A((void**)&s->mid, F * 4);
+  A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
+  A((void**)&s->partial, c.n_kv_heads * s->max_chunks * G * (c.head_dim + 2) * 4);
+  A((void**)&s->counters, c.n_kv_heads * 4);
+  A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
+  A((void**)&s->state, sizeof(DevState));
+  A((void**)&s->out_tokens, max_seq_len * 4);
+  A((void**)&s->feed_ids, max_seq_len * 4);
+  if (rc != IFX_OK) { session_free(s); return rc; }
+  if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
+    session_free(s);
+    return set_error(IFX_E_HIP, "stream/event creation failed");
+  }
+  // RoPE table in the reference arithmetic (src/ops.rs:278-280), glibc powf/sinf/cosf:
+  // inv = 1/powf(base, i/rope_dim); angle = pos*inv.
+  const uint64_t half = c.rope_dim / 2;
+  std::vector<float2> cs(max_seq_len * std::max<uint64_t>(half, 1));
+  std::vector<float> inv(half);
+  for (uint64_t i = 0; i < half; i++)
+    inv[i] = 1.0f / powf(c.rope_base, (float)(2 * i) / (float)c.rope_dim);
+  for (uint64_t p = 0; p < max_seq_len; p++)
+    for (uint64_t i = 0; i < half; i++) {
+      const float ang = (float)p * inv[i];
+      cs[p * half + i] = make_float2(cosf(ang), sinf(ang));
+    }
+  DevState init{};
+  init.rope_mode = IFX_ROPE_REFERENCE;
+  init.feed_ids = s->feed_ids;
+  init.out_tokens = s->out_tokens;
+  init.out_cap = (uint32_t)max_seq_len;
+  if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemset(s->counters, 0, c.n_kv_heads * 4) != hipSuccess ||
+      hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
+      hipMemset(s->vc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    session_free(s);
+    return set_error(IFX_E_HIP, "session initialisation failed");
+  }
+  *out = s;
+  return IFX_OK;
+}
+
+void ifx_session_destroy(ifx_session* s) { session_free(s); }
+
+int ifx_session_clear(ifx_session* s) {
+  if (!s) return set_error(IFX_E_INVALID_ARG, "null session");
+  IFX_TRY(state_op(s, STATE_RESET, 0, 0));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  s->len = 0;
+  s->steps = 0;
+  return IFX_OK;
+}
+
+int ifx_session_len(const ifx_session* s, uint64_t* len) {
+  if (!s || !len) return set_error(IFX_E_INVALID_ARG, "null argument");
+  *len = s->len;
+  return IFX_OK;
+}
+
+int ifx_session_set_rope_mode(ifx_session* s, int mode) {
+  if (!s || (mode != IFX_ROPE_REFERENCE && mode != IFX_ROPE_ABSOLUTE))
+    return set_error(IFX_E_INVALID_ARG, "bad rope mode");
+  s->rope_mode = mode;
+  IFX_TRY(state_op(s, STATE_MODE, (uint32_t)mode, 0));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  return IFX_OK;
+}
+
+int ifx_decode_step(ifx_session* s, uint32_t token, float* logits_out) {
+  clear_error();
+  if (!s) return set_error(IFX_E_INVALID_ARG, "null session");
+  ifx_model* m = s->m;
+  if (token >= m->cfg.vocab_size)
+    return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: %u", token);
+  IFX_TRY(check_vocab(m));
+  if (s->len >= s->max_seq) return set_error(IFX_E_KV_FULL, "KV cache full (%llu rows)", (unsigned long long)s->max_seq);
+  IFX_TRY(state_op(s, STATE_DECODE, token, 0));
+  IFX_TRY(run_step(s));
+  if (logits_out)
+    IFX_HIP(hipMemcpyAsync(logits_out, s->logits, (size_t)m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, s->stream));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  s->len += 1;
+  return IFX_OK;
+}
+
+int ifx_prefill(ifx_session* s, const uint32_t* ids, uint64_t n, float* logits_out) {
+  clear_error();
+  if (!s || (n && !ids)) return set_error(IFX_E_INVALID_ARG, "null argument");
+  ifx_model* m = s->m;
+  for (uint64_t i = 0; i < n; i++)
+    if (ids[i] >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: 0");
+  if (n == 0) return IFX_OK;
+  IFX_TRY(check_vocab(m));
+  if (s->len + n > s->max_seq) return set_error(IFX_E_KV_FULL, "prefill of %llu rows overflows the KV cache", (unsigned long long)n);
+  IFX_HIP(hipMemcpyAsync(s->feed_ids, ids, n * 4, hipMemcpyHostToDevice, s->stream));
+  IFX_TRY(state_op(s, STATE_PREFILL, 0, (uint32_t)n));
+  IFX_HIP(hipEventRecord(s->ev0, s->stream));
+  const size_t V = m->cfg.vocab_size;
+  for (uint64_t t = 0; t < n; t++) {
+    IFX_TRY(run_step(s));
+    if (logits_out)
+      IFX_HIP(hipMemcpyAsync(logits_out + t * V, s->logits, V * 4, hipMemcpyDeviceToHost, s->stream));
+  }
+  IFX_HIP(hipEventRecord(s->ev1, s->stream));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
+  s->len += n;
+  return IFX_OK;
+}
+
+int ifx_decode_greedy(ifx_session* s, uint32_t token, uint64_t n_steps, uint32_t* out_tokens) {
+  clear_error();
+  if (!s || (n_steps && !out_tokens)) return set_error(IFX_E_INVALID_ARG, "null argument");
+  ifx_model* m = s->m;
+  if (token >= m->cfg.vocab_size)
+    return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: %u", token);
+  IFX_TRY(check_vocab(m));
+  if (s->len + n_steps > s->max_seq) return set_error(IFX_E_KV_FULL, "%llu steps overflow the KV cache", (unsigned long long)n_steps);
+  const uint64_t first = s->steps;
+  IFX_TRY(state_op(s, STATE_DECODE, token, 0));
+  IFX_HIP(hipEventRecord(s->ev0, s->stream));
+  for (uint64_t i = 0; i < n_steps; i++) IFX_TRY(run_step(s));
+  IFX_HIP(hipEventRecord(s->ev1, s->stream));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
+  s->len += n_steps;
+  if (n_steps == 0) return IFX_OK;
+  IFX_HIP(hipMemcpy(out_tokens, s->out_tokens + first, n_steps * 4, hipMemcpyDeviceToHost));
+  int rc = IFX_OK;
+  for (uint64_t i = 0; i < n_steps; i++) {
+    if (out_tokens[i] & 0x80000000u) rc = IFX_E_NAN_LOGIT;
+    out_tokens[i] &= 0x7fffffffu;
+  }
+  return rc == IFX_OK ? IFX_OK : set_error(rc, "NaN logit met by argmax");
+}
+
+int ifx_generate(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t max_tokens,
+                 uint32_t* out_tokens) {
+  clear_error();
+  if (!s || !prompt || (max_tokens && !out_tokens)) return set_error(IFX_E_INVALID_ARG, "null argument");
+  if (n == 0) return set_error(IFX_E_INVALID_ARG, "empty prompt");
+  IFX_TRY(ifx_session_clear(s));
+  if (n + max_tokens > s->max_seq) {
+    // validate ids first so the reference's error order (InvalidTensorIndex) is kept
+    for (uint64_t i = 0; i < n; i++)
+      if (prompt[i] >= s->m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: 0");
+    return set_error(IFX_E_KV_FULL, "prompt + max_tokens exceeds the KV cache");
+  }
+  IFX_TRY(ifx_prefill(s, prompt, n, nullptr));
+  // the greedy loop continues on the device: the last prefill step left its
+  // argmax as the next input token (src/model/forward.rs:605-609)
+  IFX_HIP(hipEventRecord(s->ev0, s->stream));
+  for (uint64_t i = 0; i < max_tokens; i++) IFX_TRY(run_step(s));
+  IFX_HIP(hipEventRecord(s->ev1, s->stream));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
+  s->len += max_tokens;
+  if (max_tokens == 0) return IFX_OK;
+  IFX_HIP(hipMemcpy(out_tokens, s->out_tokens + (n - 1), max_tokens * 4, hipMemcpyDeviceToHost));
+  int rc = IFX_OK;
+  for (uint64_t i = 0; i < max_tokens; i++) {
+    if (out_tokens[i] & 0x80000000u) rc = IFX_E_NAN_LOGIT;
+    out_tokens[i] &= 0x7fffffffu;
+  }
+  return rc == IFX_OK ? IFX_OK : set_error(rc, "NaN logit met by argmax");
+}
+
+int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len) {
+  if (!s || (len && (!k || !v))) return set_error(IFX_E_INVALID_ARG, "null argument");
+  if (len > s->max_seq) return set_error(IFX_E_KV_FULL, "import of %llu rows", (unsigned long long)len);
+  const ifx_config& c = s->m->cfg;
+  const uint64_t kvd = c.n_kv_heads * c.head_dim;
+  for (uint64_t l = 0; l < c.n_layers; l++) {
+    IFX_HIP(hipMemcpyAsync(s->kc + l * s->max_seq * kvd, k + l * len * kvd, len * kvd * 4, hipMemcpyHostToDevice, s->stream));
+    IFX_HIP(hipMemcpyAsync(s->vc + l * s->max_seq * kvd, v + l * len * kvd, len * kvd * 4, hipMemcpyHostToDevice, s->stream));
+  }
+  IFX_TRY(state_op(s, STATE_RESET, 0, (uint32_t)len));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  s->len = len;
+  s->steps = 0;
+  return IFX_OK;
+}
+
+int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len) {
+  if (!s || (len && (!k || !v))) return set_error(IFX_E_INVALID_ARG, "null argument");
+  if (len > s->len) return set_error(IFX_E_INVALID_ARG, "export of %llu rows, %llu cached", (unsigned long long)len, (unsigned long long)s->len);
+  const ifx_config& c = s->m->cfg;
+  const uint64_t kvd = c.n_kv_heads * c.head_dim;
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  for (uint64_t l = 0; l < c.n_layers; l++) {
+    IFX_HIP(hipMemcpy(k + l * len * kvd, s->kc + l * s->max_seq * kvd, len * kvd * 4, hipMemcpyDeviceToHost));
+    IFX_HIP(hipMemcpy(v + l * len * kvd, s->vc + l * s->max_seq * kvd, len * kvd * 4, hipMemcpyDeviceToHost));
+  }
+  return IFX_OK;
+}
+
+// Measurement hook: n_steps greedy decode steps with direct launches and a HIP
+// event pair around every kernel on the session stream.  Per kernel class
+// (0 embed, 1 qkv+rope+kv-append, 2 attention, 3 attn_output+residual,
+//  4 ffn gate/up+swiglu, 5 ffn_down+residual, 6 output head+argmax, 7 finalize):
+// avg_ms = mean duration per launch, launches = launches per step,
+// bytes = stored weight bytes streamed per launch (0 where no weights).
+int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
+                        uint64_t* launches, uint64_t* bytes) {
+  clear_error();
+  if (!s || !avg_ms || !launches || !bytes || n_steps == 0) return set_error(IFX_E_INVALID_ARG, "bad arguments");
+  ifx_model* m = s->m;
+  if (token >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "token");
+  IFX_TRY(check_vocab(m));
+  if (s->len + n_steps > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
+  double sum[8] = {0};
+  uint64_t cnt[8] = {0};
+  IFX_TRY(state_op(s, STATE_DECODE, token, 0));
+  for (uint64_t i = 0; i < n_steps; i++) {
+    std::vector<hipEvent_t> ev;
+    std::vector<int> cls;
+    int rc = enqueue_step(s, StepProbe{&ev, &cls});
+    s->steps++;
+    IFX_HIP(hipStreamSynchronize(s->stream));
+    for (size_t k = 0; k + 1 < ev.size(); k++) {
+      float ms = 0.f;
+      (void)hipEventElapsedTime(&ms, ev[k], ev[k + 1]);
+      if (cls[k] >= 0 && cls[k] < 8) { sum[cls[k]] += ms; cnt[cls[k]]++; }
+    }
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    if (rc != IFX_OK) return rc;
+  }
+  s->len += n_steps;
+  for (int k = 0; k < 8; k++) {
+    avg_ms[k] = cnt[k] ? (float)(sum[k] / cnt[k]) : 0.f;
+    launches[k] = cnt[k] / n_steps;
+  }
+  const LayerDev& L0 = m->layers.empty() ? LayerDev{} : m->layers[0];
+  bytes[0] = 0;
+  bytes[1] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.q) + tensor_stream_bytes(L0.k) + tensor_stream_bytes(L0.v);
+  bytes[2] = 0;
+  bytes[3] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.o);
+  bytes[4] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.gate) + tensor_stream_bytes(L0.up);
+  bytes[5] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.down);
+  bytes[6] = tensor_stream_bytes(m->output);
+  bytes[7] = 0;
+  return IFX_OK;
+}
+
+int ifx_session_last_token(ifx_session* s, uint32_t* token) {
+  if (!s || !token) return set_error(IFX_E_INVALID_ARG, "null argument");
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  IFX_HIP(hipMemcpy(token, &s->state->cur_token, 4, hipMemcpyDeviceToHost));
+  return IFX_OK;
+}
+
+int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms) {
+  if (!s || !ms) return set_error(IFX_E_INVALID_ARG, "null argument");
+  *ms = s->last_ms;
+  return IFX_OK;
+}
+
+// Model::forward (src/model/forward.rs:448-482): non-causal attention over the
+// chunk, no cache carried over.  Layer-major: each layer runs its GEMVs for all
+// rows before the next layer, since every row attends to every other row.
+int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out) {
+  clear_error();
+  if (!m || (n && (!ids || !logits_out))) return set_error(IFX_E_INVALID_ARG, "null argument");
+  for (uint64_t i = 0; i < n; i++)
+    if (ids[i] >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: 0");
+  if (n == 0) return IFX_OK;
+  IFX_TRY(check_vocab(m));
+  ifx_session* s = nullptr;
+  IFX_TRY(ifx_session_create(m, n, &s));
+  const ifx_config& c = m->cfg;
+  const uint64_t D = c.hidden_size, F = c.intermediate_size, kvd = c.n_kv_heads * c.head_dim;
+  const size_t V = c.vocab_size;
+  float *X = nullptr, *Q = nullptr, *A = nullptr;
+  uint32_t* dids = nullptr;
+  int rc = dev_alloc(s->allocs, (void**)&X, n * D * 4);
+  if (rc == IFX_OK) rc = dev_alloc(s->allocs, (void**)&Q, n * D * 4);
+  if (rc == IFX_OK) rc = dev_alloc(s->allocs, (void**)&A, n * D * 4);
+  if (rc == IFX_OK) rc = dev_alloc(s->allocs, (void**)&dids, n * 4);
+  hipStream_t st = s->stream;
+  auto hip = [&](hipError_t e) {
+    if (rc == IFX_OK && e != hipSuccess) rc = set_error(IFX_E_HIP, "forward: %s", hipGetErrorString(e));
+  };
+  if (rc == IFX_OK) {
+    hip(hipMemcpyAsync(dids, ids, n * 4, hipMemcpyHostToDevice, st));
+    hip(launch_embed_rows(devw(m->embd), dids, n, X, st));
+  }
+  for (size_t l = 0; l < m->layers.size() && rc == IFX_OK; l++) {
+    const LayerDev& L = m->layers[l];
+    float* kc = s->kc + l * s->max_seq * kvd;
+    float* vc = s->vc + l * s->max_seq * kvd;
+    for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
+      hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
+      GemvLaunch g;
+      g.seg[0] = seg_of(L.q); g.seg[1] = seg_of(L.k); g.seg[2] = seg_of(L.v);
+      g.nseg = 3; g.cols = (uint32_t)D; g.x = X + t * D; g.norm_w = L.attn_norm; g.eps = c.norm_eps;
+      QkvEpi e{Q + t * D, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, (uint32_t)kvd};
+      hip(gemv_qkv(g, e, st));
+    }
+    for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
+      hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
+      AttnArgs a{Q + t * D, kc, vc, A + t * D, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
+                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
+      hip(launch_attn_decode(a, st));
+    }
+    for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
+      GemvLaunch go;
+      go.seg[0] = seg_of(L.o); go.nseg = 1; go.cols = (uint32_t)D; go.x = A + t * D;
+      hip(gemv_residual(go, X + t * D, st));
+      GemvLaunch gf;
+      gf.seg[0] = seg_of(L.gate); gf.seg[1] = seg_of(L.up); gf.nseg = 2; gf.paired = true;
+      gf.cols = (uint32_t)D; gf.x = X + t * D; gf.norm_w = L.ffn_norm; gf.eps = c.norm_eps;
+      hip(gemv_swiglu(gf, s->mid, st));
+      GemvLaunch gd;
+      gd.seg[0] = seg_of(L.down); gd.nseg = 1; gd.cols = (uint32_t)F; gd.x = s->mid;
+      hip(gemv_residual(gd, X + t * D, st));
+    }
+  }
+  for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
+    GemvLaunch gh;
+    gh.seg[0] = seg_of(m->output); gh.nseg = 1; gh.cols = (uint32_t)D; gh.x = X + t * D;
+    gh.norm_w = m->out_norm; gh.eps = c.norm_eps;
+    hip(gemv_logits(gh, s->logits, s->state, st));
+    hip(hipMemcpyAsync(logits_out + t * V, s->logits, V * 4, hipMemcpyDeviceToHost, st));
+  }
+  hip(hipStreamSynchronize(st));
+  session_free(s);
+  return rc;
+}
+
+}  // extern "C"

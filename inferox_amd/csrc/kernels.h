@@ -1,0 +1,110 @@
+// kernels.h — host-side launchers of the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dev_quant.h"
+#include "ifx_common.h"
+
+namespace ifx {
+
+// Per-session state that lives in device memory, so that one captured decode
+// step replays correctly for every token (the kernels read positions from here,
+// the finalize kernel advances them).
+struct DevState {
+  uint32_t len;          // cache rows holding keys/values before the current token
+  uint32_t rope_pos;     // RoPE position of the current token
+  uint32_t attn_lo;      // first cache row the current token attends to
+  uint32_t cur_token;    // token fed to the next step's embedding gather
+  uint32_t step;         // next slot of out_tokens
+  uint32_t rope_mode;    // IFX_ROPE_REFERENCE / IFX_ROPE_ABSOLUTE
+  uint32_t prefill;      // 1 while a prefill chunk is being fed
+  uint32_t chunk_start;  // cache index of the first token of the prefill chunk
+  uint32_t feed_n;       // tokens in feed_ids (prefill)
+  int32_t status;        // IFX_OK, or IFX_E_NAN_LOGIT once a NaN logit was seen
+  unsigned long long argmax_key;  // packed (ordered logit << 32 | index), max-reduced
+  const uint32_t* feed_ids;       // prefill token ids (device)
+  uint32_t* out_tokens;           // greedy picks (device)
+  uint32_t out_cap;
+  uint32_t attn_end;     // 0: attend rows [attn_lo, len]; else rows [attn_lo, attn_end)
+};
+
+// ---- dequantization (kern_dequant.hip) ----
+hipError_t launch_dequant_raw(uint32_t type, const uint8_t* bytes, uint64_t n, float* out,
+                              hipStream_t st);
+hipError_t launch_dequant_dev(const DevW& w, uint64_t n, float* out, hipStream_t st);
+hipError_t launch_embed_rows(const DevW& w, const uint32_t* ids, uint64_t n_ids, float* out,
+                             hipStream_t st);
+// hidden[cols] = row state->cur_token of the table
+hipError_t launch_embed_state(const DevW& w, const DevState* state, float* hidden, hipStream_t st);
+
+// ---- fused GEMV (kern_gemv.hip) ----
+struct GemvSeg {
+  const uint8_t* body;
+  const uint8_t* scal;
+  uint32_t type;
+  uint32_t rows;
+};
+
+struct GemvLaunch {
+  GemvSeg seg[3];
+  int nseg = 0;
+  uint32_t cols = 0;
+  const float* x = nullptr;       // input vector [cols]
+  const float* norm_w = nullptr;  // non-null: x := rms_norm(x, norm_w, eps) in the prologue
+  float eps = 0.f;
+  bool paired = false;            // seg[0]/seg[1] rows interleaved per tile (gate/up)
+};
+
+struct QkvEpi {
+  float* q_out;          // [q rows]
+  float* k_cache;        // layer base, row-major [max_seq][kv_dim]
+  float* v_cache;
+  const float2* rope_cs; // [max_pos][rope_dim/2] (cos, sin)
+  const DevState* state;
+  uint32_t head_dim, rope_dim, kv_dim;
+};
+
+hipError_t gemv_store(const GemvLaunch& L, float* y, hipStream_t st);
+hipError_t gemv_residual(const GemvLaunch& L, float* hidden, hipStream_t st);
+hipError_t gemv_qkv(const GemvLaunch& L, const QkvEpi& e, hipStream_t st);
+hipError_t gemv_swiglu(const GemvLaunch& L, float* mid, hipStream_t st);
+hipError_t gemv_logits(const GemvLaunch& L, float* logits, DevState* state, hipStream_t st);
+int gemv_supported(uint32_t type);
+
+// ---- small ops (kern_ops.hip) ----
+hipError_t launch_matmul_t_f32(const float* a, const float* b, float* c, uint64_t m, uint64_t n,
+                               uint64_t k, hipStream_t st);
+hipError_t launch_rms_norm_rows(float* x, const float* w, uint64_t n, uint64_t rows, float eps,
+                                hipStream_t st);
+hipError_t launch_swiglu(const float* g, const float* u, float* o, uint64_t n, hipStream_t st);
+hipError_t launch_add(float* o, const float* b, uint64_t n, hipStream_t st);
+hipError_t launch_softmax_rows(float* x, uint64_t rows, uint64_t cols, hipStream_t st);
+hipError_t launch_rope(float* x, uint64_t seq, uint64_t heads, uint64_t hd, uint64_t rope_dim,
+                       float base, uint64_t pos0, hipStream_t st);
+hipError_t launch_argmax(const float* x, uint64_t n, uint32_t* out, int* status, hipStream_t st);
+hipError_t launch_finalize(DevState* state, hipStream_t st);
+enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT };
+struct StateOp {
+  uint32_t kind;
+  uint32_t value;
+  uint32_t len;
+};
+hipError_t launch_state(DevState* state, const StateOp& op, hipStream_t st);
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t st);
+
+// ---- attention (kern_attn.hip) ----
+struct AttnArgs {
+  const float* q;        // [n_heads * head_dim]
+  const float* k_cache;  // layer base [max_seq][kv_dim]
+  const float* v_cache;
+  float* out;            // [n_heads * head_dim]
+  float* partial;        // [n_kv][max_chunks][group][head_dim + 2]
+  uint32_t* counters;    // [n_kv], zero between launches
+  const DevState* state;
+  uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk;
+};
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
+
+}  // namespace ifx
