@@ -183,7 +183,8 @@ def main():
         dom = max(range(8), key=lambda k: avg[k] * launches[k])
         # algorithmic bytes of one launch of the dominant kernel: its weight bytes
         # + the f32 input vector (+ the f32 norm weight when the norm is fused)
-        extra = {1: 2, 4: 2, 6: 2}.get(dom, 1) * spec.dim * 4 if dom != 5 else spec.ffn * 4
+        # (attention: the K/V rows it reads, reported by the library)
+        extra = 0 if dom == 2 else ({1: 2, 4: 2, 6: 2}.get(dom, 1) * spec.dim * 4 if dom != 5 else spec.ffn * 4)
         alg = wbytes[dom] + extra
         achieved = alg / (avg[dom] * 1e-3)
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,

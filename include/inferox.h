@@ -152,7 +152,8 @@ int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms);
  * 3 attn_output GEMV (+residual), 4 ffn gate/up GEMV (+RMSNorm, SwiGLU),
  * 5 ffn_down GEMV (+residual), 6 output head GEMV (+RMSNorm, argmax),
  * 7 finalize.  avg_ms: mean duration per launch; launches: per step;
- * bytes: stored weight bytes each launch streams.  len grows by n_steps. */
+ * bytes: stored weight bytes each launch streams (attention: the f32 K/V
+ * rows it reads).  len grows by n_steps. */
 int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
                         uint64_t* launches, uint64_t* bytes);
 

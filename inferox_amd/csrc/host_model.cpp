@@ -631,6 +631,7 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   if (token >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "token");
   IFX_TRY(check_vocab(m));
   if (s->len + n_steps > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
+  const uint64_t len0 = s->len;
   double sum[8] = {0};
   uint64_t cnt[8] = {0};
   IFX_TRY(state_op(s, STATE_DECODE, token, 0));
@@ -656,7 +657,9 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   const LayerDev& L0 = m->layers.empty() ? LayerDev{} : m->layers[0];
   bytes[0] = 0;
   bytes[1] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.q) + tensor_stream_bytes(L0.k) + tensor_stream_bytes(L0.v);
-  bytes[2] = 0;
+  // attention streams the f32 K and V rows it attends (average over the steps)
+  const uint64_t kvd = m->cfg.n_kv_heads * m->cfg.head_dim;
+  bytes[2] = 2 * (len0 + (n_steps + 1) / 2) * kvd * 4;
   bytes[3] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.o);
   bytes[4] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.gate) + tensor_stream_bytes(L0.up);
   bytes[5] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.down);

@@ -36,11 +36,13 @@ __device__ __forceinline__ float wave_max(float v) {
 __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   __shared__ float qs[kMaxGroup * kMaxHd];
   __shared__ float sc[kMaxGroup * kMaxChunk];
+  __shared__ float red[kThreads * 4 * kMaxGroup];  // phase-3 partials [pos group][g][HD]: npg*HD <= 1024
   __shared__ float mstat[kMaxGroup], lstat[kMaxGroup];
   __shared__ int is_last;
 
   const uint32_t c = blockIdx.x, hk = blockIdx.y;
   const uint32_t G = a.n_heads / a.n_kv_heads, HD = a.head_dim, kvd = a.n_kv_heads * HD;
+  const uint32_t nc4 = HD / 4;  // float4 chunks per head row
   const uint32_t lo = a.state->attn_lo;
   const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
   const uint32_t nrows = hi > lo ? hi - lo : 0;
@@ -53,25 +55,47 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   for (uint32_t i = tid; i < G * HD; i += kThreads) qs[i] = a.q[(hk * G) * HD + i];
   __syncthreads();
 
-  // scores (src/model/forward.rs:388-397)
-  const float rs = sqrtf((float)HD);
-  for (uint32_t item = tid; item < G * n; item += kThreads) {
-    const uint32_t t = item / G, g = item % G;
-    const float4* k4 = (const float4*)(a.k_cache + (uint64_t)(t0 + t) * kvd + hk * HD);
-    const float4* q4 = (const float4*)(qs + g * HD);
-    float s0 = 0.f, s1 = 0.f;
-    for (uint32_t d = 0; d < HD / 4; d++) {
-      const float4 kv = k4[d], qv = q4[d];
-      s0 = fmaf(qv.x, kv.x, s0);
-      s1 = fmaf(qv.y, kv.y, s1);
-      s0 = fmaf(qv.z, kv.z, s0);
-      s1 = fmaf(qv.w, kv.w, s1);
+  // ---- scores (src/model/forward.rs:388-397): 4 threads per cache row, each on
+  // every 4th float4 of the row; all K loads of a thread issued together.
+  {
+    const uint32_t p = tid >> 2, part = tid & 3;
+    float4 kr[16];
+    const float4* k4 = (const float4*)(a.k_cache + (uint64_t)(t0 + p) * kvd + hk * HD);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t ch = part + 4 * i;
+      if (p < n && ch < nc4) kr[i] = k4[ch];
     }
-    sc[g * kMaxChunk + t] = (s0 + s1) / rs;
+    float s[kMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; g++) s[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t ch = part + 4 * i;
+      if (p < n && ch < nc4) {
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; g++) {
+          if (g < (int)G) {
+            const float4 qv = *(const float4*)(qs + g * HD + 4 * ch);
+            s[g] = fmaf(qv.x, kr[i].x, s[g]);
+            s[g] = fmaf(qv.y, kr[i].y, s[g]);
+            s[g] = fmaf(qv.z, kr[i].z, s[g]);
+            s[g] = fmaf(qv.w, kr[i].w, s[g]);
+          }
+        }
+      }
+    }
+    const float rs = sqrtf((float)HD);
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; g++) {
+      s[g] += __shfl_xor(s[g], 1, 64);
+      s[g] += __shfl_xor(s[g], 2, 64);
+      if (g < (int)G && part == 0 && p < n) sc[g * kMaxChunk + p] = s[g] / rs;
+    }
   }
   __syncthreads();
 
-  // chunk-local softmax statistics (softmax_rows, src/ops.rs:223-239)
+  // ---- chunk-local softmax statistics (softmax_rows, src/ops.rs:223-239) ----
   for (uint32_t g = wave; g < G; g += kThreads / 64) {
     const float v = lane < (int)n ? sc[g * kMaxChunk + lane] : -INFINITY;
     const float m = wave_max(v);
@@ -82,28 +106,58 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   }
   __syncthreads();
 
-  // unnormalised o = sum_t e_t v_t (src/model/forward.rs:401-409)
+  // ---- o = sum_t e_t v_t (src/model/forward.rs:401-409): thread = (float4
+  // column chunk, position group); its V loads are issued together, then the
+  // position groups are summed through LDS.
+  const uint32_t npg = kThreads / nc4;
+  {
+    const uint32_t ch = tid % nc4, pg = tid / nc4;
+    float4 vr[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t p = pg + npg * i;
+      if (pg < npg && p < n) vr[i] = *((const float4*)(a.v_cache + (uint64_t)(t0 + p) * kvd + hk * HD) + ch);
+    }
+    float4 o[kMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; g++) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t p = pg + npg * i;
+      if (pg < npg && p < n) {
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; g++) {
+          if (g < (int)G) {
+            const float e = sc[g * kMaxChunk + p];
+            o[g].x = fmaf(e, vr[i].x, o[g].x);
+            o[g].y = fmaf(e, vr[i].y, o[g].y);
+            o[g].z = fmaf(e, vr[i].z, o[g].z);
+            o[g].w = fmaf(e, vr[i].w, o[g].w);
+          }
+        }
+      }
+    }
+    if (pg < npg) {
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; g++)
+        if (g < (int)G) *(float4*)(red + ((size_t)pg * G + g) * HD + 4 * ch) = o[g];
+    }
+  }
+  __syncthreads();
   const uint32_t pstride = HD + 2;
   float* part = a.partial + ((uint64_t)hk * a.max_chunks + c) * G * pstride;
   for (uint32_t item = tid; item < G * HD; item += kThreads) {
     const uint32_t g = item / HD, d = item % HD;
-    const float* vcol = a.v_cache + (uint64_t)t0 * kvd + hk * HD + d;
-    const float* e = sc + g * kMaxChunk;
-    float o0 = 0.f, o1 = 0.f;
-    uint32_t t = 0;
-    for (; t + 1 < n; t += 2) {
-      o0 = fmaf(e[t], vcol[(uint64_t)t * kvd], o0);
-      o1 = fmaf(e[t + 1], vcol[(uint64_t)(t + 1) * kvd], o1);
-    }
-    if (t < n) o0 = fmaf(e[t], vcol[(uint64_t)t * kvd], o0);
-    part[g * pstride + d] = o0 + o1;
+    float acc = 0.f;
+    for (uint32_t pg = 0; pg < npg; pg++) acc += red[((size_t)pg * G + g) * HD + d];
+    part[g * pstride + d] = acc;
   }
   if (tid < (int)G) {
     part[tid * pstride + HD] = mstat[tid];
     part[tid * pstride + HD + 1] = lstat[tid];
   }
 
-  // merge: the last workgroup of this kv head combines all chunks
+  // ---- merge: the last workgroup of this kv head combines all chunks ----
   __threadfence();
   __syncthreads();
   if (tid == 0) {
@@ -144,7 +198,8 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
 
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
   if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > kMaxGroup ||
-      a.head_dim > kMaxHd || a.head_dim % 4 || a.chunk == 0 || a.chunk > kMaxChunk)
+      a.head_dim > kMaxHd || a.head_dim % 4 || a.chunk == 0 || a.chunk > kMaxChunk ||
+      kThreads / (a.head_dim / 4) * 16 < a.chunk)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attn_decode, dim3(a.max_chunks, a.n_kv_heads), dim3(kThreads), 0, st, a);
   return hipGetLastError();

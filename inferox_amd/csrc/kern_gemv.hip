@@ -33,6 +33,7 @@ struct KArgs {
   uint32_t vbegin[4];  // first virtual row of each segment (padded to kR)
   int nseg;
   int paired;
+  int generic;  // rows are not whole 32-element groups (F32/F16 only)
   uint32_t cols, groups, ntiles;
   const float* x;
   const float* norm_w;
@@ -40,6 +41,13 @@ struct KArgs {
 };
 
 __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xffu); }
+// byte b of v as a signed int8, to f32 (v_bfe_i32 + v_cvt_f32_i32)
+__device__ __forceinline__ float sbyte(int v, int b) { return (float)((v << (24 - 8 * b)) >> 24); }
+
+// x lives in LDS with each 32-element group padded to 36 floats, so lanes
+// reading consecutive groups (a 144-byte stride) hit distinct banks.
+constexpr int kGroupStride = 36;
+__device__ __forceinline__ uint32_t xpad(uint32_t i) { return (i >> 5) * kGroupStride + (i & 31); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -138,10 +146,10 @@ __device__ __forceinline__ float dot_q80(const uint8_t* qs, uint32_t dbits, cons
   for (int w = 0; w < 8; w++) {
     const float4 xa = xv[w];
     const int v = (int)qw[w];
-    s0 = fmaf((float)__builtin_amdgcn_sbfe(v, 0, 8), xa.x, s0);
-    s1 = fmaf((float)__builtin_amdgcn_sbfe(v, 8, 8), xa.y, s1);
-    s0 = fmaf((float)__builtin_amdgcn_sbfe(v, 16, 8), xa.z, s0);
-    s1 = fmaf((float)(v >> 24), xa.w, s1);
+    s0 = fmaf(sbyte(v, 0), xa.x, s0);
+    s1 = fmaf(sbyte(v, 1), xa.y, s1);
+    s0 = fmaf(sbyte(v, 2), xa.z, s0);
+    s1 = fmaf(sbyte(v, 3), xa.w, s1);
   }
   return h2f(dbits) * (s0 + s1);
 }
@@ -182,10 +190,10 @@ __device__ __forceinline__ float dot_q8k(const uint8_t* blk, uint32_t dd, int su
     for (int w = 0; w < 2; w++) {
       const int v = (int)qw[2 * s + w];
       const float4 x4 = xv[2 * s + w];
-      a = fmaf((float)__builtin_amdgcn_sbfe(v, 0, 8), x4.x, a);
-      a = fmaf((float)__builtin_amdgcn_sbfe(v, 8, 8), x4.y, a);
-      a = fmaf((float)__builtin_amdgcn_sbfe(v, 16, 8), x4.z, a);
-      a = fmaf((float)(v >> 24), x4.w, a);
+      a = fmaf(sbyte(v, 0), x4.x, a);
+      a = fmaf(sbyte(v, 1), x4.y, a);
+      a = fmaf(sbyte(v, 2), x4.z, a);
+      a = fmaf(sbyte(v, 3), x4.w, a);
     }
     tot = fmaf(d * cvtb(scw, s), a, tot);
   }
@@ -231,7 +239,7 @@ __device__ __forceinline__ void tile_dot(const GemvSeg* segs, const int* segof, 
                                          const float* xl, const float* xs, uint32_t groups,
                                          uint32_t cols, int lane, float* acc) {
   for (uint32_t g = lane; g < groups; g += 64) {
-    const float4* xv4 = (const float4*)(xl + 32 * g);
+    const float4* xv4 = (const float4*)(xl + kGroupStride * g);
     float4 xv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) xv[i] = xv4[i];
@@ -264,6 +272,24 @@ __device__ __forceinline__ void tile_dot(const GemvSeg* segs, const int* segof, 
       }
       acc[r] += v;
     }
+  }
+}
+
+// Any row length (F32/F16 rows that are not whole 32-element groups): lanes
+// stride over the elements of each row.
+__device__ __forceinline__ void tile_dot_generic(const GemvSeg* segs, const int* segof, const int* rows,
+                                                 const float* xl, uint32_t cols, int lane, float* acc) {
+#pragma unroll
+  for (int r = 0; r < kR; r++) {
+    if (rows[r] < 0) continue;
+    const GemvSeg& s = segs[segof[r]];
+    const uint64_t base = (uint64_t)rows[r] * cols;
+    float a = 0.f;
+    for (uint32_t l = lane; l < cols; l += 64) {
+      const float w = s.type == T_F32 ? ((const float*)s.body)[base + l] : h2f(((const uint16_t*)s.body)[base + l]);
+      a = fmaf(w, xl[xpad(l)], a);
+    }
+    acc[r] += a;
   }
 }
 
@@ -365,20 +391,17 @@ struct EpiLogits {
 template <class Epi>
 __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
   extern __shared__ float lds[];
-  float* xl = lds;                  // [cols]
-  float* xs = lds + a.cols;         // [cols/16]
+  float* xl = lds;                                        // [groups][36]
+  float* xs = lds + (size_t)a.groups * kGroupStride;      // [cols/16]
   __shared__ float red[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // ---- prologue: x (optionally RMS-normalised) into LDS ----
   float ss = 0.f;
-  for (uint32_t i = 4 * tid; i < a.cols; i += 4 * kThreads) {
-    const float4 v = *(const float4*)(a.x + i);
-    *(float4*)(xl + i) = v;
-    ss = fmaf(v.x, v.x, ss);
-    ss = fmaf(v.y, v.y, ss);
-    ss = fmaf(v.z, v.z, ss);
-    ss = fmaf(v.w, v.w, ss);
+  for (uint32_t i = tid; i < a.cols; i += kThreads) {
+    const float v = a.x[i];
+    xl[xpad(i)] = v;
+    ss = fmaf(v, v, ss);
   }
   if (a.norm_w) {
     ss = wave_sum(ss);
@@ -389,16 +412,18 @@ __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
     for (int w = 0; w < kWaves; w++) tot += red[w];
     // rms_norm (src/ops.rs:162-167): scale = 1/sqrt(mean + eps); x = (x*scale)*w
     const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
-    for (uint32_t i = tid; i < a.cols; i += kThreads) xl[i] = (xl[i] * scale) * a.norm_w[i];
+    for (uint32_t i = tid; i < a.cols; i += kThreads) xl[xpad(i)] = (xl[xpad(i)] * scale) * a.norm_w[i];
   }
   __syncthreads();
-  for (uint32_t j = tid; j < a.cols / 16; j += kThreads) {
-    const float4* p = (const float4*)(xl + 16 * j);
-    const float4 u0 = p[0], u1 = p[1], u2 = p[2], u3 = p[3];
-    xs[j] = ((u0.x + u0.y) + (u0.z + u0.w)) + ((u1.x + u1.y) + (u1.z + u1.w)) +
-            (((u2.x + u2.y) + (u2.z + u2.w)) + ((u3.x + u3.y) + (u3.z + u3.w)));
+  if (!a.generic) {
+    for (uint32_t j = tid; j < a.cols / 16; j += kThreads) {
+      const float4* p = (const float4*)(xl + (j >> 1) * kGroupStride + 16 * (j & 1));
+      const float4 u0 = p[0], u1 = p[1], u2 = p[2], u3 = p[3];
+      xs[j] = ((u0.x + u0.y) + (u0.z + u0.w)) + ((u1.x + u1.y) + (u1.z + u1.w)) +
+              (((u2.x + u2.y) + (u2.z + u2.w)) + ((u3.x + u3.y) + (u3.z + u3.w)));
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   // ---- row tiles ----
   typename Epi::Wave ws;
@@ -426,7 +451,8 @@ __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
     float acc[kR];
 #pragma unroll
     for (int r = 0; r < kR; r++) acc[r] = 0.f;
-    switch (a.seg[segi].type) {
+    if (a.generic) tile_dot_generic(a.seg, segof, rows, xl, a.cols, lane, acc);
+    else switch (a.seg[segi].type) {
       case T_Q4K: tile_dot<T_Q4K>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
       case T_Q6K: tile_dot<T_Q6K>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
       case T_Q8_0: tile_dot<T_Q8_0>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
@@ -443,12 +469,13 @@ __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
 }
 
 bool build_args(const GemvLaunch& L, KArgs* a) {
-  if (L.nseg < 1 || L.nseg > 3 || L.cols == 0 || L.cols % 32) return false;
+  if (L.nseg < 1 || L.nseg > 3 || L.cols == 0) return false;
   *a = KArgs{};
   a->nseg = L.nseg;
   a->paired = L.paired ? 1 : 0;
   a->cols = L.cols;
-  a->groups = L.cols / 32;
+  a->generic = L.cols % 32 ? 1 : 0;
+  a->groups = (L.cols + 31) / 32;
   a->x = L.x;
   a->norm_w = L.norm_w;
   a->eps = L.eps;
@@ -459,6 +486,7 @@ bool build_args(const GemvLaunch& L, KArgs* a) {
     v += (L.seg[s].rows + kR - 1) / kR * kR;
     if ((L.seg[s].type == T_Q4K || L.seg[s].type == T_Q6K || L.seg[s].type == T_Q8K) && L.cols % 256)
       return false;
+    if (a->generic && L.seg[s].type != T_F32 && L.seg[s].type != T_F16) return false;
   }
   a->vbegin[L.nseg] = v;
   if (L.paired) {
@@ -474,7 +502,7 @@ template <class Epi>
 hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   KArgs a;
   if (!build_args(L, &a)) return hipErrorInvalidValue;
-  const size_t lds = (size_t)a.cols * 4 + (size_t)(a.cols / 16) * 4;
+  const size_t lds = (size_t)a.groups * kGroupStride * 4 + (size_t)(a.cols / 16) * 4;
   if (lds > 150 * 1024) return hipErrorInvalidValue;
   uint32_t blocks = (a.ntiles + kWaves - 1) / kWaves;
   if (blocks > 1024) blocks = 1024;
