@@ -8,6 +8,7 @@
 // scratch of DecodeBuffers, a HIP stream and one captured decode step that is
 // replayed for every token (positions live in device memory).
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -238,6 +239,13 @@ uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->
 int run_step(ifx_session* s) {
   if (!s->graph_tried) {
     s->graph_tried = true;
+    // IFX_NO_GRAPH=1: launch the step's kernels directly (used under profilers
+    // that do not follow captured graphs)
+    const char* ng = getenv("IFX_NO_GRAPH");
+    if (ng && ng[0] == '1') {
+      s->steps++;
+      return enqueue_step(s);
+    }
     hipGraph_t g = nullptr;
     if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeRelaxed) == hipSuccess) {
       int rc = enqueue_step(s);
@@ -421,7 +429,7 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   A((void**)&s->attn, D * 4);
   A((void**)&s->mid, F * 4);
   A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
-  A((void**)&s->partial, c.n_kv_heads * s->max_chunks * G * (c.head_dim + 2) * 4);
+  A((void**)&s->partial, (uint64_t)c.n_kv_heads * s->max_chunks * attn_partial_floats(G, c.head_dim) * 4);
   A((void**)&s->counters, c.n_kv_heads * 4);
   A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
   A((void**)&s->state, sizeof(DevState));

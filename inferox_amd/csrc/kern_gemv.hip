@@ -6,46 +6,62 @@
 // quantized form and decoded in registers.
 //
 // Work decomposition
-//   * A workgroup (4 wave64) first stages x in LDS, optionally applying
-//     RMSNorm (ops::rms_norm, src/ops.rs:155-168) so the norm costs no launch,
-//     and precomputes 16-element partial sums of x (the min/offset terms of the
-//     K-quants factor out as scale * sum(x)).
-//   * A wave owns a tile of R = 4 rows and sweeps K with each lane on one
-//     32-element group per step (lane = group within a 64-group step), so each
-//     lane reads contiguous 16-byte pieces of the packed blocks and the x group
-//     read from LDS is reused for all R rows.
-//   * The R row sums are reduced across the wave; the epilogue fuses RoPE + KV
+//   * Persistent workgroups of 8 wave64, two per CU (16 waves per CU, at most
+//     128 VGPRs each).  Each wave issues the loads of its first unit, then the
+//     workgroup stages x in LDS, optionally applying RMSNorm (ops::rms_norm,
+//     src/ops.rs:155-168) so the norm costs no launch, and precomputes
+//     16-element partial sums of x (the min/offset terms of the K-quants factor
+//     out as scale * sum(x)).
+//   * A wave owns tiles of R = 4 rows.  A "unit" is one 32-element group of
+//     each of the R rows per lane (lane l takes group l + 64 i), so each lane
+//     reads contiguous 16-byte pieces of the packed blocks and one x group read
+//     from LDS serves R rows.  The loads of the next unit are issued as soon as
+//     the current one is decoded; the other waves of the CU cover the latency.
+//     Tile and row bookkeeping is wave-uniform (scalar registers).
+//   * Row sums are reduced across the wave; the epilogue fuses RoPE + KV
 //     append (QKV), SwiGLU (gate/up), the residual add (O, down) or the logits
 //     store + greedy argmax (output head).
 // Compiled with -ffp-contract=off: only the explicit fmaf below are fused.
+#include <algorithm>
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace ifx {
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kBlocksPerCu = 2;  // 16 waves per CU
+constexpr int kWavesPerSimd = kBlocksPerCu * kWaves / 4;  // 4: at most 128 VGPRs per lane
 constexpr int kThreads = kWaves * 64;
 constexpr int kR = 4;
 
 struct KArgs {
   GemvSeg seg[3];
-  uint32_t vbegin[4];  // first virtual row of each segment (padded to kR)
-  int nseg;
-  int paired;
-  int generic;  // rows are not whole 32-element groups (F32/F16 only)
-  uint32_t cols, groups, ntiles;
+  uint32_t ntiles[3];  // tiles per logical segment (paired: one logical segment)
+  uint32_t rot[3];     // first-wave rotation per segment (balances small segments)
+  uint32_t use_b;      // bit s: segment s decodes with the kernel's second type
+  int nseg;            // logical segments
+  uint32_t cols, groups;
   const float* x;
   const float* norm_w;
   float eps;
 };
 
 __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xffu); }
+// Hides a masked word from the combiner so that cvtb(w, k) selects
+// v_cvt_f32_ubyte<k> (one instruction) instead of a bit-field extract of the
+// unmasked word followed by a convert.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
 // byte b of v as a signed int8, to f32 (v_bfe_i32 + v_cvt_f32_i32)
 __device__ __forceinline__ float sbyte(int v, int b) { return (float)((v << (24 - 8 * b)) >> 24); }
 
 // x lives in LDS with each 32-element group padded to 36 floats, so lanes
-// reading consecutive groups (a 144-byte stride) hit distinct banks.
+// reading consecutive groups (a 144-byte stride) spread over the banks.
 constexpr int kGroupStride = 36;
 __device__ __forceinline__ uint32_t xpad(uint32_t i) { return (i >> 5) * kGroupStride + (i & 31); }
 
@@ -55,285 +71,392 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// ---- per-type dot of one 32-element group of one row with x (xv: 8 float4) ----
+template <class T>
+__device__ __forceinline__ T ldg(const void* p) { return *(const T*)p; }
+
+// Row r of tile `tile` of logical segment s, wave-uniform.  Paired launches
+// (gate/up) put rows 2t, 2t+1 of segment 0 in r = 0, 1 and the same rows of
+// segment 1 in r = 2, 3.
+struct RowRef {
+  const uint8_t* body;
+  const uint8_t* scal;
+  uint64_t row;
+  bool ok;  // false for padding rows past the end of the segment
+};
+
+template <bool PAIRED>
+__device__ __forceinline__ RowRef row_of(const KArgs& a, int s, uint32_t tile, int r) {
+  // padding rows read the last real row (loads stay unconditional) and are
+  // skipped by the decode and the epilogue
+  if (PAIRED) {
+    const GemvSeg& sg = a.seg[r < kR / 2 ? 0 : 1];
+    const uint32_t row = tile * (kR / 2) + (r % (kR / 2));
+    return RowRef{sg.body, sg.scal, row < sg.rows ? row : sg.rows - 1, row < sg.rows};
+  }
+  const GemvSeg& sg = a.seg[s];
+  const uint32_t row = tile * kR + r;
+  return RowRef{sg.body, sg.scal, row < sg.rows ? row : sg.rows - 1, row < sg.rows};
+}
+
+// ---------------------------------------------------------------------------
+// Per-type fragments: the raw bytes of one unit (group g of the kR rows of a
+// tile) held in registers, and the decode + dot of that group with x.
+// ---------------------------------------------------------------------------
 
 // Q4_K (src/gguf/dequant.rs:133-161): element 32g+l is nibble (l&1) of
 // qs[16g + l/2];  sum_l ((d*sc)*q_l - dmin*mn) x_l = (d*sc)*S - (dmin*mn)*sum(x).
-__device__ __forceinline__ float dot_q4k(const uint8_t* blk, int sub, const float4* xv, float xsum) {
-  const uint4 h = *(const uint4*)blk;
-  const uint4 q = *(const uint4*)(blk + 16 + 16 * sub);
-  const int j = sub & 3;
-  uint32_t sc, mn;
-  if (sub < 4) {
-    sc = (h.y >> (8 * j)) & 63u;
-    mn = (h.z >> (8 * j)) & 63u;
-  } else {
-    sc = ((h.w >> (8 * j)) & 15u) | (((h.y >> (8 * j + 6)) & 3u) << 4);
-    mn = ((h.w >> (8 * j + 4)) & 15u) | (((h.z >> (8 * j + 6)) & 3u) << 4);
-  }
-  const float d = h2f(h.x), dmin = h2f(h.x >> 16);
-  float s0 = 0.f, s1 = 0.f;
-  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+struct FragQ4K {
+  uint4 h[kR], q[kR];
+  template <bool P>
+  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
 #pragma unroll
-  for (int w = 0; w < 4; w++) {
-    const uint32_t lo = qw[w] & 0x0F0F0F0Fu, hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
-    const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-    s0 = fmaf(cvtb(lo, 0), xa.x, s0);
-    s1 = fmaf(cvtb(hi, 0), xa.y, s1);
-    s0 = fmaf(cvtb(lo, 1), xa.z, s0);
-    s1 = fmaf(cvtb(hi, 1), xa.w, s1);
-    s0 = fmaf(cvtb(lo, 2), xb.x, s0);
-    s1 = fmaf(cvtb(hi, 2), xb.y, s1);
-    s0 = fmaf(cvtb(lo, 3), xb.z, s0);
-    s1 = fmaf(cvtb(hi, 3), xb.w, s1);
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      // wave-uniform row base + 32-bit lane offset (scalar-base loads)
+      const uint8_t* row = rr.body + rr.row * ((a.groups / 8) * 144);
+      const uint32_t off = (g / 8) * 144;
+      h[r] = ldg<uint4>(row + off);
+      q[r] = ldg<uint4>(row + off + 16 + 16 * (g & 7));
+    }
   }
-  const float A = d * (float)sc, M = dmin * (float)mn;
-  return fmaf(A, s0 + s1, -(M * xsum));
-}
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float xsa, float xsb,
+                      float* acc) const {
+    const int sub = g & 7, j = sub & 3;
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      if (!row_of<P>(a, s, tile, r).ok) continue;
+      uint32_t sc, mn;
+      if (sub < 4) {
+        sc = (h[r].y >> (8 * j)) & 63u;
+        mn = (h[r].z >> (8 * j)) & 63u;
+      } else {
+        sc = ((h[r].w >> (8 * j)) & 15u) | (((h[r].y >> (8 * j + 6)) & 3u) << 4);
+        mn = ((h[r].w >> (8 * j + 4)) & 15u) | (((h[r].z >> (8 * j + 6)) & 3u) << 4);
+      }
+      const float d = h2f(h[r].x), dmin = h2f(h[r].x >> 16);
+      float s0 = 0.f, s1 = 0.f;
+      const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        // high nibbles stay in place (16 q): s1 is scaled by 1/16 below, exactly
+        const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);
+        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+        s0 = fmaf(cvtb(lo, 0), xa.x, s0);
+        s1 = fmaf(cvtb(hi, 0), xa.y, s1);
+        s0 = fmaf(cvtb(lo, 1), xa.z, s0);
+        s1 = fmaf(cvtb(hi, 1), xa.w, s1);
+        s0 = fmaf(cvtb(lo, 2), xb.x, s0);
+        s1 = fmaf(cvtb(hi, 2), xb.y, s1);
+        s0 = fmaf(cvtb(lo, 3), xb.z, s0);
+        s1 = fmaf(cvtb(hi, 3), xb.w, s1);
+      }
+      const float A = d * (float)sc, M = dmin * (float)mn;
+      acc[r] = fmaf(A, fmaf(s1, 0.0625f, s0), fmaf(-M, xsa + xsb, acc[r]));
+    }
+  }
+};
 
 // Q6_K in the device layout (ql | re-ordered qh | u8 sc; d separate):
 // q = lo | hi<<4, y = (d*sc)*(q-32)  (src/gguf/dequant.rs:182-197).
-__device__ __forceinline__ float dot_q6k(const uint8_t* blk, uint32_t dbits, int h, const float4* xv,
-                                         float xs_a, float xs_b) {
-  const uint4 ql = *(const uint4*)(blk + 16 * h);
-  const uint2 qh = *(const uint2*)(blk + 128 + 8 * h);
-  const uint32_t scw = *(const uint16_t*)(blk + 192 + 2 * h);
-  const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
-  // half a: elements 0..15 (ql.x: 0-7, ql.y: 8-15; high bits in qh.x)
-  const uint32_t e0 = (ql.x & m4) | (qh.x & m2), o0 = ((ql.x >> 4) & m4) | ((qh.x >> 2) & m2);
-  const uint32_t e1 = (ql.y & m4) | ((qh.x << 4) & m2), o1 = ((ql.y >> 4) & m4) | ((qh.x << 2) & m2);
-  // half b: elements 16..31 (ql.z, ql.w; qh.y)
-  const uint32_t e2 = (ql.z & m4) | (qh.y & m2), o2 = ((ql.z >> 4) & m4) | ((qh.y >> 2) & m2);
-  const uint32_t e3 = (ql.w & m4) | ((qh.y << 4) & m2), o3 = ((ql.w >> 4) & m4) | ((qh.y << 2) & m2);
-  float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-  const uint32_t ev[4] = {e0, e1, e2, e3}, ov[4] = {o0, o1, o2, o3};
-#pragma unroll
-  for (int w = 0; w < 2; w++) {
-    const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-    a0 = fmaf(cvtb(ev[w], 0), xa.x, a0);
-    a1 = fmaf(cvtb(ov[w], 0), xa.y, a1);
-    a0 = fmaf(cvtb(ev[w], 1), xa.z, a0);
-    a1 = fmaf(cvtb(ov[w], 1), xa.w, a1);
-    a0 = fmaf(cvtb(ev[w], 2), xb.x, a0);
-    a1 = fmaf(cvtb(ov[w], 2), xb.y, a1);
-    a0 = fmaf(cvtb(ev[w], 3), xb.z, a0);
-    a1 = fmaf(cvtb(ov[w], 3), xb.w, a1);
-  }
-#pragma unroll
-  for (int w = 2; w < 4; w++) {
-    const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-    b0 = fmaf(cvtb(ev[w], 0), xa.x, b0);
-    b1 = fmaf(cvtb(ov[w], 0), xa.y, b1);
-    b0 = fmaf(cvtb(ev[w], 1), xa.z, b0);
-    b1 = fmaf(cvtb(ov[w], 1), xa.w, b1);
-    b0 = fmaf(cvtb(ev[w], 2), xb.x, b0);
-    b1 = fmaf(cvtb(ov[w], 2), xb.y, b1);
-    b0 = fmaf(cvtb(ev[w], 3), xb.z, b0);
-    b1 = fmaf(cvtb(ov[w], 3), xb.w, b1);
-  }
-  const float d = h2f(dbits);
-  const float sa = (float)(scw & 0xffu), sb = (float)(scw >> 8);
-  const float ta = fmaf(-32.f, xs_a, a0 + a1), tb = fmaf(-32.f, xs_b, b0 + b1);
-  return d * fmaf(sa, ta, sb * tb);
-}
-
-// Q8_0 (device layout qs[32] | d): y = f32(i8 q) * delta (src/gguf/dequant.rs:101-109).
-__device__ __forceinline__ float dot_q80(const uint8_t* qs, uint32_t dbits, const float4* xv) {
-  const uint4 qa = *(const uint4*)qs, qb = *(const uint4*)(qs + 16);
-  const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int w = 0; w < 8; w++) {
-    const float4 xa = xv[w];
-    const int v = (int)qw[w];
-    s0 = fmaf(sbyte(v, 0), xa.x, s0);
-    s1 = fmaf(sbyte(v, 1), xa.y, s1);
-    s0 = fmaf(sbyte(v, 2), xa.z, s0);
-    s1 = fmaf(sbyte(v, 3), xa.w, s1);
-  }
-  return h2f(dbits) * (s0 + s1);
-}
-
-// Q4_0 (device layout qs[16] | d): low nibble -> element j, high -> j+16, value q-8.
-__device__ __forceinline__ float dot_q40(const uint8_t* qs, uint32_t dbits, const float4* xv, float xsum) {
-  const uint4 q = *(const uint4*)qs;
-  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; w++) {
-    const uint32_t lo = qw[w] & 0x0F0F0F0Fu, hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
-    const float4 xa = xv[w], xb = xv[4 + w];
-    s0 = fmaf(cvtb(lo, 0), xa.x, s0);
-    s0 = fmaf(cvtb(lo, 1), xa.y, s0);
-    s0 = fmaf(cvtb(lo, 2), xa.z, s0);
-    s0 = fmaf(cvtb(lo, 3), xa.w, s0);
-    s1 = fmaf(cvtb(hi, 0), xb.x, s1);
-    s1 = fmaf(cvtb(hi, 1), xb.y, s1);
-    s1 = fmaf(cvtb(hi, 2), xb.z, s1);
-    s1 = fmaf(cvtb(hi, 3), xb.w, s1);
-  }
-  return h2f(dbits) * fmaf(-8.f, xsum, s0 + s1);
-}
-
-// Q8_K (device layout sc[32] | qs[256]; {d, dmin}): y = ((d*sc)*q) - dmin.
-__device__ __forceinline__ float dot_q8k(const uint8_t* blk, uint32_t dd, int sub, const float4* xv,
-                                         float xsum) {
-  const uint32_t scw = *(const uint32_t*)(blk + 4 * sub);
-  const uint4 qa = *(const uint4*)(blk + 32 + 32 * sub), qb = *(const uint4*)(blk + 48 + 32 * sub);
-  const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-  const float d = h2f(dd), dmin = h2f(dd >> 16);
-  float tot = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; s++) {  // sub-blocks of 8 elements share one scale byte
-    float a = 0.f;
-#pragma unroll
-    for (int w = 0; w < 2; w++) {
-      const int v = (int)qw[2 * s + w];
-      const float4 x4 = xv[2 * s + w];
-      a = fmaf(sbyte(v, 0), x4.x, a);
-      a = fmaf(sbyte(v, 1), x4.y, a);
-      a = fmaf(sbyte(v, 2), x4.z, a);
-      a = fmaf(sbyte(v, 3), x4.w, a);
-    }
-    tot = fmaf(d * cvtb(scw, s), a, tot);
-  }
-  return fmaf(-dmin, xsum, tot);
-}
-
-__device__ __forceinline__ float dot_f32(const float* w, const float4* xv) {
-  const float4* w4 = (const float4*)w;
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float4 a = w4[i], x = xv[i];
-    s0 = fmaf(a.x, x.x, s0);
-    s1 = fmaf(a.y, x.y, s1);
-    s0 = fmaf(a.z, x.z, s0);
-    s1 = fmaf(a.w, x.w, s1);
-  }
-  return s0 + s1;
-}
-
-__device__ __forceinline__ float dot_f16(const uint16_t* w, const float4* xv) {
-  const uint4* w4 = (const uint4*)w;
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint4 a = w4[i];
-    const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const float4 x = xv[2 * i + k];
-      s0 = fmaf(h2f(aw[2 * k]), x.x, s0);
-      s1 = fmaf(h2f(aw[2 * k] >> 16), x.y, s1);
-      s0 = fmaf(h2f(aw[2 * k + 1]), x.z, s0);
-      s1 = fmaf(h2f(aw[2 * k + 1] >> 16), x.w, s1);
-    }
-  }
-  return s0 + s1;
-}
-
-// Sweep all groups of a tile of kR rows (one segment type) for this lane.
-template <int TYPE>
-__device__ __forceinline__ void tile_dot(const GemvSeg* segs, const int* segof, const int* rows,
-                                         const float* xl, const float* xs, uint32_t groups,
-                                         uint32_t cols, int lane, float* acc) {
-  for (uint32_t g = lane; g < groups; g += 64) {
-    const float4* xv4 = (const float4*)(xl + kGroupStride * g);
-    float4 xv[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) xv[i] = xv4[i];
-    const float xsa = xs[2 * g], xsb = xs[2 * g + 1];
+struct FragQ6K {
+  uint4 ql[kR];
+  uint2 qh[kR];
+  uint32_t sd[kR];  // the group's two scale bytes (low 16 bits) | d bits (high 16)
+  template <bool P>
+  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
 #pragma unroll
     for (int r = 0; r < kR; r++) {
-      if (rows[r] < 0) continue;
-      const GemvSeg& s = segs[segof[r]];
-      const uint64_t row = (uint64_t)rows[r];
-      float v;
-      if (TYPE == T_Q4K) {
-        const uint64_t blk = row * (groups / 8) + g / 8;
-        v = dot_q4k(s.body + blk * 144, g & 7, xv, xsa + xsb);
-      } else if (TYPE == T_Q6K) {
-        const uint64_t blk = row * (groups / 8) + g / 8;
-        v = dot_q6k(s.body + blk * 208, ((const uint16_t*)s.scal)[blk], g & 7, xv, xsa, xsb);
-      } else if (TYPE == T_Q8_0) {
-        const uint64_t blk = row * groups + g;
-        v = dot_q80(s.body + blk * 32, ((const uint16_t*)s.scal)[blk], xv);
-      } else if (TYPE == T_Q4_0) {
-        const uint64_t blk = row * groups + g;
-        v = dot_q40(s.body + blk * 16, ((const uint16_t*)s.scal)[blk], xv, xsa + xsb);
-      } else if (TYPE == T_Q8K) {
-        const uint64_t blk = row * (groups / 8) + g / 8;
-        v = dot_q8k(s.body + blk * 288, ((const uint32_t*)s.scal)[blk], g & 7, xv, xsa + xsb);
-      } else if (TYPE == T_F32) {
-        v = dot_f32((const float*)s.body + row * cols + 32 * g, xv);
-      } else {
-        v = dot_f16((const uint16_t*)s.body + row * cols + 32 * g, xv);
-      }
-      acc[r] += v;
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      const uint32_t nb = a.groups / 8;
+      const uint8_t* row = rr.body + rr.row * (nb * 208);
+      const uint8_t* rowd = rr.scal + rr.row * (nb * 2);
+      const uint32_t off = (g / 8) * 208, h = g & 7;
+      ql[r] = ldg<uint4>(row + off + 16 * h);
+      qh[r] = ldg<uint2>(row + off + 128 + 8 * h);
+      sd[r] = (uint32_t)ldg<uint16_t>(row + off + 192 + 2 * h) | ((uint32_t)ldg<uint16_t>(rowd + (g / 8) * 2) << 16);
     }
   }
-}
-
-// Any row length (F32/F16 rows that are not whole 32-element groups): lanes
-// stride over the elements of each row.
-__device__ __forceinline__ void tile_dot_generic(const GemvSeg* segs, const int* segof, const int* rows,
-                                                 const float* xl, uint32_t cols, int lane, float* acc) {
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
+                      float* acc) const {
+    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
 #pragma unroll
-  for (int r = 0; r < kR; r++) {
-    if (rows[r] < 0) continue;
-    const GemvSeg& s = segs[segof[r]];
-    const uint64_t base = (uint64_t)rows[r] * cols;
-    float a = 0.f;
-    for (uint32_t l = lane; l < cols; l += 64) {
-      const float w = s.type == T_F32 ? ((const float*)s.body)[base + l] : h2f(((const uint16_t*)s.body)[base + l]);
-      a = fmaf(w, xl[xpad(l)], a);
+    for (int r = 0; r < kR; r++) {
+      if (!row_of<P>(a, s, tile, r).ok) continue;
+      const uint4 L = ql[r];
+      const uint2 H = qh[r];
+      // half a: elements 0..15 (L.x: 0-7, L.y: 8-15; high bits in H.x); half b: 16..31
+      const uint32_t ev[4] = {opaque((L.x & m4) | (H.x & m2)), opaque((L.y & m4) | ((H.x << 4) & m2)),
+                              opaque((L.z & m4) | (H.y & m2)), opaque((L.w & m4) | ((H.y << 4) & m2))};
+      const uint32_t ov[4] = {opaque(((L.x >> 4) & m4) | ((H.x >> 2) & m2)),
+                              opaque(((L.y >> 4) & m4) | ((H.x << 2) & m2)),
+                              opaque(((L.z >> 4) & m4) | ((H.y >> 2) & m2)),
+                              opaque(((L.w >> 4) & m4) | ((H.y << 2) & m2))};
+      float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 2; w++) {
+        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+        a0 = fmaf(cvtb(ev[w], 0), xa.x, a0);
+        a1 = fmaf(cvtb(ov[w], 0), xa.y, a1);
+        a0 = fmaf(cvtb(ev[w], 1), xa.z, a0);
+        a1 = fmaf(cvtb(ov[w], 1), xa.w, a1);
+        a0 = fmaf(cvtb(ev[w], 2), xb.x, a0);
+        a1 = fmaf(cvtb(ov[w], 2), xb.y, a1);
+        a0 = fmaf(cvtb(ev[w], 3), xb.z, a0);
+        a1 = fmaf(cvtb(ov[w], 3), xb.w, a1);
+      }
+#pragma unroll
+      for (int w = 2; w < 4; w++) {
+        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+        b0 = fmaf(cvtb(ev[w], 0), xa.x, b0);
+        b1 = fmaf(cvtb(ov[w], 0), xa.y, b1);
+        b0 = fmaf(cvtb(ev[w], 1), xa.z, b0);
+        b1 = fmaf(cvtb(ov[w], 1), xa.w, b1);
+        b0 = fmaf(cvtb(ev[w], 2), xb.x, b0);
+        b1 = fmaf(cvtb(ov[w], 2), xb.y, b1);
+        b0 = fmaf(cvtb(ev[w], 3), xb.z, b0);
+        b1 = fmaf(cvtb(ov[w], 3), xb.w, b1);
+      }
+      const float d = h2f(sd[r] >> 16);
+      const float sa = (float)(sd[r] & 0xffu), sb = (float)((sd[r] >> 8) & 0xffu);
+      const float ta = fmaf(-32.f, xsa, a0 + a1), tb = fmaf(-32.f, xsb, b0 + b1);
+      acc[r] = fmaf(d, fmaf(sa, ta, sb * tb), acc[r]);
     }
-    acc[r] += a;
   }
-}
+};
 
-// ---- epilogues ----
+// Q8_0 (device layout qs[32] | d): y = f32(i8 q) * delta (src/gguf/dequant.rs:101-109).
+struct FragQ80 {
+  uint4 qa[kR], qb[kR];
+  uint32_t d[kR];
+  template <bool P>
+  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      const uint8_t* row = rr.body + rr.row * (a.groups * 32);
+      qa[r] = ldg<uint4>(row + g * 32);
+      qb[r] = ldg<uint4>(row + g * 32 + 16);
+      d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
+    }
+  }
+  // q x = (u - 128) x with u = q ^ 0x80 unsigned: one convert per byte, the
+  // -128 sum(x) term from the staged group sums
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
+                      float* acc) const {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      if (!row_of<P>(a, s, tile, r).ok) continue;
+      const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        const float4 xa = xv[w];
+        const uint32_t u = opaque(qw[w] ^ 0x80808080u);
+        s0 = fmaf(cvtb(u, 0), xa.x, s0);
+        s1 = fmaf(cvtb(u, 1), xa.y, s1);
+        s0 = fmaf(cvtb(u, 2), xa.z, s0);
+        s1 = fmaf(cvtb(u, 3), xa.w, s1);
+      }
+      acc[r] = fmaf(h2f(d[r]), fmaf(-128.f, xsa + xsb, s0 + s1), acc[r]);
+    }
+  }
+};
+
+// Q4_0 (device layout qs[16] | d): low nibble -> element j, high -> j+16, value q-8.
+struct FragQ40 {
+  uint4 q[kR];
+  uint32_t d[kR];
+  template <bool P>
+  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      q[r] = ldg<uint4>(rr.body + rr.row * (a.groups * 16) + g * 16);
+      d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
+    }
+  }
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
+                      float* acc) const {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      if (!row_of<P>(a, s, tile, r).ok) continue;
+      const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);  // hi: 16 q
+        const float4 xa = xv[w], xb = xv[4 + w];
+        s0 = fmaf(cvtb(lo, 0), xa.x, s0);
+        s0 = fmaf(cvtb(lo, 1), xa.y, s0);
+        s0 = fmaf(cvtb(lo, 2), xa.z, s0);
+        s0 = fmaf(cvtb(lo, 3), xa.w, s0);
+        s1 = fmaf(cvtb(hi, 0), xb.x, s1);
+        s1 = fmaf(cvtb(hi, 1), xb.y, s1);
+        s1 = fmaf(cvtb(hi, 2), xb.z, s1);
+        s1 = fmaf(cvtb(hi, 3), xb.w, s1);
+      }
+      acc[r] = fmaf(h2f(d[r]), fmaf(-8.f, xsa + xsb, fmaf(s1, 0.0625f, s0)), acc[r]);
+    }
+  }
+};
+
+// Q8_K (device layout sc[32] | qs[256]; {d, dmin}): y = ((d*sc)*q) - dmin.
+struct FragQ8K {
+  uint4 qa[kR], qb[kR];
+  uint32_t sc[kR], dd[kR];
+  template <bool P>
+  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      const uint32_t nb = a.groups / 8, sub = g & 7;
+      const uint8_t* blk = rr.body + rr.row * (nb * 288) + (g / 8) * 288;
+      sc[r] = ldg<uint32_t>(blk + 4 * sub);
+      qa[r] = ldg<uint4>(blk + 32 + 32 * sub);
+      qb[r] = ldg<uint4>(blk + 48 + 32 * sub);
+      dd[r] = ldg<uint32_t>(rr.scal + rr.row * (nb * 4) + (g / 8) * 4);
+    }
+  }
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
+                      float* acc) const {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      if (!row_of<P>(a, s, tile, r).ok) continue;
+      const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+      const float d = h2f(dd[r]), dmin = h2f(dd[r] >> 16);
+      float tot = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {  // sub-blocks of 8 elements share one scale byte
+        float acc8 = 0.f;
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+          const int v = (int)qw[2 * k + w];
+          const float4 x4 = xv[2 * k + w];
+          acc8 = fmaf(sbyte(v, 0), x4.x, acc8);
+          acc8 = fmaf(sbyte(v, 1), x4.y, acc8);
+          acc8 = fmaf(sbyte(v, 2), x4.z, acc8);
+          acc8 = fmaf(sbyte(v, 3), x4.w, acc8);
+        }
+        tot = fmaf(d * cvtb(sc[r], k), acc8, tot);
+      }
+      acc[r] += fmaf(-dmin, xsa + xsb, tot);
+    }
+  }
+};
+
+// F32 / F16 rows of whole groups: read at use, no prefetch (toy models, tests).
+struct FragF32 {
+  template <bool P>
+  __device__ void load(const KArgs&, int, uint32_t, uint32_t) {}
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float, float,
+                      float* acc) const {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      if (!rr.ok) continue;
+      const float4* w4 = (const float4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 8;
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float4 w = w4[i], x = xv[i];
+        s0 = fmaf(w.x, x.x, s0);
+        s1 = fmaf(w.y, x.y, s1);
+        s0 = fmaf(w.z, x.z, s0);
+        s1 = fmaf(w.w, x.w, s1);
+      }
+      acc[r] += s0 + s1;
+    }
+  }
+};
+
+struct FragF16 {
+  template <bool P>
+  __device__ void load(const KArgs&, int, uint32_t, uint32_t) {}
+  template <bool P>
+  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float, float,
+                      float* acc) const {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const RowRef rr = row_of<P>(a, s, tile, r);
+      if (!rr.ok) continue;
+      const uint4* w4 = (const uint4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 4;
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint4 w = w4[i];
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const float4 x = xv[2 * i + k];
+          s0 = fmaf(h2f(ww[2 * k]), x.x, s0);
+          s1 = fmaf(h2f(ww[2 * k] >> 16), x.y, s1);
+          s0 = fmaf(h2f(ww[2 * k + 1]), x.z, s0);
+          s1 = fmaf(h2f(ww[2 * k + 1] >> 16), x.w, s1);
+        }
+      }
+      acc[r] += s0 + s1;
+    }
+  }
+};
+
+// ---- epilogues: apply(segment, tile, reduced sums); lane r < kR owns row r ----
 struct EpiStore {
+  static constexpr bool kPaired = false;
   float* y;
   uint32_t seg_out[3];  // output offset of each segment
   struct Wave {};
-  __device__ void apply(Wave&, int segi, const int* rows, const int* segof, const float* acc, int lane) const {
-    if (lane < kR && rows[lane] >= 0) y[seg_out[segof[lane]] + rows[lane]] = acc[lane];
+  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
+    if (lane < kR) {
+      const RowRef rr = row_of<false>(a, s, tile, lane);
+      if (rr.ok) y[seg_out[s] + rr.row] = acc[lane];
+    }
   }
   __device__ void finish(Wave&, int) const {}
 };
 
 struct EpiResidual {
+  static constexpr bool kPaired = false;
   float* h;
   struct Wave {};
-  __device__ void apply(Wave&, int, const int* rows, const int*, const float* acc, int lane) const {
-    if (lane < kR && rows[lane] >= 0) h[rows[lane]] = acc[lane] + h[rows[lane]];
+  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
+    if (lane < kR) {
+      const RowRef rr = row_of<false>(a, s, tile, lane);
+      if (rr.ok) h[rr.row] = acc[lane] + h[rr.row];
+    }
   }
   __device__ void finish(Wave&, int) const {}
 };
 
 struct EpiQkv {
+  static constexpr bool kPaired = false;
   QkvEpi e;
   struct Wave {};
   // rope (src/ops.rs:273-284): x[2i] = a*cos - b*sin, x[2i+1] = a*sin + b*cos
-  __device__ void apply(Wave&, int segi, const int* rows, const int*, const float* acc, int lane) const {
-    if (lane >= kR || rows[lane] < 0) return;
-    const int r = rows[lane];
+  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
+    if (lane >= kR) return;
+    const RowRef rr = row_of<false>(a, s, tile, lane);
+    if (!rr.ok) return;
+    const uint32_t r = (uint32_t)rr.row;
     float v = acc[lane];
-    if (segi < 2) {
-      const uint32_t i = (uint32_t)r % e.head_dim;
+    if (s < 2) {
+      const uint32_t i = r % e.head_dim;
       if (i < e.rope_dim) {
         const float2 cs = e.rope_cs[(uint64_t)e.state->rope_pos * (e.rope_dim / 2) + i / 2];
         const float other = acc[lane ^ 1];
         v = (i & 1) ? (other * cs.y + v * cs.x) : (v * cs.x - other * cs.y);
       }
     }
-    if (segi == 0) {
+    if (s == 0) {
       e.q_out[r] = v;
     } else {
-      const uint64_t off = (uint64_t)e.state->len * e.kv_dim + (uint64_t)r;
-      if (segi == 1) e.k_cache[off] = v;
+      const uint64_t off = (uint64_t)e.state->len * e.kv_dim + r;
+      if (s == 1) e.k_cache[off] = v;
       else e.v_cache[off] = v;
     }
   }
@@ -341,18 +464,20 @@ struct EpiQkv {
 };
 
 struct EpiSwiglu {
+  static constexpr bool kPaired = true;
   float* mid;
   struct Wave {};
   // swiglu (src/ops.rs:190-209): silu(g) * u, sigmoid clamped to +-80
-  __device__ void apply(Wave&, int, const int* rows, const int*, const float* acc, int lane) const {
+  __device__ void apply(Wave&, const KArgs& a, int, uint32_t tile, const float* acc, int lane) const {
     constexpr int H = kR / 2;
-    if (lane >= H || rows[lane] < 0) return;
-    float g = acc[lane];
-    const float u = acc[lane + H];
+    if (lane >= H) return;
+    const RowRef rr = row_of<true>(a, 0, tile, lane);
+    if (!rr.ok) return;
+    const float g = acc[lane], u = acc[lane + H];
     float c = fminf(fmaxf(g, -80.f), 80.f);
     if (g != g) c = g;
     const float sig = 1.0f / (1.0f + expf(-c));
-    mid[rows[lane]] = (g * sig) * u;
+    mid[rr.row] = (g * sig) * u;
   }
   __device__ void finish(Wave&, int) const {}
 };
@@ -364,19 +489,21 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) 
 }
 
 struct EpiLogits {
+  static constexpr bool kPaired = false;
   float* logits;
   DevState* state;
   struct Wave {
     unsigned long long best = 0;
     bool nan = false;
   };
-  __device__ void apply(Wave& w, int, const int* rows, const int*, const float* acc, int lane) const {
-    if (lane < kR && rows[lane] >= 0) logits[rows[lane]] = acc[lane];
+  __device__ void apply(Wave& w, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
 #pragma unroll
     for (int r = 0; r < kR; r++) {
-      if (rows[r] < 0) continue;
+      const RowRef rr = row_of<false>(a, s, tile, r);
+      if (!rr.ok) continue;
+      if (lane == r) logits[rr.row] = acc[r];
       if (acc[r] != acc[r]) w.nan = true;
-      const unsigned long long k = argmax_key(acc[r], (uint32_t)rows[r]);
+      const unsigned long long k = argmax_key(acc[r], (uint32_t)rr.row);
       w.best = k > w.best ? k : w.best;
     }
   }
@@ -388,15 +515,45 @@ struct EpiLogits {
   }
 };
 
-template <class Epi>
-__global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
-  extern __shared__ float lds[];
-  float* xl = lds;                                        // [groups][36]
-  float* xs = lds + (size_t)a.groups * kGroupStride;      // [cols/16]
-  __shared__ float red[kWaves];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// The units of one logical segment owned by this wave: tiles first, first+W,
+// ..., each swept in NG group steps.  `f` arrives holding the loads of the
+// first unit; the loads of each next unit are issued as soon as the current
+// one is decoded.  Latency is hidden by the other waves of the CU (no second
+// register buffer: keeps the kernel at four waves per SIMD).
+template <class Frag, class Epi>
+__device__ __forceinline__ void run_segment(const KArgs& a, const Epi& epi, typename Epi::Wave& ws, int s,
+                                            uint32_t first, uint32_t W, Frag& f, const float* xl,
+                                            const float* xs, int lane) {
+  constexpr bool P = Epi::kPaired;
+  const uint32_t NG = (a.groups + 63) / 64;
+  for (uint32_t tile = first; tile < a.ntiles[s]; tile += W) {
+    float acc[kR] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t it = 0; it < NG; it++) {
+      const uint32_t g = lane + 64 * it;
+      if (g < a.groups) {
+        const float4* xv4 = (const float4*)(xl + kGroupStride * g);
+        float4 xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = xv4[i];
+        f.template dot<P>(a, s, tile, g, xv, xs[2 * g], xs[2 * g + 1], acc);
+      }
+      uint32_t nt = tile, ni = it + 1;
+      if (ni == NG) {
+        ni = 0;
+        nt += W;
+      }
+      if (nt < a.ntiles[s]) f.template load<P>(a, s, nt, min(lane + 64 * ni, a.groups - 1));
+    }
+#pragma unroll
+    for (int r = 0; r < kR; r++) acc[r] = wave_sum(acc[r]);
+    epi.apply(ws, a, s, tile, acc, lane);
+  }
+}
 
-  // ---- prologue: x (optionally RMS-normalised) into LDS ----
+// Workgroup prologue: x (optionally RMS-normalised) into LDS, then the
+// 16-element sums of x.
+__device__ __forceinline__ void stage_x(const KArgs& a, float* xl, float* xs, float* red, int tid, int lane,
+                                        int wave, bool sums) {
   float ss = 0.f;
   for (uint32_t i = tid; i < a.cols; i += kThreads) {
     const float v = a.x[i];
@@ -415,7 +572,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
     for (uint32_t i = tid; i < a.cols; i += kThreads) xl[xpad(i)] = (xl[xpad(i)] * scale) * a.norm_w[i];
   }
   __syncthreads();
-  if (!a.generic) {
+  if (sums) {
     for (uint32_t j = tid; j < a.cols / 16; j += kThreads) {
       const float4* p = (const float4*)(xl + (j >> 1) * kGroupStride + 16 * (j & 1));
       const float4 u0 = p[0], u1 = p[1], u2 = p[2], u3 = p[3];
@@ -424,98 +581,195 @@ __global__ void __launch_bounds__(kThreads) k_gemv(KArgs a, Epi epi) {
     }
     __syncthreads();
   }
+}
 
-  // ---- row tiles ----
+// Main kernel: segments decode with FragA, or with FragB where use_b is set
+// (a Q4_K_M layer's QKV has Q4_K q/k and Q6_K v).
+template <class Epi, class FragA, class FragB>
+__global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi epi) {
+  extern __shared__ float lds[];
+  float* xl = lds;                                    // [groups][36]
+  float* xs = lds + (size_t)a.groups * kGroupStride;  // [cols/16]
+  __shared__ float red[kWaves];
+  // the wave index is uniform: tile and row bookkeeping stays in scalar registers
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t W = gridDim.x * kWaves, wid = blockIdx.x * kWaves + wave;
   typename Epi::Wave ws;
-  for (uint32_t tile = blockIdx.x * kWaves + wave; tile < a.ntiles; tile += gridDim.x * kWaves) {
-    int rows[kR], segof[kR], segi = 0;
-    if (a.paired) {
-      constexpr int H = kR / 2;
-#pragma unroll
-      for (int r = 0; r < kR; r++) {
-        const int s = r < H ? 0 : 1;
-        const uint32_t row = tile * H + (r % H);
-        segof[r] = s;
-        rows[r] = row < a.seg[s].rows ? (int)row : -1;
-      }
+
+  // first unit of segment 0 (always FragA) in flight while x is staged
+  constexpr bool P = Epi::kPaired;
+  constexpr bool kMixed = !std::is_same<FragA, FragB>::value;
+  {
+    const uint32_t first = (wid + W - a.rot[0]) % W;
+    FragA f;
+    // lanes past the last group load a real group (unconditional loads keep
+    // the fragments' live ranges short); their values are never used
+    if (first < a.ntiles[0]) f.template load<P>(a, 0, first, min((uint32_t)lane, a.groups - 1));
+    stage_x(a, xl, xs, red, tid, lane, wave, true);
+    if (first < a.ntiles[0]) run_segment<FragA, Epi>(a, epi, ws, 0, first, W, f, xl, xs, lane);
+  }
+  for (int s = 1; s < a.nseg; s++) {
+    const uint32_t first = (wid + W - a.rot[s]) % W;
+    if (first >= a.ntiles[s]) continue;
+    const uint32_t g0 = min((uint32_t)lane, a.groups - 1);
+    if (kMixed && ((a.use_b >> s) & 1u)) {
+      FragB f;
+      f.template load<P>(a, s, first, g0);
+      run_segment<FragB, Epi>(a, epi, ws, s, first, W, f, xl, xs, lane);
     } else {
-      const uint32_t v0 = tile * kR;
-      while (segi + 1 < a.nseg && v0 >= a.vbegin[segi + 1]) segi++;
-#pragma unroll
-      for (int r = 0; r < kR; r++) {
-        const uint32_t row = v0 + r - a.vbegin[segi];
-        segof[r] = segi;
-        rows[r] = row < a.seg[segi].rows ? (int)row : -1;
-      }
+      FragA f;
+      f.template load<P>(a, s, first, g0);
+      run_segment<FragA, Epi>(a, epi, ws, s, first, W, f, xl, xs, lane);
     }
-    float acc[kR];
-#pragma unroll
-    for (int r = 0; r < kR; r++) acc[r] = 0.f;
-    if (a.generic) tile_dot_generic(a.seg, segof, rows, xl, a.cols, lane, acc);
-    else switch (a.seg[segi].type) {
-      case T_Q4K: tile_dot<T_Q4K>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      case T_Q6K: tile_dot<T_Q6K>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      case T_Q8_0: tile_dot<T_Q8_0>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      case T_Q4_0: tile_dot<T_Q4_0>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      case T_Q8K: tile_dot<T_Q8K>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      case T_F32: tile_dot<T_F32>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-      default: tile_dot<T_F16>(a.seg, segof, rows, xl, xs, a.groups, a.cols, lane, acc); break;
-    }
-#pragma unroll
-    for (int r = 0; r < kR; r++) acc[r] = wave_sum(acc[r]);
-    epi.apply(ws, segi, rows, segof, acc, lane);
   }
   epi.finish(ws, lane);
 }
 
-bool build_args(const GemvLaunch& L, KArgs* a) {
-  if (L.nseg < 1 || L.nseg > 3 || L.cols == 0) return false;
-  *a = KArgs{};
-  a->nseg = L.nseg;
-  a->paired = L.paired ? 1 : 0;
-  a->cols = L.cols;
-  a->generic = L.cols % 32 ? 1 : 0;
-  a->groups = (L.cols + 31) / 32;
-  a->x = L.x;
-  a->norm_w = L.norm_w;
-  a->eps = L.eps;
-  uint32_t v = 0;
-  for (int s = 0; s < L.nseg; s++) {
-    a->seg[s] = L.seg[s];
-    a->vbegin[s] = v;
-    v += (L.seg[s].rows + kR - 1) / kR * kR;
-    if ((L.seg[s].type == T_Q4K || L.seg[s].type == T_Q6K || L.seg[s].type == T_Q8K) && L.cols % 256)
-      return false;
-    if (a->generic && L.seg[s].type != T_F32 && L.seg[s].type != T_F16) return false;
+// Rows that are not whole 32-element groups (F32/F16 only): lanes stride over
+// the elements of each row.
+template <class Epi>
+__global__ void __launch_bounds__(kThreads) k_gemv_generic(KArgs a, Epi epi) {
+  extern __shared__ float lds[];
+  __shared__ float red[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_x(a, lds, nullptr, red, tid, lane, wave, false);
+  const uint32_t W = gridDim.x * kWaves, wid = blockIdx.x * kWaves + wave;
+  typename Epi::Wave ws;
+  for (int s = 0; s < a.nseg; s++) {
+    for (uint32_t t = (wid + W - a.rot[s]) % W; t < a.ntiles[s]; t += W) {
+      float acc[kR] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < kR; r++) {
+        const RowRef rr = row_of<Epi::kPaired>(a, s, t, r);
+        if (!rr.ok) continue;
+        const bool f32 = a.seg[Epi::kPaired ? (r < kR / 2 ? 0 : 1) : s].type == T_F32;
+        const uint64_t base = rr.row * a.cols;
+        float v = 0.f;
+        for (uint32_t l = lane; l < a.cols; l += 64) {
+          const float w = f32 ? ((const float*)rr.body)[base + l] : h2f(((const uint16_t*)rr.body)[base + l]);
+          v = fmaf(w, lds[xpad(l)], v);
+        }
+        acc[r] = v;
+      }
+#pragma unroll
+      for (int r = 0; r < kR; r++) acc[r] = wave_sum(acc[r]);
+      epi.apply(ws, a, s, t, acc, lane);
+    }
   }
-  a->vbegin[L.nseg] = v;
-  if (L.paired) {
-    if (L.nseg != 2 || L.seg[0].rows != L.seg[1].rows || L.seg[0].type != L.seg[1].type) return false;
-    a->ntiles = (L.seg[0].rows + kR / 2 - 1) / (kR / 2);
-  } else {
-    a->ntiles = v / kR;
+  epi.finish(ws, lane);
+}
+
+int device_cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+    if (n <= 0) n = 256;
   }
-  return true;
+  return n;
+}
+
+template <class K>
+hipError_t lds_opt_in(K kernel, size_t lds, bool& done) {
+  if (lds > 64 * 1024 && !done) {  // rows of >16K columns need more than 64 KiB of LDS
+    hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+    if (e != hipSuccess) return e;
+    done = true;
+  }
+  return hipSuccess;
+}
+
+template <class Epi, class FA, class FB>
+hipError_t dispatch(const KArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
+  static bool done = false;
+  hipError_t e = lds_opt_in(k_gemv<Epi, FA, FB>, lds, done);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_gemv<Epi, FA, FB>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
+  return hipGetLastError();
+}
+
+template <class Epi, class FA>
+hipError_t dispatch_b(const KArgs& a, uint32_t tb, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
+  switch (tb) {
+    case T_Q4K: return dispatch<Epi, FA, FragQ4K>(a, epi, blocks, lds, st);
+    case T_Q6K: return dispatch<Epi, FA, FragQ6K>(a, epi, blocks, lds, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <class Epi>
 hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
-  KArgs a;
-  if (!build_args(L, &a)) return hipErrorInvalidValue;
+  if (L.nseg < 1 || L.nseg > 3 || L.cols == 0) return hipErrorInvalidValue;
+  KArgs a{};
+  a.cols = L.cols;
+  a.groups = (L.cols + 31) / 32;
+  a.x = L.x;
+  a.norm_w = L.norm_w;
+  a.eps = L.eps;
+  const bool generic = L.cols % 32 != 0;
+  for (int s = 0; s < L.nseg; s++) {
+    a.seg[s] = L.seg[s];
+    const uint32_t t = L.seg[s].type;
+    if ((t == T_Q4K || t == T_Q6K || t == T_Q8K) && L.cols % 256) return hipErrorInvalidValue;
+    if (generic && t != T_F32 && t != T_F16) return hipErrorInvalidValue;
+  }
+  if (Epi::kPaired) {
+    if (L.nseg != 2 || L.seg[0].rows != L.seg[1].rows || L.seg[0].type != L.seg[1].type) return hipErrorInvalidValue;
+    a.nseg = 1;
+    a.ntiles[0] = (L.seg[0].rows + kR / 2 - 1) / (kR / 2);
+  } else {
+    a.nseg = L.nseg;
+    for (int s = 0; s < L.nseg; s++) a.ntiles[s] = (L.seg[s].rows + kR - 1) / kR;
+  }
   const size_t lds = (size_t)a.groups * kGroupStride * 4 + (size_t)(a.cols / 16) * 4;
   if (lds > 150 * 1024) return hipErrorInvalidValue;
-  uint32_t blocks = (a.ntiles + kWaves - 1) / kWaves;
-  if (blocks > 1024) blocks = 1024;
-  if (blocks == 0) return hipSuccess;
-  static bool lds_attr_set = false;  // rows of >16K columns need more than 64 KiB of LDS
-  if (lds > 64 * 1024 && !lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_gemv<Epi>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       150 * 1024);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
+  uint32_t total = 0;
+  for (int s = 0; s < a.nseg; s++) total += a.ntiles[s];
+  if (total == 0) return hipSuccess;
+  // persistent grid: as many workgroups as fit per CU (LDS-bound for long
+  // rows), never more waves than tiles
+  const uint32_t per_cu = (uint32_t)std::max<size_t>(1, std::min<size_t>(kBlocksPerCu, (160 * 1024) / lds));
+  const uint32_t blocks = std::min<uint32_t>((total + kWaves - 1) / kWaves, per_cu * device_cu_count());
+  const uint32_t W = blocks * kWaves;
+  uint32_t acc = 0;
+  for (int s = 0; s < a.nseg; s++) {
+    a.rot[s] = acc % W;
+    acc += a.ntiles[s];
   }
-  hipLaunchKernelGGL(k_gemv<Epi>, dim3(blocks), dim3(kThreads), lds, st, a, epi);
-  return hipGetLastError();
+  if (generic) {
+    static bool done = false;
+    hipError_t e = lds_opt_in(k_gemv_generic<Epi>, lds, done);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_gemv_generic<Epi>, dim3(blocks), dim3(kThreads), lds, st, a, epi);
+    return hipGetLastError();
+  }
+  // segments of the first type decode with FragA, the others with FragB
+  const uint32_t ta = L.seg[0].type;
+  uint32_t tb = ta;
+  for (int s = 0; s < a.nseg; s++)
+    if (L.seg[s].type != ta) {
+      if (tb != ta && L.seg[s].type != tb) return hipErrorInvalidValue;  // at most two types
+      tb = L.seg[s].type;
+      a.use_b |= 1u << s;
+    }
+  if (tb == ta) {
+    switch (ta) {
+      case T_Q4K: return dispatch<Epi, FragQ4K, FragQ4K>(a, epi, blocks, lds, st);
+      case T_Q6K: return dispatch<Epi, FragQ6K, FragQ6K>(a, epi, blocks, lds, st);
+      case T_Q8_0: return dispatch<Epi, FragQ80, FragQ80>(a, epi, blocks, lds, st);
+      case T_Q4_0: return dispatch<Epi, FragQ40, FragQ40>(a, epi, blocks, lds, st);
+      case T_Q8K: return dispatch<Epi, FragQ8K, FragQ8K>(a, epi, blocks, lds, st);
+      case T_F32: return dispatch<Epi, FragF32, FragF32>(a, epi, blocks, lds, st);
+      case T_F16: return dispatch<Epi, FragF16, FragF16>(a, epi, blocks, lds, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (ta) {  // mixed Q4_K / Q6_K (Q4_K_M layers)
+    case T_Q4K: return dispatch_b<Epi, FragQ4K>(a, tb, epi, blocks, lds, st);
+    case T_Q6K: return dispatch_b<Epi, FragQ6K>(a, tb, epi, blocks, lds, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace

@@ -100,11 +100,16 @@ struct AttnArgs {
   const float* k_cache;  // layer base [max_seq][kv_dim]
   const float* v_cache;
   float* out;            // [n_heads * head_dim]
-  float* partial;        // [n_kv][max_chunks][group][head_dim + 2]
+  float* partial;        // [n_kv][max_chunks][attn_partial_floats(group, head_dim)]
   uint32_t* counters;    // [n_kv], zero between launches
   const DevState* state;
   uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk;
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
+// floats of one partial record (per kv head and chunk): o[group][head_dim],
+// max[group], sum[group], padded to a multiple of 4
+__host__ __device__ inline uint32_t attn_partial_floats(uint32_t group, uint32_t head_dim) {
+  return (group * head_dim + 2 * group + 3) & ~3u;
+}
 
 }  // namespace ifx
