@@ -550,10 +550,86 @@ __device__ __forceinline__ void run_segment(const KArgs& a, const Epi& epi, type
   }
 }
 
-// Workgroup prologue: x (optionally RMS-normalised) into LDS, then the
-// 16-element sums of x.
-__device__ __forceinline__ void stage_x(const KArgs& a, float* xl, float* xs, float* red, int tid, int lane,
-                                        int wave, bool sums) {
+// rms_norm (src/ops.rs:162-167): scale = 1/sqrt(mean(x^2) + eps); x = (x*scale)*w.
+// Reduces the per-thread sums of squares over the workgroup.
+__device__ __forceinline__ float norm_scale(const KArgs& a, float ss, float* red, int lane, int wave) {
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) tot += red[w];
+  return 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+}
+
+// Workgroup prologue (cols % 32 == 0): x, optionally RMS-normalised, into LDS
+// and the 16-element sums of x.  Every thread issues all its float4 loads of
+// x (and of the norm weights, staged in wl) before the first wait, so the
+// prologue costs one memory round trip.
+constexpr int kStage = 8;  // float4 loads per thread per batch
+template <bool NORM>
+__device__ __forceinline__ float stage_load(const KArgs& a, float* xl, float* wl, int tid) {
+  const uint32_t n4 = a.cols / 4;
+  const float4* x4 = (const float4*)a.x;
+  const float4* w4 = (const float4*)a.norm_w;
+  float ss = 0.f;
+  for (uint32_t b = tid; b < n4; b += kThreads * kStage) {
+    float4 v[kStage], w[kStage];
+#pragma unroll
+    for (int k = 0; k < kStage; k++) {
+      const uint32_t i = min(b + k * kThreads, n4 - 1);  // clamped: loads stay unconditional
+      v[k] = x4[i];
+      if (NORM) w[k] = w4[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kStage; k++) {
+      const uint32_t i = b + k * kThreads;
+      if (i < n4) {
+        *(float4*)(xl + xpad(4 * i)) = v[k];  // 4 | 32: a float4 never straddles a group
+        if (NORM) {
+          *(float4*)(wl + 4 * i) = w[k];
+          ss = fmaf(v[k].x, v[k].x, ss);
+          ss = fmaf(v[k].y, v[k].y, ss);
+          ss = fmaf(v[k].z, v[k].z, ss);
+          ss = fmaf(v[k].w, v[k].w, ss);
+        }
+      }
+    }
+  }
+  return ss;
+}
+
+__device__ __forceinline__ void stage_x(const KArgs& a, float* xl, float* xs, float* wl, float* red, int tid,
+                                        int lane, int wave) {
+  const uint32_t n4 = a.cols / 4;
+  if (a.norm_w) {
+    const float ss = stage_load<true>(a, xl, wl, tid);
+    const float scale = norm_scale(a, ss, red, lane, wave);
+    for (uint32_t i = tid; i < n4; i += kThreads) {
+      float4 v = *(float4*)(xl + xpad(4 * i));
+      const float4 w = *(const float4*)(wl + 4 * i);
+      v.x = (v.x * scale) * w.x;
+      v.y = (v.y * scale) * w.y;
+      v.z = (v.z * scale) * w.z;
+      v.w = (v.w * scale) * w.w;
+      *(float4*)(xl + xpad(4 * i)) = v;
+    }
+  } else {
+    stage_load<false>(a, xl, wl, tid);
+  }
+  __syncthreads();
+  for (uint32_t j = tid; j < a.cols / 16; j += kThreads) {
+    const float4* p = (const float4*)(xl + (j >> 1) * kGroupStride + 16 * (j & 1));
+    const float4 u0 = p[0], u1 = p[1], u2 = p[2], u3 = p[3];
+    xs[j] = ((u0.x + u0.y) + (u0.z + u0.w)) + ((u1.x + u1.y) + (u1.z + u1.w)) +
+            (((u2.x + u2.y) + (u2.z + u2.w)) + ((u3.x + u3.y) + (u3.z + u3.w)));
+  }
+  __syncthreads();
+}
+
+// Prologue of the generic kernel (any cols): x, optionally RMS-normalised, into LDS.
+__device__ __forceinline__ void stage_x_generic(const KArgs& a, float* xl, float* red, int tid, int lane,
+                                                int wave) {
   float ss = 0.f;
   for (uint32_t i = tid; i < a.cols; i += kThreads) {
     const float v = a.x[i];
@@ -561,26 +637,10 @@ __device__ __forceinline__ void stage_x(const KArgs& a, float* xl, float* xs, fl
     ss = fmaf(v, v, ss);
   }
   if (a.norm_w) {
-    ss = wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) tot += red[w];
-    // rms_norm (src/ops.rs:162-167): scale = 1/sqrt(mean + eps); x = (x*scale)*w
-    const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+    const float scale = norm_scale(a, ss, red, lane, wave);
     for (uint32_t i = tid; i < a.cols; i += kThreads) xl[xpad(i)] = (xl[xpad(i)] * scale) * a.norm_w[i];
   }
   __syncthreads();
-  if (sums) {
-    for (uint32_t j = tid; j < a.cols / 16; j += kThreads) {
-      const float4* p = (const float4*)(xl + (j >> 1) * kGroupStride + 16 * (j & 1));
-      const float4 u0 = p[0], u1 = p[1], u2 = p[2], u3 = p[3];
-      xs[j] = ((u0.x + u0.y) + (u0.z + u0.w)) + ((u1.x + u1.y) + (u1.z + u1.w)) +
-              (((u2.x + u2.y) + (u2.z + u2.w)) + ((u3.x + u3.y) + (u3.z + u3.w)));
-    }
-    __syncthreads();
-  }
 }
 
 // Main kernel: segments decode with FragA, or with FragB where use_b is set
@@ -590,6 +650,7 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
   extern __shared__ float lds[];
   float* xl = lds;                                    // [groups][36]
   float* xs = lds + (size_t)a.groups * kGroupStride;  // [cols/16]
+  float* wl = xs + ((a.cols / 16 + 3) & ~3u);         // [cols] norm weights (norm launches), 16-B aligned
   __shared__ float red[kWaves];
   // the wave index is uniform: tile and row bookkeeping stays in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -605,7 +666,7 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
     // lanes past the last group load a real group (unconditional loads keep
     // the fragments' live ranges short); their values are never used
     if (first < a.ntiles[0]) f.template load<P>(a, 0, first, min((uint32_t)lane, a.groups - 1));
-    stage_x(a, xl, xs, red, tid, lane, wave, true);
+    stage_x(a, xl, xs, wl, red, tid, lane, wave);
     if (first < a.ntiles[0]) run_segment<FragA, Epi>(a, epi, ws, 0, first, W, f, xl, xs, lane);
   }
   for (int s = 1; s < a.nseg; s++) {
@@ -632,7 +693,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(KArgs a, Epi epi) {
   extern __shared__ float lds[];
   __shared__ float red[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_x(a, lds, nullptr, red, tid, lane, wave, false);
+  stage_x_generic(a, lds, red, tid, lane, wave);
   const uint32_t W = gridDim.x * kWaves, wid = blockIdx.x * kWaves + wave;
   typename Epi::Wave ws;
   for (int s = 0; s < a.nseg; s++) {
@@ -722,7 +783,8 @@ hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     a.nseg = L.nseg;
     for (int s = 0; s < L.nseg; s++) a.ntiles[s] = (L.seg[s].rows + kR - 1) / kR;
   }
-  const size_t lds = (size_t)a.groups * kGroupStride * 4 + (size_t)(a.cols / 16) * 4;
+  const size_t lds = (size_t)a.groups * kGroupStride * 4 + (size_t)((a.cols / 16 + 3) & ~3u) * 4 +
+                     (L.norm_w && !generic ? (size_t)a.cols * 4 : 0);
   if (lds > 150 * 1024) return hipErrorInvalidValue;
   uint32_t total = 0;
   for (int s = 0; s < a.nseg; s++) total += a.ntiles[s];
