@@ -24,18 +24,11 @@ constexpr int kChunk = 64;       // cache rows per workgroup (4 threads per row 
 constexpr int kMaxGroup = 8;
 constexpr int kMaxHd = 256;
 constexpr int kMaxMerge = 256;   // chunks per kv head (max_seq <= kMaxMerge * kChunk)
-constexpr int kMergeBatch = 16;  // partial rows loaded together per merging thread
+constexpr int kMergeBatch = 24;  // partial rows loaded together per merging thread
+// true: the last workgroup of each kv head merges the chunk records (counter +
+// release/acquire); false: a second launch merges them
+constexpr bool kFusedMerge = false;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
 __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
   acc.x = fmaf(w, v.x, acc.x);
   acc.y = fmaf(w, v.y, acc.y);
@@ -47,147 +40,54 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-// HDT: the head dim when > 0 (register arrays sized exactly), 0 for any
-// multiple of 4 up to kMaxHd.
-template <int HDT>
-__global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
-  constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;                    // float4 per head row
-  constexpr int KPT = (NC4M + 3) / 4;                                    // K float4 per thread
-  constexpr int VPT = HDT > 0 ? (kChunk * NC4M + kThreads - 1) / kThreads : 16;  // V float4 per thread
-  __shared__ float4 qs[kMaxGroup * NC4M];
-  __shared__ float sc[kMaxGroup * kChunk];
-  __shared__ float4 red[kThreads * kMaxGroup];  // [position group][g][float4 column], npg * nc4 <= kThreads
-  __shared__ float mstat[kMaxGroup], lstat[kMaxGroup];
-  __shared__ float cw[kMaxGroup * kMaxMerge];
-  __shared__ int is_last;
+// ---- wave reductions on the DPP network (no LDS round trips) ----
+// gfx9 DPP controls: row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+// Prefix doubling inside each 16-lane row (shr 1, 2, then 4 and 8 on the upper
+// banks) leaves the row total in its lane 15; the row broadcasts carry rows
+// 0..2 into lane 63.  Lanes whose source is outside the row take the identity.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK,
+                                                    BANK_MASK, false));
+}
+// max / sum over the 64 lanes, returned uniform (lane 63 holds the full result)
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f<0x111, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<0x112, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<0x114, 0xf, 0xe>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<0x118, 0xf, 0xc>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<0x142, 0xa, 0xf>(-INFINITY, v));
+  v = fmaxf(v, dpp_f<0x143, 0xc, 0xf>(-INFINITY, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0x111, 0xf, 0xf>(0.f, v);
+  v += dpp_f<0x112, 0xf, 0xf>(0.f, v);
+  v += dpp_f<0x114, 0xf, 0xe>(0.f, v);
+  v += dpp_f<0x118, 0xf, 0xc>(0.f, v);
+  v += dpp_f<0x142, 0xa, 0xf>(0.f, v);
+  v += dpp_f<0x143, 0xc, 0xf>(0.f, v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// sum over the four lanes of each quad, result in all four (quad_perm [1,0,3,2], [2,3,0,1])
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+  return v;
+}
 
-  const uint32_t c = blockIdx.x, hk = blockIdx.y;
-  const uint32_t G = a.n_heads / a.n_kv_heads;
-  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4, kvd = a.n_kv_heads * HD;
-  const uint32_t lo = a.state->attn_lo;
-  const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
-  const uint32_t nrows = hi > lo ? hi - lo : 0;
-  const uint32_t nch = (nrows + kChunk - 1) / kChunk;
-  if (c >= nch) return;
-  const uint32_t t0 = lo + c * kChunk;
-  const uint32_t n = (t0 + kChunk <= hi) ? kChunk : hi - t0;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+constexpr int kRowsPerWave = kChunk / (kThreads / 64);  // 16
 
-  // ---- K rows (4 threads per row, every 4th float4) and V rows (thread =
-  // float4 column x position group), all loads in flight together ----
-  const uint32_t kp = tid >> 2, kq = tid & 3;
-  float4 kr[KPT];
-  {
-    const float4* k4 = (const float4*)(a.k_cache + (uint64_t)(t0 + kp) * kvd + hk * HD);
-#pragma unroll
-    for (int i = 0; i < KPT; i++) {
-      const uint32_t ch = kq + 4 * i;
-      if (kp < n && ch < nc4) kr[i] = k4[ch];
-    }
-  }
-  const uint32_t npg = kThreads / nc4, vch = tid % nc4, pg = tid / nc4;
-  float4 vr[VPT];
-#pragma unroll
-  for (int i = 0; i < VPT; i++) {
-    const uint32_t p = pg + npg * i;
-    if (pg < npg && p < n) vr[i] = ((const float4*)(a.v_cache + (uint64_t)(t0 + p) * kvd + hk * HD))[vch];
-  }
-  for (uint32_t i = tid; i < G * nc4; i += kThreads) qs[i] = ((const float4*)(a.q + (uint64_t)hk * G * HD))[i];
-  __syncthreads();
-
-  // ---- scores (src/model/forward.rs:388-397) ----
-  {
-    float s[kMaxGroup];
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; g++) s[g] = 0.f;
-#pragma unroll
-    for (int i = 0; i < KPT; i++) {
-      const uint32_t ch = kq + 4 * i;
-      if (kp < n && ch < nc4) {
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; g++) {
-          if (g < (int)G) {
-            const float4 qv = qs[g * nc4 + ch];
-            s[g] = fmaf(qv.x, kr[i].x, s[g]);
-            s[g] = fmaf(qv.y, kr[i].y, s[g]);
-            s[g] = fmaf(qv.z, kr[i].z, s[g]);
-            s[g] = fmaf(qv.w, kr[i].w, s[g]);
-          }
-        }
-      }
-    }
-    const float rs = sqrtf((float)HD);
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; g++) {
-      s[g] += __shfl_xor(s[g], 1, 64);
-      s[g] += __shfl_xor(s[g], 2, 64);
-      if (g < (int)G && kq == 0 && kp < n) sc[g * kChunk + kp] = s[g] / rs;
-    }
-  }
-  __syncthreads();
-
-  // ---- chunk-local softmax statistics (softmax_rows, src/ops.rs:223-239) ----
-  for (uint32_t g = wave; g < G; g += kThreads / 64) {
-    const float v = lane < (int)n ? sc[g * kChunk + lane] : -INFINITY;
-    const float m = wave_max(v);
-    const float e = lane < (int)n ? expf(v - m) : 0.f;
-    const float l = wave_sum(e);
-    if (lane < (int)n) sc[g * kChunk + lane] = e;
-    if (lane == 0) {
-      mstat[g] = m;
-      lstat[g] = l;
-    }
-  }
-  __syncthreads();
-
-  // ---- o = sum_t e_t v_t (src/model/forward.rs:401-409), position groups
-  // summed through LDS ----
-  if (pg < npg) {
-    float4 o[kMaxGroup];
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; g++) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < VPT; i++) {
-      const uint32_t p = pg + npg * i;
-      if (p < n) {
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; g++)
-          if (g < (int)G) o[g] = fma4(sc[g * kChunk + p], vr[i], o[g]);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; g++)
-      if (g < (int)G) red[(pg * G + g) * nc4 + vch] = o[g];
-  }
-  __syncthreads();
+// Combines the chunk records of kv head hk into the attention output: weights
+// w_c = exp(m_c - M) / sum_c l_c w_c over the chunks c (the usual max rescaling).
+template <int HDT, int GT>
+__device__ __forceinline__ void merge_head(const AttnArgs& a, uint32_t hk, uint32_t nch, float* cw, float* lstat,
+                                           float4* red) {
+  constexpr int GM = GT > 0 ? GT : kMaxGroup;
+  const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
   const uint32_t rec = attn_partial_floats(G, HD);
-  float* part = a.partial + ((uint64_t)hk * a.max_chunks + c) * rec;
-  for (uint32_t item = tid; item < G * nc4; item += kThreads) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t q = 0; q < npg; q++) acc = add4(acc, red[q * G * nc4 + item]);
-    ((float4*)part)[item] = acc;
-  }
-  if (tid < (int)G) {
-    part[G * HD + tid] = mstat[tid];
-    part[G * HD + G + tid] = lstat[tid];
-  }
-
-  // ---- the last workgroup of this kv head merges all chunks ----
-  // Every wave waits until its partial stores have reached L2; after the
-  // barrier one agent-scope release (an L2 write-back) by wave 0 publishes the
-  // whole record before the counter increment.  One write-back per workgroup
-  // instead of one per wave: these serialise per L2 and dominate otherwise.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (wave == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(&a.counters[hk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (old == nch - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* base = a.partial + (uint64_t)hk * a.max_chunks * rec;
   const uint32_t items = G * nc4;
   const uint32_t nsplit = items >= (uint32_t)kThreads ? 1u : kThreads / items;
@@ -201,29 +101,33 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
       ov[k] = ((const float4*)(base + (uint64_t)cc * rec))[item0];
     }
   }
-  // weights w_c = exp(m_c - M) and den = sum_c l_c w_c, one wave per query head
-  for (uint32_t g = wave; g < G; g += kThreads / 64) {
+  // weights w_c = exp(m_c - M) and den = sum_c l_c w_c, one wave per query
+  // head; the loads are clamped to real chunks (no branches around them)
+#pragma unroll
+  for (int gg = 0; gg < (GM + 3) / 4; gg++) {
+    const uint32_t g = wave + 4 * gg;
+    if (g >= G) break;
     float m[kMaxMerge / 64], l[kMaxMerge / 64];
     float M = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kMaxMerge / 64; j++) {
       const uint32_t cc = lane + 64 * j;
-      m[j] = cc < nch ? base[(uint64_t)cc * rec + G * HD + g] : -INFINITY;
-      l[j] = cc < nch ? base[(uint64_t)cc * rec + G * HD + G + g] : 0.f;
+      const uint64_t at = (uint64_t)min(cc, nch - 1) * rec + G * HD;
+      const float mv = base[at + g];
+      m[j] = cc < nch ? mv : -INFINITY;
+      l[j] = base[at + G + g];
       M = fmaxf(M, m[j]);
     }
-    M = wave_max(M);
+    M = wave_max_dpp(M);
     float den = 0.f;
 #pragma unroll
     for (int j = 0; j < kMaxMerge / 64; j++) {
       const uint32_t cc = lane + 64 * j;
-      if (cc < nch) {
-        const float w = expf(m[j] - M);
-        cw[g * kMaxMerge + cc] = w;
-        den = fmaf(l[j], w, den);
-      }
+      const float w = cc < nch ? expf(m[j] - M) : 0.f;
+      cw[g * kMaxMerge + cc] = w;
+      den = fmaf(l[j], w, den);
     }
-    den = wave_sum(den);
+    den = wave_sum_dpp(den);
     if (lane == 0) lstat[g] = den;
   }
   __syncthreads();
@@ -266,7 +170,206 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
           make_float4(acc.x / den, acc.y / den, acc.z / den, acc.w / den);
     }
   }
+}
+
+// HDT: the head dim when > 0 (register arrays sized exactly), 0 for any
+// multiple of 4 up to kMaxHd.  GT: the query heads per kv head when > 0, 0 for
+// any up to kMaxGroup.  With both fixed the unrolled loops carry no branches.
+//
+// Each wave owns 16 cache rows of the chunk end to end:
+//   scores  lane = (row l/4, quarter l%4): the quarter's float4 columns
+//           ch = l%4 + 4i, q from LDS, a quad reduction on the DPP network;
+//   softmax max / sum over the wave's rows on the DPP network;
+//   p . V   lane = columns 2l, 2l+1 (+128 j) of all 16 rows, the row weights
+//           broadcast with readlane: no cross-lane reduction.
+// The four waves are combined once through LDS into the chunk's record.
+template <int HDT, int GT, bool FUSED>
+__global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
+  constexpr int GM = GT > 0 ? GT : kMaxGroup;  // loop bound over query heads
+  constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;      // float4 per head row
+  constexpr int KPT = (NC4M + 3) / 4;                      // K float4 per lane
+  constexpr int VJ = ((HDT > 0 ? HDT : kMaxHd) + 127) / 128;  // column pairs per lane
+  __shared__ float4 qs[GM * NC4M];
+  __shared__ float wst[kThreads / 64][2][GM];                      // per wave: max, sum
+  __shared__ float2 wo[kThreads / 64][GM][NC4M * 2];               // per wave: unnormalised o
+  __shared__ float4 red[kThreads];                                 // merge: split partial sums
+  __shared__ float lstat[GM];
+  __shared__ float cw[GM * kMaxMerge];
+  __shared__ int is_last;
+
+  const uint32_t c = blockIdx.x, hk = blockIdx.y;
+  const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4, kvd = a.n_kv_heads * HD;
+  const uint32_t lo = a.state->attn_lo;
+  const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
+  const uint32_t nrows = hi > lo ? hi - lo : 0;
+  const uint32_t nch = (nrows + kChunk - 1) / kChunk;
+  if (c >= nch) return;
+  const uint32_t t0 = lo + c * kChunk;
+  const uint32_t n = (t0 + kChunk <= hi) ? kChunk : hi - t0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t r0 = wave * kRowsPerWave;  // first chunk row of this wave
+  // rows past the chunk's end read the last real row (weight 0)
+  auto cache_row = [&](uint32_t r) -> uint64_t { return (uint64_t)(t0 + min(r, n - 1)) * kvd + hk * HD; };
+
+  // ---- K, V and q loads, all in flight together ----
+  const uint32_t kr_row = r0 + lane / 4, kq = lane & 3;
+  float4 kr[KPT];
+  {
+    const float4* k4 = (const float4*)(a.k_cache + cache_row(kr_row));
+#pragma unroll
+    for (int i = 0; i < KPT; i++) {
+      const uint32_t ch = kq + 4 * i;
+      kr[i] = ch < nc4 ? k4[ch] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float2 vr[kRowsPerWave][VJ];
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; r++) {
+    const float* vrow = a.v_cache + cache_row(r0 + r);
+#pragma unroll
+    for (int jj = 0; jj < VJ; jj++) {
+      const uint32_t col = 2 * lane + 128 * jj;
+      vr[r][jj] = col < HD ? *(const float2*)(vrow + col) : make_float2(0.f, 0.f);
+    }
+  }
+  for (uint32_t i = tid; i < G * nc4; i += kThreads) qs[i] = ((const float4*)(a.q + (uint64_t)hk * G * HD))[i];
+  // the compiler may issue the q load first and wait for it alone; waiting
+  // for everything here keeps K, V and q in one memory round trip
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // ---- scores (src/model/forward.rs:388-397) and the wave's softmax statistics
+  // (softmax_rows, src/ops.rs:223-239) ----
+  const bool row_ok = kr_row < n;
+  const float rs = sqrtf((float)HD);
+  float e_row[GM];  // exp(s - m_wave) of this lane's row, per query head
+  float m_w[GM], l_w[GM];
+#pragma unroll
+  for (int g = 0; g < GM; g++) {
+    e_row[g] = 0.f;
+    m_w[g] = -INFINITY;
+    l_w[g] = 0.f;
+    if (g < (int)G) {
+      float sg = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPT; i++) {
+        const uint32_t ch = kq + 4 * i;
+        if (ch < nc4) {
+          const float4 qv = qs[g * nc4 + ch];
+          sg = fmaf(qv.x, kr[i].x, sg);
+          sg = fmaf(qv.y, kr[i].y, sg);
+          sg = fmaf(qv.z, kr[i].z, sg);
+          sg = fmaf(qv.w, kr[i].w, sg);
+        }
+      }
+      const float sv = quad_sum(sg) / rs;
+      m_w[g] = wave_max_dpp(row_ok ? sv : -INFINITY);
+      e_row[g] = row_ok ? expf(sv - m_w[g]) : 0.f;
+      l_w[g] = wave_sum_dpp(kq == 0 ? e_row[g] : 0.f);
+    }
+  }
+
+  // ---- o = sum_t e_t v_t over the wave's rows (src/model/forward.rs:401-409) ----
+  float2 o[GM][VJ];
+#pragma unroll
+  for (int g = 0; g < GM; g++)
+#pragma unroll
+    for (int jj = 0; jj < VJ; jj++) o[g][jj] = make_float2(0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; r++) {
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+      if (g < (int)G) {
+        const float e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_row[g]), 4 * r));
+#pragma unroll
+        for (int jj = 0; jj < VJ; jj++) {
+          o[g][jj].x = fmaf(e, vr[r][jj].x, o[g][jj].x);
+          o[g][jj].y = fmaf(e, vr[r][jj].y, o[g][jj].y);
+        }
+      }
+    }
+  }
+
+  // ---- combine the four waves into the chunk's record ----
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+      wst[wave][0][g] = m_w[g];
+      wst[wave][1][g] = l_w[g];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GM; g++)
+#pragma unroll
+    for (int jj = 0; jj < VJ; jj++)
+      if (g < (int)G && 2 * lane + 128 * jj < HD) wo[wave][g][lane + 64 * jj] = o[g][jj];
+  __syncthreads();
+  const uint32_t rec = attn_partial_floats(G, HD);
+  float* part = a.partial + ((uint64_t)hk * a.max_chunks + c) * rec;
+  for (uint32_t item = tid; item < G * HD / 2; item += kThreads) {
+    const uint32_t g = item / (HD / 2), cp = item % (HD / 2);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) M = fmaxf(M, wst[w][0][g]);
+    float2 acc = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) {
+      // waves whose rows are all past the chunk end have max -inf: weight 0
+      const float mw = wst[w][0][g];
+      const float sc = mw == -INFINITY ? 0.f : expf(mw - M);
+      acc.x = fmaf(sc, wo[w][g][cp].x, acc.x);
+      acc.y = fmaf(sc, wo[w][g][cp].y, acc.y);
+    }
+    *(float2*)(part + g * HD + 2 * cp) = acc;
+  }
+  if (tid < (int)G) {
+    float M = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) M = fmaxf(M, wst[w][0][tid]);
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) {
+      const float mw = wst[w][0][tid];
+      L = fmaf(mw == -INFINITY ? 0.f : expf(mw - M), wst[w][1][tid], L);
+    }
+    part[G * HD + tid] = M;
+    part[G * HD + G + tid] = L;
+  }
+
+  if (!FUSED) return;
+  // ---- the last workgroup of this kv head merges all chunks ----
+  // Every wave waits until its partial stores have reached L2; after the
+  // barrier one agent-scope release (an L2 write-back) by wave 0 publishes the
+  // whole record before the counter increment.  One write-back per workgroup
+  // instead of one per wave: these serialise per L2 and dominate otherwise.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (wave == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(&a.counters[hk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (old == nch - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  merge_head<HDT, GT>(a, hk, nch, cw, lstat, red);
   if (tid == 0) __hip_atomic_store(&a.counters[hk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The merge as its own launch (one workgroup per kv head): the kernel boundary
+// publishes the chunk records, so no counter, fence or L2 write-back is needed.
+template <int HDT, int GT>
+__global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
+  constexpr int GM = GT > 0 ? GT : kMaxGroup;
+  __shared__ float4 red[kThreads];
+  __shared__ float lstat[GM];
+  __shared__ float cw[GM * kMaxMerge];
+  const uint32_t lo = a.state->attn_lo;
+  const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
+  const uint32_t nrows = hi > lo ? hi - lo : 0;
+  const uint32_t nch = (nrows + kChunk - 1) / kChunk;
+  if (nch == 0) return;
+  merge_head<HDT, GT>(a, blockIdx.x, nch, cw, lstat, red);
 }
 
 }  // namespace
@@ -277,11 +380,20 @@ hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
       a.max_chunks == 0)
     return hipErrorInvalidValue;
   const dim3 grid(a.max_chunks, a.n_kv_heads);
-  switch (a.head_dim) {
-    case 64: hipLaunchKernelGGL(k_attn_decode<64>, grid, dim3(kThreads), 0, st, a); break;
-    case 128: hipLaunchKernelGGL(k_attn_decode<128>, grid, dim3(kThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_attn_decode<0>, grid, dim3(kThreads), 0, st, a); break;
-  }
+  const uint32_t G = a.n_heads / a.n_kv_heads;
+#define IFX_ATTN(HD_, G_)                                                                          \
+  do {                                                                                             \
+    hipLaunchKernelGGL((k_attn_decode<HD_, G_, kFusedMerge>), grid, dim3(kThreads), 0, st, a);    \
+    if (!kFusedMerge)                                                                              \
+      hipLaunchKernelGGL((k_attn_merge<HD_, G_>), dim3(a.n_kv_heads), dim3(kThreads), 0, st, a);  \
+  } while (0)
+  if (a.head_dim == 128 && G == 4) IFX_ATTN(128, 4);        // Llama-3 8B
+  else if (a.head_dim == 128 && G == 8) IFX_ATTN(128, 8);   // Llama-3 70B
+  else if (a.head_dim == 128 && G == 1) IFX_ATTN(128, 1);
+  else if (a.head_dim == 64 && G == 4) IFX_ATTN(64, 4);
+  else if (a.head_dim == 64 && G == 1) IFX_ATTN(64, 1);
+  else IFX_ATTN(0, 0);
+#undef IFX_ATTN
   return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@ struct KArgs {
   uint32_t ntiles[3];  // tiles per logical segment (paired: one logical segment)
   uint32_t rot[3];     // first-wave rotation per segment (balances small segments)
   uint32_t use_b;      // bit s: segment s decodes with the kernel's second type
+  uint32_t split;      // waves per row tile (1, 2, 4 or 8): they share its units
   int nseg;            // logical segments
   uint32_t cols, groups;
   const float* x;
@@ -74,6 +75,19 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <class T>
 __device__ __forceinline__ T ldg(const void* p) { return *(const T*)p; }
 
+// Selects acc[r] for lane r (r < kR) with a chain of selects; the asm
+// barriers keep the compiler from folding it back into a dynamic index of a
+// register array (which it would place in scratch memory).
+__device__ __forceinline__ float lane_acc(const float* acc, int lane) {
+  float v = acc[0];
+#pragma unroll
+  for (int r = 1; r < kR; r++) {
+    v = lane == r ? acc[r] : v;
+    asm("" : "+v"(v));
+  }
+  return v;
+}
+
 // Row r of tile `tile` of logical segment s, wave-uniform.  Paired launches
 // (gate/up) put rows 2t, 2t+1 of segment 0 in r = 0, 1 and the same rows of
 // segment 1 in r = 2, 3.
@@ -101,6 +115,13 @@ __device__ __forceinline__ RowRef row_of(const KArgs& a, int s, uint32_t tile, i
 // ---------------------------------------------------------------------------
 // Per-type fragments: the raw bytes of one unit (group g of the kR rows of a
 // tile) held in registers, and the decode + dot of that group with x.
+//   load_row(a, s, tile, g, r): issue the loads of row r, group g (always a
+//     real group of a real row: padding rows and lanes are clamped).
+//   dot_row(a, s, tile, g, valid, xv, xsa, xsb, acc, r): acc[r] += row r . x
+//     over group g; xv holds the group's 32 x values, xsa/xsb its two
+//     16-element sums.  Lanes with !valid and padding rows add nothing.
+// The main loop is free of branches so that the compiler can wait for exactly
+// the loads a row needs (a join in the control flow makes it wait for all).
 // ---------------------------------------------------------------------------
 
 // Q4_K (src/gguf/dequant.rs:133-161): element 32g+l is nibble (l&1) of
@@ -108,52 +129,44 @@ __device__ __forceinline__ RowRef row_of(const KArgs& a, int s, uint32_t tile, i
 struct FragQ4K {
   uint4 h[kR], q[kR];
   template <bool P>
-  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      // wave-uniform row base + 32-bit lane offset (scalar-base loads)
-      const uint8_t* row = rr.body + rr.row * ((a.groups / 8) * 144);
-      const uint32_t off = (g / 8) * 144;
-      h[r] = ldg<uint4>(row + off);
-      q[r] = ldg<uint4>(row + off + 16 + 16 * (g & 7));
-    }
+  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    // wave-uniform row base + 32-bit lane offset (scalar-base loads)
+    const uint8_t* row = rr.body + rr.row * ((a.groups / 8) * 144);
+    const uint32_t off = (g / 8) * 144;
+    h[r] = ldg<uint4>(row + off);
+    q[r] = ldg<uint4>(row + off + 16 + 16 * (g & 7));
   }
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float xsa, float xsb,
-                      float* acc) const {
-    const int sub = g & 7, j = sub & 3;
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t g, bool valid, const float4* xv, float xsa,
+                          float xsb, float* acc, int r) const {
+    const uint32_t sub = g & 7, j = sub & 3;
+    const uint4 hv = h[r];
+    // 6-bit scale / min of sub-block `sub` (get_scale_min_k4), selected without a branch
+    const uint32_t sc_lo = (hv.y >> (8 * j)) & 63u, mn_lo = (hv.z >> (8 * j)) & 63u;
+    const uint32_t sc_hi = ((hv.w >> (8 * j)) & 15u) | (((hv.y >> (8 * j + 6)) & 3u) << 4);
+    const uint32_t mn_hi = ((hv.w >> (8 * j + 4)) & 15u) | (((hv.z >> (8 * j + 6)) & 3u) << 4);
+    const uint32_t sc = sub < 4 ? sc_lo : sc_hi, mn = sub < 4 ? mn_lo : mn_hi;
+    const float d = h2f(hv.x), dmin = h2f(hv.x >> 16);
+    float s0 = 0.f, s1 = 0.f;
+    const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      if (!row_of<P>(a, s, tile, r).ok) continue;
-      uint32_t sc, mn;
-      if (sub < 4) {
-        sc = (h[r].y >> (8 * j)) & 63u;
-        mn = (h[r].z >> (8 * j)) & 63u;
-      } else {
-        sc = ((h[r].w >> (8 * j)) & 15u) | (((h[r].y >> (8 * j + 6)) & 3u) << 4);
-        mn = ((h[r].w >> (8 * j + 4)) & 15u) | (((h[r].z >> (8 * j + 6)) & 3u) << 4);
-      }
-      const float d = h2f(h[r].x), dmin = h2f(h[r].x >> 16);
-      float s0 = 0.f, s1 = 0.f;
-      const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-        // high nibbles stay in place (16 q): s1 is scaled by 1/16 below, exactly
-        const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);
-        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-        s0 = fmaf(cvtb(lo, 0), xa.x, s0);
-        s1 = fmaf(cvtb(hi, 0), xa.y, s1);
-        s0 = fmaf(cvtb(lo, 1), xa.z, s0);
-        s1 = fmaf(cvtb(hi, 1), xa.w, s1);
-        s0 = fmaf(cvtb(lo, 2), xb.x, s0);
-        s1 = fmaf(cvtb(hi, 2), xb.y, s1);
-        s0 = fmaf(cvtb(lo, 3), xb.z, s0);
-        s1 = fmaf(cvtb(hi, 3), xb.w, s1);
-      }
-      const float A = d * (float)sc, M = dmin * (float)mn;
-      acc[r] = fmaf(A, fmaf(s1, 0.0625f, s0), fmaf(-M, xsa + xsb, acc[r]));
+    for (int w = 0; w < 4; w++) {
+      // high nibbles stay in place (16 q): s1 is scaled by 1/16 below, exactly
+      const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);
+      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+      s0 = fmaf(cvtb(lo, 0), xa.x, s0);
+      s1 = fmaf(cvtb(hi, 0), xa.y, s1);
+      s0 = fmaf(cvtb(lo, 1), xa.z, s0);
+      s1 = fmaf(cvtb(hi, 1), xa.w, s1);
+      s0 = fmaf(cvtb(lo, 2), xb.x, s0);
+      s1 = fmaf(cvtb(hi, 2), xb.y, s1);
+      s0 = fmaf(cvtb(lo, 3), xb.z, s0);
+      s1 = fmaf(cvtb(hi, 3), xb.w, s1);
     }
+    const float A = d * (float)sc, M = dmin * (float)mn;
+    const float v = fmaf(A, fmaf(s1, 0.0625f, s0), -M * (xsa + xsb));
+    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
   }
 };
 
@@ -164,65 +177,59 @@ struct FragQ6K {
   uint2 qh[kR];
   uint32_t sd[kR];  // the group's two scale bytes (low 16 bits) | d bits (high 16)
   template <bool P>
-  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      const uint32_t nb = a.groups / 8;
-      const uint8_t* row = rr.body + rr.row * (nb * 208);
-      const uint8_t* rowd = rr.scal + rr.row * (nb * 2);
-      const uint32_t off = (g / 8) * 208, h = g & 7;
-      ql[r] = ldg<uint4>(row + off + 16 * h);
-      qh[r] = ldg<uint2>(row + off + 128 + 8 * h);
-      sd[r] = (uint32_t)ldg<uint16_t>(row + off + 192 + 2 * h) | ((uint32_t)ldg<uint16_t>(rowd + (g / 8) * 2) << 16);
-    }
+  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    const uint32_t nb = a.groups / 8;
+    const uint8_t* row = rr.body + rr.row * (nb * 208);
+    const uint8_t* rowd = rr.scal + rr.row * (nb * 2);
+    const uint32_t off = (g / 8) * 208, h = g & 7;
+    ql[r] = ldg<uint4>(row + off + 16 * h);
+    qh[r] = ldg<uint2>(row + off + 128 + 8 * h);
+    sd[r] = (uint32_t)ldg<uint16_t>(row + off + 192 + 2 * h) | ((uint32_t)ldg<uint16_t>(rowd + (g / 8) * 2) << 16);
   }
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t, bool valid, const float4* xv, float xsa,
+                          float xsb, float* acc, int r) const {
     const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+    const uint4 L = ql[r];
+    const uint2 H = qh[r];
+    // half a: elements 0..15 (L.x: 0-7, L.y: 8-15; high bits in H.x); half b: 16..31
+    const uint32_t ev[4] = {opaque((L.x & m4) | (H.x & m2)), opaque((L.y & m4) | ((H.x << 4) & m2)),
+                            opaque((L.z & m4) | (H.y & m2)), opaque((L.w & m4) | ((H.y << 4) & m2))};
+    const uint32_t ov[4] = {opaque(((L.x >> 4) & m4) | ((H.x >> 2) & m2)),
+                            opaque(((L.y >> 4) & m4) | ((H.x << 2) & m2)),
+                            opaque(((L.z >> 4) & m4) | ((H.y >> 2) & m2)),
+                            opaque(((L.w >> 4) & m4) | ((H.y << 2) & m2))};
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      if (!row_of<P>(a, s, tile, r).ok) continue;
-      const uint4 L = ql[r];
-      const uint2 H = qh[r];
-      // half a: elements 0..15 (L.x: 0-7, L.y: 8-15; high bits in H.x); half b: 16..31
-      const uint32_t ev[4] = {opaque((L.x & m4) | (H.x & m2)), opaque((L.y & m4) | ((H.x << 4) & m2)),
-                              opaque((L.z & m4) | (H.y & m2)), opaque((L.w & m4) | ((H.y << 4) & m2))};
-      const uint32_t ov[4] = {opaque(((L.x >> 4) & m4) | ((H.x >> 2) & m2)),
-                              opaque(((L.y >> 4) & m4) | ((H.x << 2) & m2)),
-                              opaque(((L.z >> 4) & m4) | ((H.y >> 2) & m2)),
-                              opaque(((L.w >> 4) & m4) | ((H.y << 2) & m2))};
-      float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-#pragma unroll
-      for (int w = 0; w < 2; w++) {
-        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-        a0 = fmaf(cvtb(ev[w], 0), xa.x, a0);
-        a1 = fmaf(cvtb(ov[w], 0), xa.y, a1);
-        a0 = fmaf(cvtb(ev[w], 1), xa.z, a0);
-        a1 = fmaf(cvtb(ov[w], 1), xa.w, a1);
-        a0 = fmaf(cvtb(ev[w], 2), xb.x, a0);
-        a1 = fmaf(cvtb(ov[w], 2), xb.y, a1);
-        a0 = fmaf(cvtb(ev[w], 3), xb.z, a0);
-        a1 = fmaf(cvtb(ov[w], 3), xb.w, a1);
-      }
-#pragma unroll
-      for (int w = 2; w < 4; w++) {
-        const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-        b0 = fmaf(cvtb(ev[w], 0), xa.x, b0);
-        b1 = fmaf(cvtb(ov[w], 0), xa.y, b1);
-        b0 = fmaf(cvtb(ev[w], 1), xa.z, b0);
-        b1 = fmaf(cvtb(ov[w], 1), xa.w, b1);
-        b0 = fmaf(cvtb(ev[w], 2), xb.x, b0);
-        b1 = fmaf(cvtb(ov[w], 2), xb.y, b1);
-        b0 = fmaf(cvtb(ev[w], 3), xb.z, b0);
-        b1 = fmaf(cvtb(ov[w], 3), xb.w, b1);
-      }
-      const float d = h2f(sd[r] >> 16);
-      const float sa = (float)(sd[r] & 0xffu), sb = (float)((sd[r] >> 8) & 0xffu);
-      const float ta = fmaf(-32.f, xsa, a0 + a1), tb = fmaf(-32.f, xsb, b0 + b1);
-      acc[r] = fmaf(d, fmaf(sa, ta, sb * tb), acc[r]);
+    for (int w = 0; w < 2; w++) {
+      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+      a0 = fmaf(cvtb(ev[w], 0), xa.x, a0);
+      a1 = fmaf(cvtb(ov[w], 0), xa.y, a1);
+      a0 = fmaf(cvtb(ev[w], 1), xa.z, a0);
+      a1 = fmaf(cvtb(ov[w], 1), xa.w, a1);
+      a0 = fmaf(cvtb(ev[w], 2), xb.x, a0);
+      a1 = fmaf(cvtb(ov[w], 2), xb.y, a1);
+      a0 = fmaf(cvtb(ev[w], 3), xb.z, a0);
+      a1 = fmaf(cvtb(ov[w], 3), xb.w, a1);
     }
+#pragma unroll
+    for (int w = 2; w < 4; w++) {
+      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
+      b0 = fmaf(cvtb(ev[w], 0), xa.x, b0);
+      b1 = fmaf(cvtb(ov[w], 0), xa.y, b1);
+      b0 = fmaf(cvtb(ev[w], 1), xa.z, b0);
+      b1 = fmaf(cvtb(ov[w], 1), xa.w, b1);
+      b0 = fmaf(cvtb(ev[w], 2), xb.x, b0);
+      b1 = fmaf(cvtb(ov[w], 2), xb.y, b1);
+      b0 = fmaf(cvtb(ev[w], 3), xb.z, b0);
+      b1 = fmaf(cvtb(ov[w], 3), xb.w, b1);
+    }
+    const float d = h2f(sd[r] >> 16);
+    const float sa = (float)(sd[r] & 0xffu), sb = (float)((sd[r] >> 8) & 0xffu);
+    const float ta = fmaf(-32.f, xsa, a0 + a1), tb = fmaf(-32.f, xsb, b0 + b1);
+    const float v = d * fmaf(sa, ta, sb * tb);
+    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
   }
 };
 
@@ -231,37 +238,31 @@ struct FragQ80 {
   uint4 qa[kR], qb[kR];
   uint32_t d[kR];
   template <bool P>
-  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      const uint8_t* row = rr.body + rr.row * (a.groups * 32);
-      qa[r] = ldg<uint4>(row + g * 32);
-      qb[r] = ldg<uint4>(row + g * 32 + 16);
-      d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
-    }
+  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    const uint8_t* row = rr.body + rr.row * (a.groups * 32);
+    qa[r] = ldg<uint4>(row + g * 32);
+    qb[r] = ldg<uint4>(row + g * 32 + 16);
+    d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
   }
   // q x = (u - 128) x with u = q ^ 0x80 unsigned: one convert per byte, the
   // -128 sum(x) term from the staged group sums
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t, bool valid, const float4* xv, float xsa,
+                          float xsb, float* acc, int r) const {
+    const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      if (!row_of<P>(a, s, tile, r).ok) continue;
-      const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int w = 0; w < 8; w++) {
-        const float4 xa = xv[w];
-        const uint32_t u = opaque(qw[w] ^ 0x80808080u);
-        s0 = fmaf(cvtb(u, 0), xa.x, s0);
-        s1 = fmaf(cvtb(u, 1), xa.y, s1);
-        s0 = fmaf(cvtb(u, 2), xa.z, s0);
-        s1 = fmaf(cvtb(u, 3), xa.w, s1);
-      }
-      acc[r] = fmaf(h2f(d[r]), fmaf(-128.f, xsa + xsb, s0 + s1), acc[r]);
+    for (int w = 0; w < 8; w++) {
+      const float4 xa = xv[w];
+      const uint32_t u = opaque(qw[w] ^ 0x80808080u);
+      s0 = fmaf(cvtb(u, 0), xa.x, s0);
+      s1 = fmaf(cvtb(u, 1), xa.y, s1);
+      s0 = fmaf(cvtb(u, 2), xa.z, s0);
+      s1 = fmaf(cvtb(u, 3), xa.w, s1);
     }
+    const float v = h2f(d[r]) * fmaf(-128.f, xsa + xsb, s0 + s1);
+    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
   }
 };
 
@@ -270,37 +271,31 @@ struct FragQ40 {
   uint4 q[kR];
   uint32_t d[kR];
   template <bool P>
-  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      q[r] = ldg<uint4>(rr.body + rr.row * (a.groups * 16) + g * 16);
-      d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
-    }
+  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    q[r] = ldg<uint4>(rr.body + rr.row * (a.groups * 16) + g * 16);
+    d[r] = ldg<uint16_t>(rr.scal + rr.row * (a.groups * 2) + g * 2);
   }
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t, bool valid, const float4* xv, float xsa,
+                          float xsb, float* acc, int r) const {
+    const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      if (!row_of<P>(a, s, tile, r).ok) continue;
-      const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-        const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);  // hi: 16 q
-        const float4 xa = xv[w], xb = xv[4 + w];
-        s0 = fmaf(cvtb(lo, 0), xa.x, s0);
-        s0 = fmaf(cvtb(lo, 1), xa.y, s0);
-        s0 = fmaf(cvtb(lo, 2), xa.z, s0);
-        s0 = fmaf(cvtb(lo, 3), xa.w, s0);
-        s1 = fmaf(cvtb(hi, 0), xb.x, s1);
-        s1 = fmaf(cvtb(hi, 1), xb.y, s1);
-        s1 = fmaf(cvtb(hi, 2), xb.z, s1);
-        s1 = fmaf(cvtb(hi, 3), xb.w, s1);
-      }
-      acc[r] = fmaf(h2f(d[r]), fmaf(-8.f, xsa + xsb, fmaf(s1, 0.0625f, s0)), acc[r]);
+    for (int w = 0; w < 4; w++) {
+      const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);  // hi: 16 q
+      const float4 xa = xv[w], xb = xv[4 + w];
+      s0 = fmaf(cvtb(lo, 0), xa.x, s0);
+      s0 = fmaf(cvtb(lo, 1), xa.y, s0);
+      s0 = fmaf(cvtb(lo, 2), xa.z, s0);
+      s0 = fmaf(cvtb(lo, 3), xa.w, s0);
+      s1 = fmaf(cvtb(hi, 0), xb.x, s1);
+      s1 = fmaf(cvtb(hi, 1), xb.y, s1);
+      s1 = fmaf(cvtb(hi, 2), xb.z, s1);
+      s1 = fmaf(cvtb(hi, 3), xb.w, s1);
     }
+    const float v = h2f(d[r]) * fmaf(-8.f, xsa + xsb, fmaf(s1, 0.0625f, s0));
+    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
   }
 };
 
@@ -309,99 +304,85 @@ struct FragQ8K {
   uint4 qa[kR], qb[kR];
   uint32_t sc[kR], dd[kR];
   template <bool P>
-  __device__ void load(const KArgs& a, int s, uint32_t tile, uint32_t g) {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      const uint32_t nb = a.groups / 8, sub = g & 7;
-      const uint8_t* blk = rr.body + rr.row * (nb * 288) + (g / 8) * 288;
-      sc[r] = ldg<uint32_t>(blk + 4 * sub);
-      qa[r] = ldg<uint4>(blk + 32 + 32 * sub);
-      qb[r] = ldg<uint4>(blk + 48 + 32 * sub);
-      dd[r] = ldg<uint32_t>(rr.scal + rr.row * (nb * 4) + (g / 8) * 4);
-    }
+  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    const uint32_t nb = a.groups / 8, sub = g & 7;
+    const uint8_t* blk = rr.body + rr.row * (nb * 288) + (g / 8) * 288;
+    sc[r] = ldg<uint32_t>(blk + 4 * sub);
+    qa[r] = ldg<uint4>(blk + 32 + 32 * sub);
+    qb[r] = ldg<uint4>(blk + 48 + 32 * sub);
+    dd[r] = ldg<uint32_t>(rr.scal + rr.row * (nb * 4) + (g / 8) * 4);
   }
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t, const float4* xv, float xsa, float xsb,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t, bool valid, const float4* xv, float xsa,
+                          float xsb, float* acc, int r) const {
+    const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+    const float d = h2f(dd[r]), dmin = h2f(dd[r] >> 16);
+    float tot = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      if (!row_of<P>(a, s, tile, r).ok) continue;
-      const uint32_t qw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
-      const float d = h2f(dd[r]), dmin = h2f(dd[r] >> 16);
-      float tot = 0.f;
+    for (int k = 0; k < 4; k++) {  // sub-blocks of 8 elements share one scale byte
+      float acc8 = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; k++) {  // sub-blocks of 8 elements share one scale byte
-        float acc8 = 0.f;
-#pragma unroll
-        for (int w = 0; w < 2; w++) {
-          const int v = (int)qw[2 * k + w];
-          const float4 x4 = xv[2 * k + w];
-          acc8 = fmaf(sbyte(v, 0), x4.x, acc8);
-          acc8 = fmaf(sbyte(v, 1), x4.y, acc8);
-          acc8 = fmaf(sbyte(v, 2), x4.z, acc8);
-          acc8 = fmaf(sbyte(v, 3), x4.w, acc8);
-        }
-        tot = fmaf(d * cvtb(sc[r], k), acc8, tot);
+      for (int w = 0; w < 2; w++) {
+        const int v = (int)qw[2 * k + w];
+        const float4 x4 = xv[2 * k + w];
+        acc8 = fmaf(sbyte(v, 0), x4.x, acc8);
+        acc8 = fmaf(sbyte(v, 1), x4.y, acc8);
+        acc8 = fmaf(sbyte(v, 2), x4.z, acc8);
+        acc8 = fmaf(sbyte(v, 3), x4.w, acc8);
       }
-      acc[r] += fmaf(-dmin, xsa + xsb, tot);
+      tot = fmaf(d * cvtb(sc[r], k), acc8, tot);
     }
+    const float v = fmaf(-dmin, xsa + xsb, tot);
+    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
   }
 };
 
 // F32 / F16 rows of whole groups: read at use, no prefetch (toy models, tests).
 struct FragF32 {
   template <bool P>
-  __device__ void load(const KArgs&, int, uint32_t, uint32_t) {}
+  __device__ void load_row(const KArgs&, int, uint32_t, uint32_t, int) {}
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float, float,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t g, bool valid, const float4* xv, float,
+                          float, float* acc, int r) const {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    const float4* w4 = (const float4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 8;
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      if (!rr.ok) continue;
-      const float4* w4 = (const float4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 8;
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float4 w = w4[i], x = xv[i];
-        s0 = fmaf(w.x, x.x, s0);
-        s1 = fmaf(w.y, x.y, s1);
-        s0 = fmaf(w.z, x.z, s0);
-        s1 = fmaf(w.w, x.w, s1);
-      }
-      acc[r] += s0 + s1;
+    for (int i = 0; i < 8; i++) {
+      const float4 w = w4[i], x = xv[i];
+      s0 = fmaf(w.x, x.x, s0);
+      s1 = fmaf(w.y, x.y, s1);
+      s0 = fmaf(w.z, x.z, s0);
+      s1 = fmaf(w.w, x.w, s1);
     }
+    acc[r] += (valid && rr.ok) ? s0 + s1 : 0.f;
   }
 };
 
 struct FragF16 {
   template <bool P>
-  __device__ void load(const KArgs&, int, uint32_t, uint32_t) {}
+  __device__ void load_row(const KArgs&, int, uint32_t, uint32_t, int) {}
   template <bool P>
-  __device__ void dot(const KArgs& a, int s, uint32_t tile, uint32_t g, const float4* xv, float, float,
-                      float* acc) const {
+  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t g, bool valid, const float4* xv, float,
+                          float, float* acc, int r) const {
+    const RowRef rr = row_of<P>(a, s, tile, r);
+    const uint4* w4 = (const uint4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 4;
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<P>(a, s, tile, r);
-      if (!rr.ok) continue;
-      const uint4* w4 = (const uint4*)rr.body + (rr.row * (uint64_t)a.groups + g) * 4;
-      float s0 = 0.f, s1 = 0.f;
+    for (int i = 0; i < 4; i++) {
+      const uint4 w = w4[i];
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint4 w = w4[i];
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-          const float4 x = xv[2 * i + k];
-          s0 = fmaf(h2f(ww[2 * k]), x.x, s0);
-          s1 = fmaf(h2f(ww[2 * k] >> 16), x.y, s1);
-          s0 = fmaf(h2f(ww[2 * k + 1]), x.z, s0);
-          s1 = fmaf(h2f(ww[2 * k + 1] >> 16), x.w, s1);
-        }
+      for (int k = 0; k < 2; k++) {
+        const float4 x = xv[2 * i + k];
+        s0 = fmaf(h2f(ww[2 * k]), x.x, s0);
+        s1 = fmaf(h2f(ww[2 * k] >> 16), x.y, s1);
+        s0 = fmaf(h2f(ww[2 * k + 1]), x.z, s0);
+        s1 = fmaf(h2f(ww[2 * k + 1] >> 16), x.w, s1);
       }
-      acc[r] += s0 + s1;
     }
+    acc[r] += (valid && rr.ok) ? s0 + s1 : 0.f;
   }
 };
 
@@ -414,7 +395,7 @@ struct EpiStore {
   __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
     if (lane < kR) {
       const RowRef rr = row_of<false>(a, s, tile, lane);
-      if (rr.ok) y[seg_out[s] + rr.row] = acc[lane];
+      if (rr.ok) y[seg_out[s] + rr.row] = lane_acc(acc, lane);
     }
   }
   __device__ void finish(Wave&, int) const {}
@@ -427,7 +408,7 @@ struct EpiResidual {
   __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
     if (lane < kR) {
       const RowRef rr = row_of<false>(a, s, tile, lane);
-      if (rr.ok) h[rr.row] = acc[lane] + h[rr.row];
+      if (rr.ok) h[rr.row] = lane_acc(acc, lane) + h[rr.row];
     }
   }
   __device__ void finish(Wave&, int) const {}
@@ -443,12 +424,12 @@ struct EpiQkv {
     const RowRef rr = row_of<false>(a, s, tile, lane);
     if (!rr.ok) return;
     const uint32_t r = (uint32_t)rr.row;
-    float v = acc[lane];
+    float v = lane_acc(acc, lane);
     if (s < 2) {
       const uint32_t i = r % e.head_dim;
       if (i < e.rope_dim) {
         const float2 cs = e.rope_cs[(uint64_t)e.state->rope_pos * (e.rope_dim / 2) + i / 2];
-        const float other = acc[lane ^ 1];
+        const float other = lane_acc(acc, lane ^ 1);
         v = (i & 1) ? (other * cs.y + v * cs.x) : (v * cs.x - other * cs.y);
       }
     }
@@ -473,7 +454,7 @@ struct EpiSwiglu {
     if (lane >= H) return;
     const RowRef rr = row_of<true>(a, 0, tile, lane);
     if (!rr.ok) return;
-    const float g = acc[lane], u = acc[lane + H];
+    const float g = lane_acc(acc, lane), u = lane_acc(acc, lane + H);
     float c = fminf(fmaxf(g, -80.f), 80.f);
     if (g != g) c = g;
     const float sig = 1.0f / (1.0f + expf(-c));
@@ -515,38 +496,68 @@ struct EpiLogits {
   }
 };
 
-// The units of one logical segment owned by this wave: tiles first, first+W,
-// ..., each swept in NG group steps.  `f` arrives holding the loads of the
-// first unit; the loads of each next unit are issued as soon as the current
-// one is decoded.  Latency is hidden by the other waves of the CU (no second
-// register buffer: keeps the kernel at four waves per SIMD).
+// The row tiles of one logical segment owned by this wave's tile group
+// (a.split waves of one workgroup): tiles first, first+TG, ..., `iters` of them
+// (the same count for every wave of the workgroup, so that the LDS reduction
+// of a split tile can use workgroup barriers).  Wave j of the group takes the
+// units j, j+split, ... of each tile.  `f` arrives holding the loads of the
+// first unit.  As soon as row r of the current unit is decoded, the loads of
+// row r of the next unit are issued into the same registers, so the wave keeps
+// loads in flight while it computes (a second register buffer would cost
+// occupancy).  Past the wave's last unit the loads repeat a real unit.
 template <class Frag, class Epi>
 __device__ __forceinline__ void run_segment(const KArgs& a, const Epi& epi, typename Epi::Wave& ws, int s,
-                                            uint32_t first, uint32_t W, Frag& f, const float* xl,
-                                            const float* xs, int lane) {
+                                            uint32_t first, uint32_t TG, uint32_t iters, uint32_t j, Frag& f,
+                                            const float* xl, const float* xs, float* part, int lane, int wave) {
   constexpr bool P = Epi::kPaired;
-  const uint32_t NG = (a.groups + 63) / 64;
-  for (uint32_t tile = first; tile < a.ntiles[s]; tile += W) {
-    float acc[kR] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t it = 0; it < NG; it++) {
-      const uint32_t g = lane + 64 * it;
-      if (g < a.groups) {
-        const float4* xv4 = (const float4*)(xl + kGroupStride * g);
+  const uint32_t NG = (a.groups + 63) / 64, S = a.split;
+  for (uint32_t k = 0; k < iters; k++) {
+    const uint32_t tile = first + k * TG;
+    const bool live = tile < a.ntiles[s];  // uniform over the wave
+    float acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; r++) acc[r] = 0.f;
+    if (live) {
+      for (uint32_t it = j; it < NG; it += S) {
+        const uint32_t g = lane + 64 * it, gc = min(g, a.groups - 1);
+        uint32_t nt = tile, ni = it + S;
+        if (ni >= NG) {
+          ni = j;
+          nt += TG;
+        }
+        if (nt >= a.ntiles[s]) nt = tile;  // uniform select: no branch around the loads
+        const uint32_t ng = min(lane + 64 * ni, a.groups - 1);
+        const float4* xv4 = (const float4*)(xl + kGroupStride * gc);
         float4 xv[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) xv[i] = xv4[i];
-        f.template dot<P>(a, s, tile, g, xv, xs[2 * g], xs[2 * g + 1], acc);
+        const float xsa = xs[2 * gc], xsb = xs[2 * gc + 1];
+#pragma unroll
+        for (int r = 0; r < kR; r++) {
+          f.template dot_row<P>(a, s, tile, gc, g < a.groups, xv, xsa, xsb, acc, r);
+          f.template load_row<P>(a, s, nt, ng, r);
+        }
       }
-      uint32_t nt = tile, ni = it + 1;
-      if (ni == NG) {
-        ni = 0;
-        nt += W;
-      }
-      if (nt < a.ntiles[s]) f.template load<P>(a, s, nt, min(lane + 64 * ni, a.groups - 1));
     }
 #pragma unroll
     for (int r = 0; r < kR; r++) acc[r] = wave_sum(acc[r]);
-    epi.apply(ws, a, s, tile, acc, lane);
+    if (S > 1) {
+      // partial sums of the group's waves through LDS (double-buffered: one barrier per tile)
+      float* pb = part + (k & 1) * kWaves * kR;
+      if (lane < kR) pb[wave * kR + lane] = lane_acc(acc, lane);
+      __syncthreads();
+      if (j == 0 && live) {
+#pragma unroll
+        for (int r = 0; r < kR; r++) {
+          float v = 0.f;
+          for (uint32_t i = 0; i < S; i++) v += pb[(wave + i) * kR + r];
+          acc[r] = v;
+        }
+        epi.apply(ws, a, s, tile, acc, lane);
+      }
+    } else if (live) {
+      epi.apply(ws, a, s, tile, acc, lane);
+    }
   }
 }
 
@@ -652,35 +663,55 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
   float* xs = lds + (size_t)a.groups * kGroupStride;  // [cols/16]
   float* wl = xs + ((a.cols / 16 + 3) & ~3u);         // [cols] norm weights (norm launches), 16-B aligned
   __shared__ float red[kWaves];
+  __shared__ float part[2 * kWaves * kR];
   // the wave index is uniform: tile and row bookkeeping stays in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t W = gridDim.x * kWaves, wid = blockIdx.x * kWaves + wave;
+  // tile groups of a.split waves; TG groups in the grid
+  const uint32_t S = a.split, GPB = kWaves / S, TG = gridDim.x * GPB;
+  const uint32_t tg = blockIdx.x * GPB + wave / S, j = wave % S;
   typename Epi::Wave ws;
+  // tiles per group of this workgroup for segment s: the count of its busiest group
+  auto block_iters = [&](int s) -> uint32_t {
+    uint32_t n = 0;
+    for (uint32_t q = 0; q < GPB; q++) {
+      const uint32_t f0 = (blockIdx.x * GPB + q + TG - a.rot[s]) % TG;
+      if (f0 < a.ntiles[s]) n = max(n, (a.ntiles[s] - 1 - f0) / TG + 1);
+    }
+    return n;
+  };
+  const uint32_t NG = (a.groups + 63) / 64;
+  const uint32_t g0 = min(lane + 64 * min(j, NG - 1), a.groups - 1);
 
   // first unit of segment 0 (always FragA) in flight while x is staged
   constexpr bool P = Epi::kPaired;
   constexpr bool kMixed = !std::is_same<FragA, FragB>::value;
   {
-    const uint32_t first = (wid + W - a.rot[0]) % W;
+    const uint32_t first = (tg + TG - a.rot[0]) % TG;
     FragA f;
     // lanes past the last group load a real group (unconditional loads keep
     // the fragments' live ranges short); their values are never used
-    if (first < a.ntiles[0]) f.template load<P>(a, 0, first, min((uint32_t)lane, a.groups - 1));
+    if (first < a.ntiles[0]) {
+#pragma unroll
+      for (int r = 0; r < kR; r++) f.template load_row<P>(a, 0, first, g0, r);
+    }
     stage_x(a, xl, xs, wl, red, tid, lane, wave);
-    if (first < a.ntiles[0]) run_segment<FragA, Epi>(a, epi, ws, 0, first, W, f, xl, xs, lane);
+    run_segment<FragA, Epi>(a, epi, ws, 0, first, TG, block_iters(0), j, f, xl, xs, part, lane, wave);
   }
   for (int s = 1; s < a.nseg; s++) {
-    const uint32_t first = (wid + W - a.rot[s]) % W;
-    if (first >= a.ntiles[s]) continue;
-    const uint32_t g0 = min((uint32_t)lane, a.groups - 1);
+    const uint32_t first = (tg + TG - a.rot[s]) % TG;
+    const uint32_t iters = block_iters(s);
+    if (iters == 0) continue;
+    const uint32_t t0 = first < a.ntiles[s] ? first : 0;
     if (kMixed && ((a.use_b >> s) & 1u)) {
       FragB f;
-      f.template load<P>(a, s, first, g0);
-      run_segment<FragB, Epi>(a, epi, ws, s, first, W, f, xl, xs, lane);
+#pragma unroll
+      for (int r = 0; r < kR; r++) f.template load_row<P>(a, s, t0, g0, r);
+      run_segment<FragB, Epi>(a, epi, ws, s, first, TG, iters, j, f, xl, xs, part, lane, wave);
     } else {
       FragA f;
-      f.template load<P>(a, s, first, g0);
-      run_segment<FragA, Epi>(a, epi, ws, s, first, W, f, xl, xs, lane);
+#pragma unroll
+      for (int r = 0; r < kR; r++) f.template load_row<P>(a, s, t0, g0, r);
+      run_segment<FragA, Epi>(a, epi, ws, s, first, TG, iters, j, f, xl, xs, part, lane, wave);
     }
   }
   epi.finish(ws, lane);
@@ -790,13 +821,21 @@ hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   for (int s = 0; s < a.nseg; s++) total += a.ntiles[s];
   if (total == 0) return hipSuccess;
   // persistent grid: as many workgroups as fit per CU (LDS-bound for long
-  // rows), never more waves than tiles
+  // rows).  Long rows (at least 4 units) with fewer row tiles than resident
+  // waves share each tile's units among `split` waves (the 8B down projection:
+  // 1024 tiles of 7 units).
   const uint32_t per_cu = (uint32_t)std::max<size_t>(1, std::min<size_t>(kBlocksPerCu, (160 * 1024) / lds));
-  const uint32_t blocks = std::min<uint32_t>((total + kWaves - 1) / kWaves, per_cu * device_cu_count());
-  const uint32_t W = blocks * kWaves;
+  const uint32_t resident = per_cu * device_cu_count() * kWaves;
+  const uint32_t NG = (a.groups + 63) / 64;
+  uint32_t split = 1;
+  if (!generic && NG >= 4)
+    while (split < (uint32_t)kWaves && split < NG && total * split < resident) split *= 2;
+  a.split = split;
+  const uint32_t blocks = std::min<uint32_t>((total * split + kWaves - 1) / kWaves, per_cu * device_cu_count());
+  const uint32_t TG = blocks * (kWaves / split);
   uint32_t acc = 0;
   for (int s = 0; s < a.nseg; s++) {
-    a.rot[s] = acc % W;
+    a.rot[s] = acc % TG;
     acc += a.ntiles[s];
   }
   if (generic) {

@@ -119,7 +119,7 @@ def _gemv_check(t, rows, cols, rng, x_scale=1.0, tol=1e-5):
 
 
 @pytest.mark.parametrize("t", ALL)
-@pytest.mark.parametrize("shape", [(64, 256), (1024, 4096), (36, 2048), (4, 14336)])
+@pytest.mark.parametrize("shape", [(64, 256), (1024, 4096), (36, 2048), (4, 14336), (1002, 4096), (6, 16384)])
 def test_gemv_vs_oracle(t, shape):
     rng = np.random.default_rng(300 + t + shape[0])
     _gemv_check(t, shape[0], shape[1], rng)
