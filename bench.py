@@ -9,7 +9,12 @@ a 2048-token KV context filled by a GPU prefill of 2048 seeded token ids, then
 in HBM when timing starts).
 
 Prints ONE JSON line (metric, value, roofline of the dominant kernel measured
-with HIP events, cpu_baseline of the CPU oracle on a bounded sample).
+with HIP events over back-to-back launches, cpu_baseline of the CPU oracle on a
+bounded sample).
+
+Profiling aids: --no-graph launches each step's kernels directly instead of
+replaying the captured step graph (for kernel tracers); --copy-probe only runs
+a device-to-device copy of known size, the calibration for HBM byte counters.
 """
 from __future__ import annotations
 
@@ -31,8 +36,11 @@ CTX = 2048
 METRIC = "decode tok/s, 8B Q4_K_M bs=1, 1×MI355X; % of HBM-BW roofline"
 KCLASS = ["embed", "qkv_gemv", "attention", "attn_output_gemv", "ffn_gate_up_gemv", "ffn_down_gemv",
           "output_head_gemv", "finalize"]
-KERNEL_NAMES = {4: "k_gemv<EpiSwiglu>", 5: "k_gemv<EpiResidual>", 6: "k_gemv<EpiLogits>",
-                1: "k_gemv<EpiQkv>", 2: "k_attn_decode"}
+KERNEL_NAMES = {1: "k_gemv<EpiQkv, FragQ4K, FragQ6K>", 2: "k_attn_decode<128, 4> + k_attn_merge<128, 4>",
+                3: "k_gemv<EpiResidual, FragQ4K, FragQ4K>", 4: "k_gemv<EpiSwiglu, FragQ4K, FragQ4K>",
+                5: "k_gemv<EpiResidual, FragQ6K, FragQ6K>", 6: "k_gemv<EpiLogits, FragQ6K, FragQ6K>"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+COPY_PROBE_BYTES = 256 << 20
 
 
 def log(msg):
@@ -49,7 +57,44 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=1, help="oracle decode steps for cpu_baseline (0: skip)")
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="direct launches instead of the step graph")
+    ap.add_argument("--copy-probe", action="store_true", help="only a d2d copy of known size (counter calibration)")
     return ap.parse_args()
+
+
+def copy_probe():
+    """8 launches of a plain copy kernel over COPY_PROBE_BYTES (an F32 tensor
+    "dequantized" to f32: read N*4 bytes, write N*4 bytes).  Under a byte
+    counter, the reading per launch against the known size is the counter's
+    scale factor."""
+    from inferox_amd import _native
+    from inferox_amd._native import check
+    L = _native.lib()
+    n = COPY_PROBE_BYTES // 4
+    host = np.zeros(n, np.float32)
+    t = C.c_void_p()
+    check(L.ifx_tensor_upload(0, host.ctypes.data_as(C.c_void_p), COPY_PROBE_BYTES, 1, n, C.byref(t)), "upload")
+    out = C.c_void_p()
+    check(L.ifx_malloc(C.byref(out), COPY_PROBE_BYTES), "malloc")
+    for _ in range(8):
+        check(L.ifx_tensor_dequant(t, out, None), "copy")
+    check(L.ifx_stream_synchronize(None), "sync")
+    L.ifx_free(out)
+    L.ifx_tensor_free(t)
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "launches": 8, "kernel": "k_dequant_dev"}), flush=True)
+
+
+def traffic_for(kclass):
+    """HBM bytes per launch of a kernel class from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor
+    measured on a copy of known size), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        k = t["kernels"][kclass]
+        return int(k["fetch_kib"] * 1024 * t["fetch_factor"] + k["write_kib"] * 1024 * t["write_factor"])
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
 
 
 def bytes_per_token(spec, ctx_avg):
@@ -91,6 +136,11 @@ def cpu_baseline(model_path, kv_k, kv_v, ctx, token, n_steps):
 
 def main():
     args = parse()
+    if args.no_graph:
+        os.environ["IFX_NO_GRAPH"] = "1"  # read by the library at the first step
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the token loop runs on a single MI355X; "
                           "multi-GPU sharding is described in DESIGN.md but not built", "n_gpus": args.gpus}))
@@ -132,18 +182,20 @@ def main():
     out = np.zeros(max(K, W, 1), np.uint32)
     check(L.ifx_decode_greedy(sess, 1, W, out.ctypes.data_as(C.c_void_p)), "warmup")
     check(L.ifx_session_clear(sess), "clear")
-    ids = synth.token_ids(args.ctx, vocab, seed=2048)
-    t0 = time.perf_counter()
-    check(L.ifx_prefill(sess, ids.ctypes.data_as(C.c_void_p), ids.size, None), "prefill")
-    prefill_s = time.perf_counter() - t0
     ms = C.c_float()
-    L.ifx_session_last_elapsed_ms(sess, C.byref(ms))
-    log(f"prefill of {args.ctx} tokens: {prefill_s:.2f} s ({args.ctx / prefill_s:.0f} tok/s)")
-
-    # the first generated token = greedy pick of the last prefill row (Model::generate)
-    first = C.c_uint32()
-    check(L.ifx_session_last_token(sess, C.byref(first)), "last_token")
-    start_tok = first.value
+    prefill_s = None
+    if args.ctx > 0:
+        ids = synth.token_ids(args.ctx, vocab, seed=2048)
+        t0 = time.perf_counter()
+        check(L.ifx_prefill(sess, ids.ctypes.data_as(C.c_void_p), ids.size, None), "prefill")
+        prefill_s = time.perf_counter() - t0
+        log(f"prefill of {args.ctx} tokens: {prefill_s:.2f} s ({args.ctx / prefill_s:.0f} tok/s)")
+        # the first generated token = greedy pick of the last prefill row (Model::generate)
+        first = C.c_uint32()
+        check(L.ifx_session_last_token(sess, C.byref(first)), "last_token")
+        start_tok = first.value
+    else:  # --ctx 0: decode from an empty cache (short runs under counters)
+        start_tok = 1
     kv_len = C.c_uint64()
     L.ifx_session_len(sess, C.byref(kv_len))
     assert kv_len.value == args.ctx
@@ -171,7 +223,7 @@ def main():
     b_tok = w_bytes + kv_bytes
     frac_tok = tok_s * b_tok / HBM_PEAK
 
-    # ---- dominant kernel: HIP events around every kernel of a decode step ----
+    # ---- dominant kernel: HIP events around back-to-back launches of each kernel class ----
     roofline = None
     prof = {}
     if not args.no_profile:
@@ -188,14 +240,14 @@ def main():
         alg = wbytes[dom] + extra
         achieved = alg / (avg[dom] * 1e-3)
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic_for(KCLASS[dom]),
                     "kernel": KERNEL_NAMES.get(dom, KCLASS[dom]), "kernel_class": KCLASS[dom],
                     "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2)}
         prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "launches_per_step": int(launches[k]),
                             "weight_bytes": int(wbytes[k]),
                             "GB_s": round(wbytes[k] / (avg[k] * 1e-3) / 1e9, 1) if avg[k] > 0 and wbytes[k] else None}
                 for k in range(8)}
-        log("per-kernel (events): " + json.dumps(prof))
+        log("per-kernel (back-to-back launches): " + json.dumps(prof))
         log(f"sum of kernel time per step: {sum(per_step.values()):.3f} ms vs {wall / K * 1e3:.3f} ms per step")
 
     cpu = None
@@ -223,7 +275,7 @@ def main():
         "roofline_tok": {"bytes_per_token": int(b_tok), "weight_bytes": int(w_bytes), "kv_bytes_f16": int(kv_bytes),
                          "roofline_tok_s": round(HBM_PEAK / b_tok, 1), "frac": round(frac_tok, 4)},
         "device_tok_s": round(K / dev_s, 2),
-        "prefill_tok_s": round(args.ctx / prefill_s, 1),
+        "prefill_tok_s": round(args.ctx / prefill_s, 1) if prefill_s else None,
         "kernels": prof or None,
     }
     print(json.dumps(line), flush=True)

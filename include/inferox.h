@@ -146,14 +146,17 @@ int ifx_session_last_token(ifx_session* s, uint32_t* token);
 int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms);
 
 /* Measurement hook (no reference counterpart; the reference has no timers):
- * n_steps greedy decode steps launched directly with a HIP event pair around
- * every kernel on the session stream.  Arrays of 8, one per kernel class:
- * 0 embedding gather, 1 QKV GEMV (+RMSNorm, RoPE, KV append), 2 attention,
- * 3 attn_output GEMV (+residual), 4 ffn gate/up GEMV (+RMSNorm, SwiGLU),
- * 5 ffn_down GEMV (+residual), 6 output head GEMV (+RMSNorm, argmax),
- * 7 finalize.  avg_ms: mean duration per launch; launches: per step;
- * bytes: stored weight bytes each launch streams (attention: the f32 K/V
- * rows it reads).  len grows by n_steps. */
+ * n_steps greedy decode steps from `token` (launched directly), then every
+ * kernel class launched back to back, once per layer or once, n_steps times
+ * over, between one HIP event pair on the session stream.  Arrays of 8, one
+ * per kernel class: 0 embedding gather, 1 QKV GEMV (+RMSNorm, RoPE, KV
+ * append), 2 attention (chunk records + merge), 3 attn_output GEMV
+ * (+residual), 4 ffn gate/up GEMV (+RMSNorm, SwiGLU), 5 ffn_down GEMV
+ * (+residual), 6 output head GEMV (+RMSNorm, argmax), 7 finalize (not timed:
+ * it advances the state; reported as 0).  avg_ms: mean time per launch;
+ * launches: per step; bytes: stored weight bytes each launch streams
+ * (attention: the f32 K/V rows it reads).  len grows by n_steps and one more
+ * row must be free; scratch is left overwritten. */
 int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
                         uint64_t* launches, uint64_t* bytes);
 

@@ -147,88 +147,110 @@ GemvSeg seg_of(const ifx_tensor* t) {
   return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows};
 }
 
-// Per-kernel event timing of one step (ifx_session_profile); null when not profiling.
-struct StepProbe {
-  std::vector<hipEvent_t>* ev;  // ev[i] recorded before kernel i, ev[n] after the last
-  std::vector<int>* cls;        // kernel class of kernel i
-  void mark(hipStream_t st, int k) {
-    if (!ev) return;
-    hipEvent_t e;
-    (void)hipEventCreate(&e);
-    (void)hipEventRecord(e, st);
-    ev->push_back(e);
-    cls->push_back(k);
-  }
-};
+// Kernel classes of one step (ifx_session_profile): 0 embed, 1 qkv + rope +
+// kv-append, 2 attention (partials + merge), 3 attn_output + residual,
+// 4 ffn gate/up + swiglu, 5 ffn_down + residual, 6 output head + argmax,
+// 7 finalize.  Classes 1..5 run once per layer, the others once per step.
+constexpr int kClasses = 8;
+bool per_layer_class(int k) { return k >= 1 && k <= 5; }
 
-// One token through the whole model: embed -> layers -> final norm + head ->
-// greedy bookkeeping.  Every kernel reads positions from s->state.
-int enqueue_step(ifx_session* s, StepProbe probe = StepProbe{nullptr, nullptr}) {
+// Launches the kernel(s) of class k (for layer l where it applies).  Every
+// kernel reads positions from s->state.
+int enqueue_class(ifx_session* s, int k, size_t l) {
   ifx_model* m = s->m;
   const ifx_config& c = m->cfg;
   hipStream_t st = s->stream;
   const uint32_t D = (uint32_t)c.hidden_size, F = (uint32_t)c.intermediate_size;
   const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim);
-  probe.mark(st, 0);
-  IFX_HIP(launch_embed_state(devw(m->embd), s->state, s->hidden, st));
-  for (size_t l = 0; l < m->layers.size(); l++) {
-    const LayerDev& L = m->layers[l];
-    float* kc = s->kc + l * s->max_seq * kvd;
-    float* vc = s->vc + l * s->max_seq * kvd;
-    probe.mark(st, 1);
-    GemvLaunch g;
-    g.seg[0] = seg_of(L.q);
-    g.seg[1] = seg_of(L.k);
-    g.seg[2] = seg_of(L.v);
-    g.nseg = 3;
-    g.cols = D;
-    g.x = s->hidden;
-    g.norm_w = L.attn_norm;
-    g.eps = c.norm_eps;
-    QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd};
-    IFX_HIP(gemv_qkv(g, e, st));
-    probe.mark(st, 2);
-    AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
-               (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
-    IFX_HIP(launch_attn_decode(a, st));
-    probe.mark(st, 3);
-    GemvLaunch go;
-    go.seg[0] = seg_of(L.o);
-    go.nseg = 1;
-    go.cols = D;
-    go.x = s->attn;
-    IFX_HIP(gemv_residual(go, s->hidden, st));
-    probe.mark(st, 4);
-    GemvLaunch gf;
-    gf.seg[0] = seg_of(L.gate);
-    gf.seg[1] = seg_of(L.up);
-    gf.nseg = 2;
-    gf.paired = true;
-    gf.cols = D;
-    gf.x = s->hidden;
-    gf.norm_w = L.ffn_norm;
-    gf.eps = c.norm_eps;
-    IFX_HIP(gemv_swiglu(gf, s->mid, st));
-    probe.mark(st, 5);
-    GemvLaunch gd;
-    gd.seg[0] = seg_of(L.down);
-    gd.nseg = 1;
-    gd.cols = F;
-    gd.x = s->mid;
-    IFX_HIP(gemv_residual(gd, s->hidden, st));
+  switch (k) {
+    case 0:
+      IFX_HIP(launch_embed_state(devw(m->embd), s->state, s->hidden, st));
+      return IFX_OK;
+    case 6: {
+      GemvLaunch gh;
+      gh.seg[0] = seg_of(m->output);
+      gh.nseg = 1;
+      gh.cols = D;
+      gh.x = s->hidden;
+      gh.norm_w = m->out_norm;
+      gh.eps = c.norm_eps;
+      IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
+      return IFX_OK;
+    }
+    case 7:
+      IFX_HIP(launch_finalize(s->state, st));
+      return IFX_OK;
+    default:
+      break;
   }
-  probe.mark(st, 6);
-  GemvLaunch gh;
-  gh.seg[0] = seg_of(m->output);
-  gh.nseg = 1;
-  gh.cols = D;
-  gh.x = s->hidden;
-  gh.norm_w = m->out_norm;
-  gh.eps = c.norm_eps;
-  IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
-  probe.mark(st, 7);
-  IFX_HIP(launch_finalize(s->state, st));
-  probe.mark(st, -1);
+  const LayerDev& L = m->layers[l];
+  float* kc = s->kc + l * s->max_seq * kvd;
+  float* vc = s->vc + l * s->max_seq * kvd;
+  switch (k) {
+    case 1: {
+      GemvLaunch g;
+      g.seg[0] = seg_of(L.q);
+      g.seg[1] = seg_of(L.k);
+      g.seg[2] = seg_of(L.v);
+      g.nseg = 3;
+      g.cols = D;
+      g.x = s->hidden;
+      g.norm_w = L.attn_norm;
+      g.eps = c.norm_eps;
+      QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd};
+      IFX_HIP(gemv_qkv(g, e, st));
+      return IFX_OK;
+    }
+    case 2: {
+      AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
+                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
+      IFX_HIP(launch_attn_decode(a, st));
+      return IFX_OK;
+    }
+    case 3: {
+      GemvLaunch go;
+      go.seg[0] = seg_of(L.o);
+      go.nseg = 1;
+      go.cols = D;
+      go.x = s->attn;
+      IFX_HIP(gemv_residual(go, s->hidden, st));
+      return IFX_OK;
+    }
+    case 4: {
+      GemvLaunch gf;
+      gf.seg[0] = seg_of(L.gate);
+      gf.seg[1] = seg_of(L.up);
+      gf.nseg = 2;
+      gf.paired = true;
+      gf.cols = D;
+      gf.x = s->hidden;
+      gf.norm_w = L.ffn_norm;
+      gf.eps = c.norm_eps;
+      IFX_HIP(gemv_swiglu(gf, s->mid, st));
+      return IFX_OK;
+    }
+    case 5: {
+      GemvLaunch gd;
+      gd.seg[0] = seg_of(L.down);
+      gd.nseg = 1;
+      gd.cols = F;
+      gd.x = s->mid;
+      IFX_HIP(gemv_residual(gd, s->hidden, st));
+      return IFX_OK;
+    }
+    default:
+      return set_error(IFX_E_INVALID_ARG, "kernel class %d", k);
+  }
+}
+
+// One token through the whole model: embed -> layers -> final norm + head ->
+// greedy bookkeeping.
+int enqueue_step(ifx_session* s) {
+  IFX_TRY(enqueue_class(s, 0, 0));
+  for (size_t l = 0; l < s->m->layers.size(); l++)
+    for (int k = 1; k <= 5; k++) IFX_TRY(enqueue_class(s, k, l));
+  IFX_TRY(enqueue_class(s, 6, 0));
+  IFX_TRY(enqueue_class(s, 7, 0));
   return IFX_OK;
 }
 
@@ -625,12 +647,16 @@ int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len) {
   return IFX_OK;
 }
 
-// Measurement hook: n_steps greedy decode steps with direct launches and a HIP
-// event pair around every kernel on the session stream.  Per kernel class
-// (0 embed, 1 qkv+rope+kv-append, 2 attention, 3 attn_output+residual,
-//  4 ffn gate/up+swiglu, 5 ffn_down+residual, 6 output head+argmax, 7 finalize):
-// avg_ms = mean duration per launch, launches = launches per step,
-// bytes = stored weight bytes streamed per launch (0 where no weights).
+// Measurement hook.  n_steps greedy decode steps run first (direct launches),
+// so the state is a real decode state; then every kernel class is launched
+// back to back, once per layer (or once), n_steps times over, between one HIP
+// event pair on the session stream: avg_ms = mean time per launch (what a
+// kernel trace reports as its duration, plus the gap between launches),
+// launches = launches per step, bytes = stored weight bytes streamed per
+// launch (attention: the f32 K and V rows it attends; 0 where no weights).
+// The repeated launches leave scratch and the next token's KV slot written;
+// the next decode step recomputes both.  Finalize (class 7) advances the
+// device state and is not repeated: its avg_ms is 0.
 int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
                         uint64_t* launches, uint64_t* bytes) {
   clear_error();
@@ -638,36 +664,38 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   ifx_model* m = s->m;
   if (token >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "token");
   IFX_TRY(check_vocab(m));
-  if (s->len + n_steps > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
+  // one spare row: the repeated qkv launches write the next token's slot
+  if (s->len + n_steps + 1 > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
   const uint64_t len0 = s->len;
-  double sum[8] = {0};
-  uint64_t cnt[8] = {0};
   IFX_TRY(state_op(s, STATE_DECODE, token, 0));
   for (uint64_t i = 0; i < n_steps; i++) {
-    std::vector<hipEvent_t> ev;
-    std::vector<int> cls;
-    int rc = enqueue_step(s, StepProbe{&ev, &cls});
+    IFX_TRY(enqueue_step(s));
     s->steps++;
-    IFX_HIP(hipStreamSynchronize(s->stream));
-    for (size_t k = 0; k + 1 < ev.size(); k++) {
-      float ms = 0.f;
-      (void)hipEventElapsedTime(&ms, ev[k], ev[k + 1]);
-      if (cls[k] >= 0 && cls[k] < 8) { sum[cls[k]] += ms; cnt[cls[k]]++; }
-    }
-    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
-    if (rc != IFX_OK) return rc;
   }
+  IFX_HIP(hipStreamSynchronize(s->stream));
   s->len += n_steps;
-  for (int k = 0; k < 8; k++) {
-    avg_ms[k] = cnt[k] ? (float)(sum[k] / cnt[k]) : 0.f;
-    launches[k] = cnt[k] / n_steps;
+  const size_t NL = m->layers.size();
+  for (int k = 0; k < kClasses; k++) {
+    const uint64_t per_step = per_layer_class(k) ? NL : 1;
+    launches[k] = per_step;
+    avg_ms[k] = 0.f;
+    // finalize advances the device state: not repeated (no weights, launch-bound)
+    if (per_step == 0 || k == 7) continue;
+    IFX_HIP(hipEventRecord(s->ev0, s->stream));
+    for (uint64_t i = 0; i < n_steps; i++)
+      for (size_t l = 0; l < per_step; l++) IFX_TRY(enqueue_class(s, k, l));
+    IFX_HIP(hipEventRecord(s->ev1, s->stream));
+    IFX_HIP(hipEventSynchronize(s->ev1));
+    float ms = 0.f;
+    IFX_HIP(hipEventElapsedTime(&ms, s->ev0, s->ev1));
+    avg_ms[k] = ms / (float)(n_steps * per_step);
   }
   const LayerDev& L0 = m->layers.empty() ? LayerDev{} : m->layers[0];
   bytes[0] = 0;
   bytes[1] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.q) + tensor_stream_bytes(L0.k) + tensor_stream_bytes(L0.v);
-  // attention streams the f32 K and V rows it attends (average over the steps)
+  // attention streams the f32 K and V rows it attends (the state after the steps)
   const uint64_t kvd = m->cfg.n_kv_heads * m->cfg.head_dim;
-  bytes[2] = 2 * (len0 + (n_steps + 1) / 2) * kvd * 4;
+  bytes[2] = 2 * (len0 + n_steps) * kvd * 4;
   bytes[3] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.o);
   bytes[4] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.gate) + tensor_stream_bytes(L0.up);
   bytes[5] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.down);

@@ -10,6 +10,27 @@
  * operations are the explicit 8-lane FMAs of matmul_t, as in the reference.
  *
  * Citations are path:line in the reference tree (phraakture/inferox).
+ *
+ * How each part is pinned (tests/test_oracle_kats.py, test_oracle_crosscheck.py):
+ *   dequant, every type   reference KATs (src/gguf/dequant.rs:248-392) + an
+ *                         independent numpy restatement, bit-equal on random and
+ *                         edge blocks (every 6-bit Q4_K scale/min value, Q6_K
+ *                         unsigned scales, all 65536 f16 values)
+ *   matmul_t              reference KATs (src/ops.rs:293-346), float64 bound, a
+ *                         lane-order vector that separates the hsum tree from a
+ *                         sequential sum
+ *   rms_norm, swiglu,     reference KATs (src/ops.rs:348-416), float64 within
+ *   softmax, add, argmax  tolerance, closed forms (softmax rows sum to 1, last
+ *                         index on ties, NaN -> error)
+ *   rope                  identity at position 0 (the decode case), rotation by
+ *                         the float64 angle elsewhere
+ *   decode/prefill/       float64 brute force of a small model, invariants
+ *   forward/generate      (prefill([t]) == decode(t), KV-row permutation), the
+ *                         all-zero-weight generate KAT (src/model/forward.rs)
+ * parity unpinned: the bit patterns of the libm-dependent values (expf in
+ * silu/softmax, powf/sinf/cosf in rope) equal the reference's only if Rust std
+ * and this glibc agree, which no reference test checks; they are pinned to
+ * tolerance above.  The same holds for whole token streams of decode/generate.
  */
 #define _GNU_SOURCE
 #include "oracle.h"
