@@ -36,9 +36,9 @@ CTX = 2048
 METRIC = "decode tok/s, 8B Q4_K_M bs=1, 1×MI355X; % of HBM-BW roofline"
 KCLASS = ["embed", "qkv_gemv", "attention", "attn_output_gemv", "ffn_gate_up_gemv", "ffn_down_gemv",
           "output_head_gemv", "finalize"]
-KERNEL_NAMES = {1: "k_gemv<EpiQkv, FragQ4K, FragQ6K>", 2: "k_attn_decode<128, 4> + k_attn_merge<128, 4>",
-                3: "k_gemv<EpiResidual, FragQ4K, FragQ4K>", 4: "k_gemv<EpiSwiglu, FragQ4K, FragQ4K>",
-                5: "k_gemv<EpiResidual, FragQ6K, FragQ6K>", 6: "k_gemv<EpiLogits, FragQ6K, FragQ6K>"}
+KERNEL_NAMES = {1: "k_gemv_mfma<EpiQkv, Q4_K, Q6_K>", 2: "k_attn_decode<128, 4> + k_attn_merge<128, 4>",
+                3: "k_gemv_mfma<EpiResidual, Q4_K>", 4: "k_gemv_mfma<EpiSwiglu, Q4_K>",
+                5: "k_gemv_mfma<EpiResidual, Q6_K>", 6: "k_gemv_mfma<EpiLogits, Q6_K>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_PROBE_BYTES = 256 << 20
 

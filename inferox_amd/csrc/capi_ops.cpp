@@ -2,6 +2,7 @@
 // the f32 operators of include/inferox.h.
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -48,21 +49,18 @@ DevW devw(const ifx_tensor* t) {
   return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal};
 }
 
-// Parallel host repack (one worker per core share) into a staging buffer.
-static void repack_parallel(uint32_t type, const uint8_t* src, uint64_t nb, uint64_t src_bb,
-                            uint8_t* body, uint64_t body_bb, uint8_t* scal, uint64_t scal_bb) {
+// Runs fn(i0, i1) over [0, n) in contiguous ranges, one worker per core share.
+template <class F>
+static void parallel_ranges(uint64_t n, uint64_t min_per_worker, F fn) {
   unsigned nt = std::thread::hardware_concurrency();
   nt = nt == 0 ? 1 : (nt > 16 ? 16 : nt);
-  if (nb < 65536) nt = 1;
+  if (n < (uint64_t)nt * min_per_worker) nt = (unsigned)std::max<uint64_t>(1, n / min_per_worker);
   std::vector<std::thread> th;
-  const uint64_t per = (nb + nt - 1) / nt;
+  const uint64_t per = (n + nt - 1) / nt;
   for (unsigned i = 0; i < nt; i++) {
-    const uint64_t b0 = i * per, b1 = b0 + per < nb ? b0 + per : nb;
-    if (b0 >= b1) break;
-    th.emplace_back([=] {
-      repack_to_device_layout(type, src + b0 * src_bb, b1 - b0, body + b0 * body_bb,
-                              scal ? scal + b0 * scal_bb : nullptr);
-    });
+    const uint64_t a = i * per, b = a + per < n ? a + per : n;
+    if (a >= b) break;
+    th.emplace_back([=] { fn(a, b); });
   }
   for (auto& t : th) t.join();
 }
@@ -103,13 +101,23 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
   t->L.n_blocks = rows * cols / be;
   t->L.blocks_per_row = cols / be;
   hipError_t e;
-  if (type == T_F32 || type == T_F16 || type == T_Q4K) {
+  if (type == T_F32 || type == T_F16) {
     e = hipMemcpy(t->L.body, src, nbytes, hipMemcpyHostToDevice);
   } else {
     std::vector<uint8_t> stage(body + scal);
-    const uint64_t nb = t->L.n_blocks;
-    repack_parallel(type, src, nb, bb, stage.data(), body / nb, scal ? stage.data() + body : nullptr,
-                    scal / nb);
+    if (type == T_Q4K || type == T_Q6K) {
+      const uint64_t tiles = (rows + kTileRows - 1) / kTileRows;
+      parallel_ranges(tiles, 64, [&](uint64_t t0, uint64_t t1) {
+        repack_tiles(type, src, rows, cols, t0, t1, stage.data());
+      });
+    } else {
+      const uint64_t nb = t->L.n_blocks, body_bb = body / nb, scal_bb = scal / nb;
+      uint8_t* sp = scal ? stage.data() + body : nullptr;
+      parallel_ranges(nb, 65536, [&](uint64_t b0, uint64_t b1) {
+        repack_to_device_layout(type, src + b0 * bb, b1 - b0, stage.data() + b0 * body_bb,
+                                sp ? sp + b0 * scal_bb : nullptr);
+      });
+    }
     e = hipMemcpy(t->L.body, stage.data(), body, hipMemcpyHostToDevice);
     if (e == hipSuccess && scal) e = hipMemcpy(t->L.scal, stage.data() + body, scal, hipMemcpyHostToDevice);
   }

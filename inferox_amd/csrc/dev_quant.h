@@ -85,13 +85,6 @@ __device__ __forceinline__ float raw_elem(uint32_t type, const uint8_t* p, uint6
   }
 }
 
-// Bit position of the high 2 bits of element e (0..31) of a Q6_K group within
-// the group's re-ordered qh words (see the layout note in ifx_common.h).
-__device__ __forceinline__ int q6_hi_bitpos(int e) {
-  int w = (e & 15) >> 3, k = e & 7;
-  return 8 * (k >> 1) + (w == 0 ? 4 : 0) + ((k & 1) ? 2 : 0);
-}
-
 struct DevW {
   uint32_t type;
   uint64_t cols;
@@ -118,19 +111,33 @@ __device__ __forceinline__ float dev_elem(const DevW& w, uint64_t e) {
       float delta = h2f(((const uint16_t*)w.scal)[b]);
       return (float)(int8_t)w.body[b * 32 + e % 32] * delta;
     }
-    case 12:
-      return raw_elem(12, w.body, e);
-    case 14: {
-      uint64_t b = e / 256;
-      int j = (int)(e % 256), g = j / 32, l = j % 32;
-      const uint8_t* blk = w.body + b * 208;
-      float d = h2f(((const uint16_t*)w.scal)[b]);
-      uint32_t qlb = blk[j / 2];
+    case 12: {  // tiled Q4_K (ifx_common.h): same arithmetic as raw_elem
+      const uint64_t row = e / w.cols, col = e % w.cols;
+      const uint8_t* u = w.body + ((row >> 4) * (w.cols >> 8) + (col >> 8)) * 2304;
+      const int n = (int)(row & 15), j = (int)(col & 255), g = j / 32, l = j % 32;
+      const uint8_t* h = u + 16 * n;
+      float d = h2f(ld_u16_unaligned(h)), dmin = h2f(ld_u16_unaligned(h + 2));
+      uint32_t sc, mn;
+      q4k_scale_min(h + 4, g, &sc, &mn);
+      float dall = d * (float)sc;
+      float dm = dmin * (float)mn;
+      uint32_t byte = u[256 + (g >> 2) * 1024 + (n + 16 * (g & 3)) * 16 + l / 2];
+      uint32_t q = (l & 1) ? (byte >> 4) : (byte & 15u);
+      return dall * (float)q - dm;
+    }
+    case 14: {  // tiled Q6_K
+      const uint64_t row = e / w.cols, col = e % w.cols;
+      const uint8_t* u = w.body + ((row >> 4) * (w.cols >> 8) + (col >> 8)) * 3360;
+      const int n = (int)(row & 15), j = (int)(col & 255), s = j / 32, k = j & 15;
+      const int lane = n + 16 * (s & 3), c = 2 * (s >> 2) + ((j >> 4) & 1);
+      uint32_t qlb = u[(s >> 2) * 1024 + lane * 16 + ((j >> 1) & 15)];
       uint32_t lo = (j & 1) ? (qlb >> 4) : (qlb & 15u);
-      const uint32_t* words = (const uint32_t*)(blk + 128);
-      uint32_t hi = (words[2 * g + (l >> 4)] >> q6_hi_bitpos(l)) & 3u;
+      const uint8_t* hw = u + 2048 + lane * 16 + 4 * c;
+      uint32_t word = (uint32_t)hw[0] | ((uint32_t)hw[1] << 8) | ((uint32_t)hw[2] << 16) | ((uint32_t)hw[3] << 24);
+      uint32_t hi = (word >> (8 * ((k & 7) >> 1) + 2 * (k & 1) + 4 * (k >> 3))) & 3u;
       int q = (int)(lo | (hi << 4));
-      return d * (float)blk[192 + j / 16] * (float)(q - 32);
+      float d = h2f(ld_u16_unaligned(u + 3328 + 2 * n));
+      return d * (float)u[3072 + 4 * lane + c] * (float)(q - 32);
     }
     case 15: {
       uint64_t b = e / 256;

@@ -69,36 +69,16 @@ const char* type_name(uint32_t t) {
 
 bool layout_sizes(uint32_t type, uint64_t rows, uint64_t cols, uint64_t* body, uint64_t* scal) {
   uint64_t n = rows * cols;
+  const uint64_t tiled = (rows + kTileRows - 1) / kTileRows * kTileRows * (cols / 256);  // blocks incl. padding
   switch (type) {
     case T_F32: *body = n * 4; *scal = 0; return true;
     case T_F16: *body = n * 2; *scal = 0; return true;
     case T_Q4_0: if (cols % 32) return false; *body = n / 32 * 16; *scal = n / 32 * 2; return true;
     case T_Q8_0: if (cols % 32) return false; *body = n / 32 * 32; *scal = n / 32 * 2; return true;
-    case T_Q4K: if (cols % 256) return false; *body = n / 256 * 144; *scal = 0; return true;
-    case T_Q6K: if (cols % 256) return false; *body = n / 256 * 208; *scal = n / 256 * 2; return true;
+    case T_Q4K: if (cols % 256) return false; *body = tiled * 144; *scal = 0; return true;
+    case T_Q6K: if (cols % 256) return false; *body = tiled * 210; *scal = 0; return true;
     case T_Q8K: if (cols % 256) return false; *body = n / 256 * 288; *scal = n / 256 * 4; return true;
     default: return false;
-  }
-}
-
-// Spread the four nibbles of a 16-bit value into the low nibbles of four bytes.
-static inline uint32_t spread_nibbles(uint32_t x) {
-  x = (x | (x << 8)) & 0x00FF00FFu;
-  return (x | (x << 4)) & 0x0F0F0F0Fu;
-}
-
-// Q6_K qh re-order for one 32-element group.  The original 64 bits hold element
-// e at bits 2e..2e+1.  For each 16-element half the new 32-bit word holds the
-// high bits of elements 0..7 in the high nibble of byte b (element 2b at bits
-// 4-5, 2b+1 at 6-7) and of elements 8..15 in the low nibble (8+2b at 0-1,
-// 8+2b+1 at 2-3), matching the even/odd nibble split of the two ql words.
-static inline void q6_reorder_group(const uint8_t* qh8, uint8_t* out8) {
-  uint64_t q;
-  memcpy(&q, qh8, 8);
-  for (int h = 0; h < 2; h++) {
-    uint32_t s = (uint32_t)(q >> (32 * h));
-    uint32_t w = (spread_nibbles(s & 0xFFFFu) << 4) | spread_nibbles(s >> 16);
-    memcpy(out8 + 4 * h, &w, 4);
   }
 }
 
@@ -107,7 +87,6 @@ void repack_to_device_layout(uint32_t type, const uint8_t* src, uint64_t nb, uin
   switch (type) {
     case T_F32: memcpy(body, src, nb * 4); return;
     case T_F16: memcpy(body, src, nb * 2); return;
-    case T_Q4K: memcpy(body, src, nb * 144); return;
     case T_Q4_0:
       for (uint64_t b = 0; b < nb; b++) {
         memcpy(scal + 2 * b, src + 18 * b, 2);
@@ -126,18 +105,65 @@ void repack_to_device_layout(uint32_t type, const uint8_t* src, uint64_t nb, uin
         memcpy(body + 288 * b, src + 292 * b + 4, 288);
       }
       return;
-    case T_Q6K:
-      for (uint64_t b = 0; b < nb; b++) {
-        const uint8_t* s = src + 210 * b;
-        uint8_t* o = body + 208 * b;
-        memcpy(scal + 2 * b, s, 2);          // d
-        memcpy(o, s + 18, 128);              // ql
-        memcpy(o + 192, s + 2, 16);          // u8 scales
-        for (int g = 0; g < 8; g++) q6_reorder_group(s + 146 + 8 * g, o + 128 + 8 * g);
-      }
-      return;
     default: return;
   }
+}
+
+// Bit position, in a Q6_K lane word, of the 2-bit high part of element k
+// (0..15) of a 16-element part: byte (k & 7) / 2, bits 2 (k & 1) + 4 (k >> 3).
+static inline int q6_word_bitpos(int k) { return 8 * ((k & 7) >> 1) + 2 * (k & 1) + 4 * (k >> 3); }
+
+// One (tile, block) unit of the tiled K-quant layout; blk[n] is row n's GGUF
+// block, or null for a padding row (zero bytes).
+static void pack_unit(uint32_t type, const uint8_t* const* blk, uint8_t* u) {
+  if (type == T_Q4K) {
+    memset(u, 0, kUnitQ4K);
+    for (uint64_t n = 0; n < kTileRows; n++) {
+      if (!blk[n]) continue;
+      memcpy(u + 16 * n, blk[n], 16);  // d, dmin, 12 scale bytes
+      for (int q = 0; q < 2; q++)
+        for (int g = 0; g < 4; g++)    // lane n + 16g: the 16 qs bytes of sub-block g + 4q
+          memcpy(u + 256 + 1024 * q + 16 * (n + 16 * g), blk[n] + 16 + 16 * (g + 4 * q), 16);
+    }
+    return;
+  }
+  // Q6_K, reference block: d @0, u8 scales @2, ql @18, qh @146 (src/gguf/dequant.rs:165-199)
+  memset(u, 0, kUnitQ6K);
+  for (uint64_t n = 0; n < kTileRows; n++) {
+    const uint8_t* b = blk[n];
+    if (!b) continue;
+    memcpy(u + 3328 + 2 * n, b, 2);
+    for (int g = 0; g < 4; g++) {
+      const uint64_t lane = n + 16 * g;
+      for (int q = 0; q < 2; q++) memcpy(u + 1024 * q + 16 * lane, b + 18 + 16 * (g + 4 * q), 16);
+      for (int c = 0; c < 4; c++) {  // part c of the lane: sub-block g + 4 (c >> 1), half c & 1
+        const int part = 2 * (g + 4 * (c >> 1)) + (c & 1);
+        uint32_t w = 0;
+        for (int k = 0; k < 16; k++) {
+          const int e = 16 * part + k;
+          const uint32_t hi = (b[146 + e / 4] >> (2 * (e % 4))) & 3u;
+          w |= hi << q6_word_bitpos(k);
+        }
+        memcpy(u + 2048 + 16 * lane + 4 * c, &w, 4);
+        u[3072 + 4 * lane + c] = b[2 + part];
+      }
+    }
+  }
+}
+
+void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t cols, uint64_t t0, uint64_t t1,
+                  uint8_t* body) {
+  const uint64_t nbr = cols / 256, bb = type == T_Q4K ? 144 : 210;
+  const uint64_t unit = type == T_Q4K ? kUnitQ4K : kUnitQ6K;
+  const uint8_t* blk[kTileRows];
+  for (uint64_t t = t0; t < t1; t++)
+    for (uint64_t b = 0; b < nbr; b++) {
+      for (uint64_t n = 0; n < kTileRows; n++) {
+        const uint64_t r = t * kTileRows + n;
+        blk[n] = r < rows ? src + (r * nbr + b) * bb : nullptr;
+      }
+      pack_unit(type, blk, body + (t * nbr + b) * unit);
+    }
 }
 
 }  // namespace ifx

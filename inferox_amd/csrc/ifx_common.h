@@ -47,18 +47,31 @@ const char* type_name(uint32_t t);
 
 // ---------------------------------------------------------------------------
 // Device weight layout of a [rows x cols] matrix (cols contiguous), as read by
-// the GEMV / embedding / device-dequant kernels.  Same bits as the GGUF blocks;
-// only the placement of block fields changes, so the bytes streamed per row
-// equal the GGUF bytes.
+// the GEMV / embedding / device-dequant kernels.  The same bits as the GGUF
+// blocks, placed for the kernel that streams them.
 //   F32, F16 : row-major elements.
-//   Q4_K     : GGUF blocks unchanged (144 B = 9 x 16 B, rows are whole blocks).
 //   Q4_0     : qs[nb][16] | d[nb] (f16).
 //   Q8_0     : qs[nb][32] | d[nb] (f16).
-//   Q6_K     : body[nb][208] = ql[128] | qh'[64] | sc[16]  and  d[nb] (f16).
-//              qh' holds the same 2-bit high parts, re-ordered per 16 elements
-//              so that a 32-bit word lines up with the nibble split of ql.
 //   Q8_K     : body[nb][288] = sc[32] | qs[256]  and  dd[nb] = {d, dmin} (f16 x 2).
+//   Q4_K, Q6_K (tiled, for the int8-MFMA GEMV): rows are grouped in tiles of
+//     16 (the last tile padded with zero blocks); unit (t, b) holds block b of
+//     rows 16t..16t+15 at ((t * cols/256) + b) * unit bytes.  Lane L = n + 16g
+//     (row n, group g = 0..3) owns sub-blocks g and g + 4 (32 elements each)
+//     of row n; its bytes sit where one 16-byte load per lane fetches them.
+//     Q4_K unit (2304 B = 16 x 144):
+//       [0, 256)      row n: d, dmin, 12 scale bytes (the block's first 16 B)
+//       [256, 2304)   [q = 0, 1][lane L][16]: the qs bytes of sub-block g + 4q
+//     Q6_K unit (3360 B = 16 x 210):
+//       [0, 2048)     [q][lane L][16]: the ql bytes of sub-block g + 4q
+//       [2048, 3072)  [lane L][c = 0..3]: 32-bit word of the 2-bit high parts
+//                     of part c (sub-block g + 4 (c >> 1), half c & 1): element
+//                     k of the part at byte (k & 7) / 2, bits 2 (k & 1) + 4 (k >> 3)
+//       [3072, 3328)  [lane L][c]: the part's u8 scale
+//       [3328, 3360)  row n: d (f16)
 // ---------------------------------------------------------------------------
+constexpr uint64_t kTileRows = 16;
+constexpr uint64_t kUnitQ4K = 16 * 144, kUnitQ6K = 16 * 210;
+
 struct DevLayout {
   uint32_t type = 0;
   uint64_t rows = 0, cols = 0;
@@ -71,10 +84,14 @@ struct DevLayout {
 };
 
 // Host-side repack of one matrix from GGUF block bytes into the device layout
-// (dst_body/dst_scal sized by layout_sizes).
+// (dst_body/dst_scal sized by layout_sizes); the block-wise types.
 bool layout_sizes(uint32_t type, uint64_t rows, uint64_t cols, uint64_t* body, uint64_t* scal);
 void repack_to_device_layout(uint32_t type, const uint8_t* src, uint64_t n_blocks, uint8_t* body,
                              uint8_t* scal);
+// Q4_K / Q6_K: row tiles [t0, t1) of the tiled layout into body (the whole
+// matrix's body; src is the whole matrix's GGUF bytes).
+void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t cols, uint64_t t0, uint64_t t1,
+                  uint8_t* body);
 
 }  // namespace ifx
 

@@ -3,7 +3,9 @@
 // Replaces the decode use of ops::matmul_t (src/ops.rs:33-44,104-134) fed by
 // the per-call f32 dequant of Weights::tensor_f32_by_index
 // (src/gguf/weights.rs:66-74): y = W x with W read once from HBM in its
-// quantized form and decoded in registers.
+// quantized form and decoded in registers.  This file holds the f32-dot path
+// (Q8_0, Q4_0, Q8_K, F32, F16) and the launcher of every GEMV; Q4_K and Q6_K
+// matrices go to the int8-MFMA kernel of kern_gemv_mfma.hip.
 //
 // Work decomposition
 //   * Persistent workgroups of 8 wave64, two per CU (16 waves per CU, at most
@@ -23,9 +25,8 @@
 //     store + greedy argmax (output head).
 // Compiled with -ffp-contract=off: only the explicit fmaf below are fused.
 #include <algorithm>
-#include <type_traits>
 
-#include "kernels.h"
+#include "gemv_epi.h"
 
 namespace ifx {
 
@@ -41,7 +42,6 @@ struct KArgs {
   GemvSeg seg[3];
   uint32_t ntiles[3];  // tiles per logical segment (paired: one logical segment)
   uint32_t rot[3];     // first-wave rotation per segment (balances small segments)
-  uint32_t use_b;      // bit s: segment s decodes with the kernel's second type
   uint32_t split;      // waves per row tile (1, 2, 4 or 8): they share its units
   int nseg;            // logical segments
   uint32_t cols, groups;
@@ -123,115 +123,6 @@ __device__ __forceinline__ RowRef row_of(const KArgs& a, int s, uint32_t tile, i
 // The main loop is free of branches so that the compiler can wait for exactly
 // the loads a row needs (a join in the control flow makes it wait for all).
 // ---------------------------------------------------------------------------
-
-// Q4_K (src/gguf/dequant.rs:133-161): element 32g+l is nibble (l&1) of
-// qs[16g + l/2];  sum_l ((d*sc)*q_l - dmin*mn) x_l = (d*sc)*S - (dmin*mn)*sum(x).
-struct FragQ4K {
-  uint4 h[kR], q[kR];
-  template <bool P>
-  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
-    const RowRef rr = row_of<P>(a, s, tile, r);
-    // wave-uniform row base + 32-bit lane offset (scalar-base loads)
-    const uint8_t* row = rr.body + rr.row * ((a.groups / 8) * 144);
-    const uint32_t off = (g / 8) * 144;
-    h[r] = ldg<uint4>(row + off);
-    q[r] = ldg<uint4>(row + off + 16 + 16 * (g & 7));
-  }
-  template <bool P>
-  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t g, bool valid, const float4* xv, float xsa,
-                          float xsb, float* acc, int r) const {
-    const uint32_t sub = g & 7, j = sub & 3;
-    const uint4 hv = h[r];
-    // 6-bit scale / min of sub-block `sub` (get_scale_min_k4), selected without a branch
-    const uint32_t sc_lo = (hv.y >> (8 * j)) & 63u, mn_lo = (hv.z >> (8 * j)) & 63u;
-    const uint32_t sc_hi = ((hv.w >> (8 * j)) & 15u) | (((hv.y >> (8 * j + 6)) & 3u) << 4);
-    const uint32_t mn_hi = ((hv.w >> (8 * j + 4)) & 15u) | (((hv.z >> (8 * j + 6)) & 3u) << 4);
-    const uint32_t sc = sub < 4 ? sc_lo : sc_hi, mn = sub < 4 ? mn_lo : mn_hi;
-    const float d = h2f(hv.x), dmin = h2f(hv.x >> 16);
-    float s0 = 0.f, s1 = 0.f;
-    const uint32_t qw[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      // high nibbles stay in place (16 q): s1 is scaled by 1/16 below, exactly
-      const uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu), hi = opaque(qw[w] & 0xF0F0F0F0u);
-      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-      s0 = fmaf(cvtb(lo, 0), xa.x, s0);
-      s1 = fmaf(cvtb(hi, 0), xa.y, s1);
-      s0 = fmaf(cvtb(lo, 1), xa.z, s0);
-      s1 = fmaf(cvtb(hi, 1), xa.w, s1);
-      s0 = fmaf(cvtb(lo, 2), xb.x, s0);
-      s1 = fmaf(cvtb(hi, 2), xb.y, s1);
-      s0 = fmaf(cvtb(lo, 3), xb.z, s0);
-      s1 = fmaf(cvtb(hi, 3), xb.w, s1);
-    }
-    const float A = d * (float)sc, M = dmin * (float)mn;
-    const float v = fmaf(A, fmaf(s1, 0.0625f, s0), -M * (xsa + xsb));
-    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
-  }
-};
-
-// Q6_K in the device layout (ql | re-ordered qh | u8 sc; d separate):
-// q = lo | hi<<4, y = (d*sc)*(q-32)  (src/gguf/dequant.rs:182-197).
-struct FragQ6K {
-  uint4 ql[kR];
-  uint2 qh[kR];
-  uint32_t sd[kR];  // the group's two scale bytes (low 16 bits) | d bits (high 16)
-  template <bool P>
-  __device__ void load_row(const KArgs& a, int s, uint32_t tile, uint32_t g, int r) {
-    const RowRef rr = row_of<P>(a, s, tile, r);
-    const uint32_t nb = a.groups / 8;
-    const uint8_t* row = rr.body + rr.row * (nb * 208);
-    const uint8_t* rowd = rr.scal + rr.row * (nb * 2);
-    const uint32_t off = (g / 8) * 208, h = g & 7;
-    ql[r] = ldg<uint4>(row + off + 16 * h);
-    qh[r] = ldg<uint2>(row + off + 128 + 8 * h);
-    sd[r] = (uint32_t)ldg<uint16_t>(row + off + 192 + 2 * h) | ((uint32_t)ldg<uint16_t>(rowd + (g / 8) * 2) << 16);
-  }
-  template <bool P>
-  __device__ void dot_row(const KArgs& a, int s, uint32_t tile, uint32_t, bool valid, const float4* xv, float xsa,
-                          float xsb, float* acc, int r) const {
-    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
-    const uint4 L = ql[r];
-    const uint2 H = qh[r];
-    // half a: elements 0..15 (L.x: 0-7, L.y: 8-15; high bits in H.x); half b: 16..31
-    const uint32_t ev[4] = {opaque((L.x & m4) | (H.x & m2)), opaque((L.y & m4) | ((H.x << 4) & m2)),
-                            opaque((L.z & m4) | (H.y & m2)), opaque((L.w & m4) | ((H.y << 4) & m2))};
-    const uint32_t ov[4] = {opaque(((L.x >> 4) & m4) | ((H.x >> 2) & m2)),
-                            opaque(((L.y >> 4) & m4) | ((H.x << 2) & m2)),
-                            opaque(((L.z >> 4) & m4) | ((H.y >> 2) & m2)),
-                            opaque(((L.w >> 4) & m4) | ((H.y << 2) & m2))};
-    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-#pragma unroll
-    for (int w = 0; w < 2; w++) {
-      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-      a0 = fmaf(cvtb(ev[w], 0), xa.x, a0);
-      a1 = fmaf(cvtb(ov[w], 0), xa.y, a1);
-      a0 = fmaf(cvtb(ev[w], 1), xa.z, a0);
-      a1 = fmaf(cvtb(ov[w], 1), xa.w, a1);
-      a0 = fmaf(cvtb(ev[w], 2), xb.x, a0);
-      a1 = fmaf(cvtb(ov[w], 2), xb.y, a1);
-      a0 = fmaf(cvtb(ev[w], 3), xb.z, a0);
-      a1 = fmaf(cvtb(ov[w], 3), xb.w, a1);
-    }
-#pragma unroll
-    for (int w = 2; w < 4; w++) {
-      const float4 xa = xv[2 * w], xb = xv[2 * w + 1];
-      b0 = fmaf(cvtb(ev[w], 0), xa.x, b0);
-      b1 = fmaf(cvtb(ov[w], 0), xa.y, b1);
-      b0 = fmaf(cvtb(ev[w], 1), xa.z, b0);
-      b1 = fmaf(cvtb(ov[w], 1), xa.w, b1);
-      b0 = fmaf(cvtb(ev[w], 2), xb.x, b0);
-      b1 = fmaf(cvtb(ov[w], 2), xb.y, b1);
-      b0 = fmaf(cvtb(ev[w], 3), xb.z, b0);
-      b1 = fmaf(cvtb(ov[w], 3), xb.w, b1);
-    }
-    const float d = h2f(sd[r] >> 16);
-    const float sa = (float)(sd[r] & 0xffu), sb = (float)((sd[r] >> 8) & 0xffu);
-    const float ta = fmaf(-32.f, xsa, a0 + a1), tb = fmaf(-32.f, xsb, b0 + b1);
-    const float v = d * fmaf(sa, ta, sb * tb);
-    acc[r] += (valid && row_of<P>(a, s, tile, r).ok) ? v : 0.f;
-  }
-};
 
 // Q8_0 (device layout qs[32] | d): y = f32(i8 q) * delta (src/gguf/dequant.rs:101-109).
 struct FragQ80 {
@@ -386,115 +277,22 @@ struct FragF16 {
   }
 };
 
-// ---- epilogues: apply(segment, tile, reduced sums); lane r < kR owns row r ----
-struct EpiStore {
-  static constexpr bool kPaired = false;
-  float* y;
-  uint32_t seg_out[3];  // output offset of each segment
-  struct Wave {};
-  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
-    if (lane < kR) {
-      const RowRef rr = row_of<false>(a, s, tile, lane);
-      if (rr.ok) y[seg_out[s] + rr.row] = lane_acc(acc, lane);
+// Hands the reduced sums of a finished tile to the row epilogue (gemv_epi.h):
+// lane r < kR owns row r (paired: lanes 0, 1 own the gate rows, whose up rows
+// sit at r + 2).
+template <class Epi>
+__device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, const KArgs& a, int s, uint32_t tile,
+                                     const float* acc, int lane) {
+  constexpr bool P = Epi::kPaired;
+  if (lane < (P ? kR / 2 : kR)) {
+    const RowRef rr = row_of<P>(a, s, tile, lane);
+    if (rr.ok) {
+      const float v = lane_acc(acc, lane);
+      const float partner = P ? lane_acc(acc, lane + kR / 2) : (Epi::kNeighbor ? lane_acc(acc, lane ^ 1) : 0.f);
+      epi.row(ws, P ? 0 : s, (uint32_t)rr.row, v, partner);
     }
   }
-  __device__ void finish(Wave&, int) const {}
-};
-
-struct EpiResidual {
-  static constexpr bool kPaired = false;
-  float* h;
-  struct Wave {};
-  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
-    if (lane < kR) {
-      const RowRef rr = row_of<false>(a, s, tile, lane);
-      if (rr.ok) h[rr.row] = lane_acc(acc, lane) + h[rr.row];
-    }
-  }
-  __device__ void finish(Wave&, int) const {}
-};
-
-struct EpiQkv {
-  static constexpr bool kPaired = false;
-  QkvEpi e;
-  struct Wave {};
-  // rope (src/ops.rs:273-284): x[2i] = a*cos - b*sin, x[2i+1] = a*sin + b*cos
-  __device__ void apply(Wave&, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
-    if (lane >= kR) return;
-    const RowRef rr = row_of<false>(a, s, tile, lane);
-    if (!rr.ok) return;
-    const uint32_t r = (uint32_t)rr.row;
-    float v = lane_acc(acc, lane);
-    if (s < 2) {
-      const uint32_t i = r % e.head_dim;
-      if (i < e.rope_dim) {
-        const float2 cs = e.rope_cs[(uint64_t)e.state->rope_pos * (e.rope_dim / 2) + i / 2];
-        const float other = lane_acc(acc, lane ^ 1);
-        v = (i & 1) ? (other * cs.y + v * cs.x) : (v * cs.x - other * cs.y);
-      }
-    }
-    if (s == 0) {
-      e.q_out[r] = v;
-    } else {
-      const uint64_t off = (uint64_t)e.state->len * e.kv_dim + r;
-      if (s == 1) e.k_cache[off] = v;
-      else e.v_cache[off] = v;
-    }
-  }
-  __device__ void finish(Wave&, int) const {}
-};
-
-struct EpiSwiglu {
-  static constexpr bool kPaired = true;
-  float* mid;
-  struct Wave {};
-  // swiglu (src/ops.rs:190-209): silu(g) * u, sigmoid clamped to +-80
-  __device__ void apply(Wave&, const KArgs& a, int, uint32_t tile, const float* acc, int lane) const {
-    constexpr int H = kR / 2;
-    if (lane >= H) return;
-    const RowRef rr = row_of<true>(a, 0, tile, lane);
-    if (!rr.ok) return;
-    const float g = lane_acc(acc, lane), u = lane_acc(acc, lane + H);
-    float c = fminf(fmaxf(g, -80.f), 80.f);
-    if (g != g) c = g;
-    const float sig = 1.0f / (1.0f + expf(-c));
-    mid[rr.row] = (g * sig) * u;
-  }
-  __device__ void finish(Wave&, int) const {}
-};
-
-__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-  uint32_t b = __float_as_uint(v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | idx;
 }
-
-struct EpiLogits {
-  static constexpr bool kPaired = false;
-  float* logits;
-  DevState* state;
-  struct Wave {
-    unsigned long long best = 0;
-    bool nan = false;
-  };
-  __device__ void apply(Wave& w, const KArgs& a, int s, uint32_t tile, const float* acc, int lane) const {
-#pragma unroll
-    for (int r = 0; r < kR; r++) {
-      const RowRef rr = row_of<false>(a, s, tile, r);
-      if (!rr.ok) continue;
-      if (lane == r) logits[rr.row] = acc[r];
-      if (acc[r] != acc[r]) w.nan = true;
-      const unsigned long long k = argmax_key(acc[r], (uint32_t)rr.row);
-      w.best = k > w.best ? k : w.best;
-    }
-  }
-  __device__ void finish(Wave& w, int lane) const {
-    if (lane == 0) {
-      if (w.best) atomicMax(&state->argmax_key, w.best);
-      if (w.nan) atomicExch(&state->status, (int)IFX_E_NAN_LOGIT);
-    }
-  }
-};
 
 // The row tiles of one logical segment owned by this wave's tile group
 // (a.split waves of one workgroup): tiles first, first+TG, ..., `iters` of them
@@ -553,10 +351,10 @@ __device__ __forceinline__ void run_segment(const KArgs& a, const Epi& epi, type
           for (uint32_t i = 0; i < S; i++) v += pb[(wave + i) * kR + r];
           acc[r] = v;
         }
-        epi.apply(ws, a, s, tile, acc, lane);
+        emit(epi, ws, a, s, tile, acc, lane);
       }
     } else if (live) {
-      epi.apply(ws, a, s, tile, acc, lane);
+      emit(epi, ws, a, s, tile, acc, lane);
     }
   }
 }
@@ -654,9 +452,8 @@ __device__ __forceinline__ void stage_x_generic(const KArgs& a, float* xl, float
   __syncthreads();
 }
 
-// Main kernel: segments decode with FragA, or with FragB where use_b is set
-// (a Q4_K_M layer's QKV has Q4_K q/k and Q6_K v).
-template <class Epi, class FragA, class FragB>
+// Main kernel: every segment decodes with Frag.
+template <class Epi, class Frag>
 __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi epi) {
   extern __shared__ float lds[];
   float* xl = lds;                                    // [groups][36]
@@ -682,12 +479,11 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
   const uint32_t NG = (a.groups + 63) / 64;
   const uint32_t g0 = min(lane + 64 * min(j, NG - 1), a.groups - 1);
 
-  // first unit of segment 0 (always FragA) in flight while x is staged
+  // first unit of segment 0 in flight while x is staged
   constexpr bool P = Epi::kPaired;
-  constexpr bool kMixed = !std::is_same<FragA, FragB>::value;
   {
     const uint32_t first = (tg + TG - a.rot[0]) % TG;
-    FragA f;
+    Frag f;
     // lanes past the last group load a real group (unconditional loads keep
     // the fragments' live ranges short); their values are never used
     if (first < a.ntiles[0]) {
@@ -695,24 +491,17 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
       for (int r = 0; r < kR; r++) f.template load_row<P>(a, 0, first, g0, r);
     }
     stage_x(a, xl, xs, wl, red, tid, lane, wave);
-    run_segment<FragA, Epi>(a, epi, ws, 0, first, TG, block_iters(0), j, f, xl, xs, part, lane, wave);
+    run_segment<Frag, Epi>(a, epi, ws, 0, first, TG, block_iters(0), j, f, xl, xs, part, lane, wave);
   }
   for (int s = 1; s < a.nseg; s++) {
     const uint32_t first = (tg + TG - a.rot[s]) % TG;
     const uint32_t iters = block_iters(s);
     if (iters == 0) continue;
     const uint32_t t0 = first < a.ntiles[s] ? first : 0;
-    if (kMixed && ((a.use_b >> s) & 1u)) {
-      FragB f;
+    Frag f;
 #pragma unroll
-      for (int r = 0; r < kR; r++) f.template load_row<P>(a, s, t0, g0, r);
-      run_segment<FragB, Epi>(a, epi, ws, s, first, TG, iters, j, f, xl, xs, part, lane, wave);
-    } else {
-      FragA f;
-#pragma unroll
-      for (int r = 0; r < kR; r++) f.template load_row<P>(a, s, t0, g0, r);
-      run_segment<FragA, Epi>(a, epi, ws, s, first, TG, iters, j, f, xl, xs, part, lane, wave);
-    }
+    for (int r = 0; r < kR; r++) f.template load_row<P>(a, s, t0, g0, r);
+    run_segment<Frag, Epi>(a, epi, ws, s, first, TG, iters, j, f, xl, xs, part, lane, wave);
   }
   epi.finish(ws, lane);
 }
@@ -745,7 +534,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(KArgs a, Epi epi) {
       }
 #pragma unroll
       for (int r = 0; r < kR; r++) acc[r] = wave_sum(acc[r]);
-      epi.apply(ws, a, s, t, acc, lane);
+      emit(epi, ws, a, s, t, acc, lane);
     }
   }
   epi.finish(ws, lane);
@@ -772,27 +561,23 @@ hipError_t lds_opt_in(K kernel, size_t lds, bool& done) {
   return hipSuccess;
 }
 
-template <class Epi, class FA, class FB>
+template <class Epi, class F>
 hipError_t dispatch(const KArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
   static bool done = false;
-  hipError_t e = lds_opt_in(k_gemv<Epi, FA, FB>, lds, done);
+  hipError_t e = lds_opt_in(k_gemv<Epi, F>, lds, done);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_gemv<Epi, FA, FB>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
+  hipLaunchKernelGGL((k_gemv<Epi, F>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
   return hipGetLastError();
-}
-
-template <class Epi, class FA>
-hipError_t dispatch_b(const KArgs& a, uint32_t tb, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
-  switch (tb) {
-    case T_Q4K: return dispatch<Epi, FA, FragQ4K>(a, epi, blocks, lds, st);
-    case T_Q6K: return dispatch<Epi, FA, FragQ6K>(a, epi, blocks, lds, st);
-    default: return hipErrorInvalidValue;
-  }
 }
 
 template <class Epi>
 hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   if (L.nseg < 1 || L.nseg > 3 || L.cols == 0) return hipErrorInvalidValue;
+  // Q4_K / Q6_K (tiled layout): the int8-MFMA kernel; a launch does not mix the two families
+  int n_mfma = 0;
+  for (int s = 0; s < L.nseg; s++) n_mfma += mfma_type(L.seg[s].type) ? 1 : 0;
+  if (n_mfma == L.nseg) return launch_mfma(L, epi, st);
+  if (n_mfma != 0) return hipErrorInvalidValue;
   KArgs a{};
   a.cols = L.cols;
   a.groups = (L.cols + 31) / 32;
@@ -803,7 +588,7 @@ hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   for (int s = 0; s < L.nseg; s++) {
     a.seg[s] = L.seg[s];
     const uint32_t t = L.seg[s].type;
-    if ((t == T_Q4K || t == T_Q6K || t == T_Q8K) && L.cols % 256) return hipErrorInvalidValue;
+    if (t == T_Q8K && L.cols % 256) return hipErrorInvalidValue;
     if (generic && t != T_F32 && t != T_F16) return hipErrorInvalidValue;
   }
   if (Epi::kPaired) {
@@ -845,30 +630,16 @@ hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     hipLaunchKernelGGL(k_gemv_generic<Epi>, dim3(blocks), dim3(kThreads), lds, st, a, epi);
     return hipGetLastError();
   }
-  // segments of the first type decode with FragA, the others with FragB
+  // one type per launch on this path (the mixed Q4_K / Q6_K layers take the MFMA kernel)
   const uint32_t ta = L.seg[0].type;
-  uint32_t tb = ta;
-  for (int s = 0; s < a.nseg; s++)
-    if (L.seg[s].type != ta) {
-      if (tb != ta && L.seg[s].type != tb) return hipErrorInvalidValue;  // at most two types
-      tb = L.seg[s].type;
-      a.use_b |= 1u << s;
-    }
-  if (tb == ta) {
-    switch (ta) {
-      case T_Q4K: return dispatch<Epi, FragQ4K, FragQ4K>(a, epi, blocks, lds, st);
-      case T_Q6K: return dispatch<Epi, FragQ6K, FragQ6K>(a, epi, blocks, lds, st);
-      case T_Q8_0: return dispatch<Epi, FragQ80, FragQ80>(a, epi, blocks, lds, st);
-      case T_Q4_0: return dispatch<Epi, FragQ40, FragQ40>(a, epi, blocks, lds, st);
-      case T_Q8K: return dispatch<Epi, FragQ8K, FragQ8K>(a, epi, blocks, lds, st);
-      case T_F32: return dispatch<Epi, FragF32, FragF32>(a, epi, blocks, lds, st);
-      case T_F16: return dispatch<Epi, FragF16, FragF16>(a, epi, blocks, lds, st);
-      default: return hipErrorInvalidValue;
-    }
-  }
-  switch (ta) {  // mixed Q4_K / Q6_K (Q4_K_M layers)
-    case T_Q4K: return dispatch_b<Epi, FragQ4K>(a, tb, epi, blocks, lds, st);
-    case T_Q6K: return dispatch_b<Epi, FragQ6K>(a, tb, epi, blocks, lds, st);
+  for (int s = 1; s < a.nseg; s++)
+    if (L.seg[s].type != ta) return hipErrorInvalidValue;
+  switch (ta) {
+    case T_Q8_0: return dispatch<Epi, FragQ80>(a, epi, blocks, lds, st);
+    case T_Q4_0: return dispatch<Epi, FragQ40>(a, epi, blocks, lds, st);
+    case T_Q8K: return dispatch<Epi, FragQ8K>(a, epi, blocks, lds, st);
+    case T_F32: return dispatch<Epi, FragF32>(a, epi, blocks, lds, st);
+    case T_F16: return dispatch<Epi, FragF16>(a, epi, blocks, lds, st);
     default: return hipErrorInvalidValue;
   }
 }

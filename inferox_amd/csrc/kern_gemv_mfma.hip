@@ -1,0 +1,545 @@
+// kern_gemv_mfma.hip — int8-MFMA dequant-GEMV for Q4_K / Q6_K on gfx950.
+//
+// Replaces, for the K-quant matrices of a Q4_K_M model, the decode use of
+// ops::matmul_t (src/ops.rs:33-44,104-134) fed by the f32 dequant of
+// Weights::tensor_f32_by_index (src/gguf/weights.rs:66-74): y = W x with W
+// streamed once in its quantized form.
+//
+// Arithmetic.  The K-quant element is w = a * q - m (Q4_K: a = d * sc,
+// m = dmin * mn, q in 0..15, per 32-element sub-block; Q6_K: a = d * sc,
+// m = 32 a, q in 0..63, per 16-element part), so a row's dot with x is
+// sum over groups of a * (q . x) - m * sum(x).  The integer dot q . x runs on
+// v_mfma_i32_16x16x64_i8 with x in fixed point: each 32-element group of x is
+// scaled by 2^(22 - E) (E: the exponent of its largest magnitude), rounded to
+// an integer X with |X| <= 2^22, and split into three signed base-256 digits
+// (X = d0 + 256 d1 + 65536 d2).  The digit sums are exact in int32 and are
+// recombined in f32, so q . x carries one rounding of the 22-bit x and one of
+// the f32 recombination: within a few ulp of an f32 dot product.  sum(x) is
+// taken in f32 from the unrounded x.
+//
+// MFMA mapping (16x16x64, A-lane i + 16g byte b meets B-lane j + 16g byte b;
+// result C[i][j] in lane j + 16 (i / 4), register i % 4):
+//   * B = weights.  Tiles are 16 rows; B-lane n + 16g holds 16 quants of row n
+//     from group g's part (tiled device layout, ifx_common.h), unpacked from
+//     nibbles (and Q6_K high bits) into bytes in the order
+//     0 2 4 6 1 3 5 7 8 10 12 14 9 11 13 15 that two mask/shift steps give.
+//   * A = x digits, staged in LDS by the workgroup prologue in the same order.
+//     A-row 4g + d (d < 3) holds digit d of the x part that B-group g uses and
+//     zero elsewhere, so lane n + 16g of C receives, in registers 0..2, the
+//     three digit sums of row n over its own part: the epilogue needs no
+//     cross-lane traffic until the row reduction.
+//   * Per 256-element block a lane runs 4 MFMAs (Q4_K: two accumulate per
+//     sub-block), so the decode costs about one VALU instruction per weight
+//     per lane instead of four for the f32 dot.
+//
+// Work decomposition: persistent workgroups of 8 waves (2 per CU).  An item is
+// one 16-row tile (two for paired gate/up launches, sharing the A reads); its
+// blocks are split over `split` waves and reduced through LDS.  Each wave
+// keeps the loads of D blocks in flight in a ring: block i is computed, then
+// its registers are refilled with the loads of block i + D (which may belong
+// to the next item), so HBM stays busy through reductions and epilogues.
+// Compiled with -ffp-contract=off: only the explicit fmaf below are fused.
+#include <algorithm>
+
+#include "gemv_epi.h"
+
+namespace ifx {
+
+bool mfma_type(uint32_t t) { return t == T_Q4K || t == T_Q6K; }
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlocksPerCu = 2;
+constexpr int kWavesPerSimd = kBlocksPerCu * kWaves / 4;  // 4: at most 128 VGPRs
+constexpr uint32_t kPartBytes = 48;   // 3 digit planes x 16 bytes per 16-element part
+constexpr uint32_t kBlockA = 16 * kPartBytes;  // A bytes of one 256-element block
+constexpr uint32_t kZeroBytes = 512;  // read by the lanes that feed zero A rows
+constexpr uint32_t kM4 = 0x0F0F0F0Fu, kM2 = 0x30303030u;
+
+struct MArgs {
+  GemvSeg seg[3];      // paired: seg[0] gate, seg[1] up
+  uint32_t ntiles[3];  // 16-row tiles per logical segment
+  uint32_t rot[3];     // first-group rotation per segment (balances small segments)
+  uint32_t use_b;      // bit s: segment s has the kernel's second type
+  uint32_t split;      // waves per item: 1, 2, 4 or 8
+  uint32_t steps;      // blocks per wave per item, padded to a multiple of D
+  int nseg;
+  uint32_t cols, nbr;  // nbr = cols / 256
+  const float* x;
+  const float* norm_w;
+  float eps;
+  uint32_t xs_off, zero_off;  // LDS byte offsets (the digit planes start at 0)
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// q . X from the three digit sums (exact int32 each; one f32 rounding per step)
+__device__ __forceinline__ float digits(v4i c) {
+  return fmaf(65536.f, (float)c[2], fmaf(256.f, (float)c[1], (float)c[0]));
+}
+
+// 16 Q4_K nibbles (8 bytes) -> 16 bytes in the A/B element order
+__device__ __forceinline__ v4i nib(uint32_t w0, uint32_t w1) {
+  return v4i{(int)(w0 & kM4), (int)((w0 >> 4) & kM4), (int)(w1 & kM4), (int)((w1 >> 4) & kM4)};
+}
+
+// 16 Q6_K quants: low nibbles (8 bytes) and the part's word of high parts
+__device__ __forceinline__ v4i six(uint32_t l0, uint32_t l1, uint32_t h) {
+  return v4i{(int)((l0 & kM4) | ((h << 4) & kM2)), (int)(((l0 >> 4) & kM4) | ((h << 2) & kM2)),
+             (int)((l1 & kM4) | (h & kM2)), (int)(((l1 >> 4) & kM4) | ((h >> 2) & kM2))};
+}
+
+__device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xffu); }
+
+// One (tile, block) unit of a segment in registers.  dot() returns this lane's
+// share of row (lane & 15)'s dot product over the block: sub-blocks g and
+// g + 4 (g = lane >> 4).  xa / xb: {scale, sum32, sum16 (part 0), sum16
+// (part 1)} of x over those sub-blocks.
+template <int T>
+struct KBuf;
+
+// Q4_K (src/gguf/dequant.rs:133-161): scales/mins of sub-blocks s < 4 are the
+// low 6 bits of bytes s / s + 4; of s >= 4, the nibbles of byte s + 4 with the
+// top bits of bytes s - 4 / s (dequant.rs:141-149).
+template <>
+struct KBuf<T_Q4K> {
+  static constexpr uint64_t kUnit = kUnitQ4K;
+  uint4 h, q0, q1;
+  // u: wave-uniform unit base; 32-bit unsigned lane offsets keep the
+  // scalar-base addressing form (no 64-bit address per lane)
+  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
+    h = *(const uint4*)(u + 16u * (lane & 15u));
+    q0 = *(const uint4*)(u + (256u + 16u * lane));
+    q1 = *(const uint4*)(u + (1280u + 16u * lane));
+  }
+  __device__ __forceinline__ float dot(const v4i* A, float4 xa, float4 xb, int g) const {
+    const v4i z = {0, 0, 0, 0};
+    v4i ca = mfma(A[0], nib(q0.x, q0.y), z);
+    ca = mfma(A[1], nib(q0.z, q0.w), ca);
+    v4i cb = mfma(A[2], nib(q1.x, q1.y), z);
+    cb = mfma(A[3], nib(q1.z, q1.w), cb);
+    const uint32_t sh = 8 * g, y = h.y >> sh, zz = h.z >> sh, w = h.w >> sh;
+    const uint32_t sca = y & 63u, mna = zz & 63u;
+    const uint32_t scb = (w & 15u) | ((y >> 2) & 48u), mnb = ((w >> 4) & 15u) | ((zz >> 2) & 48u);
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    float v = ((d * (float)sca) * xa.x) * digits(ca);
+    v = fmaf(-(dmin * (float)mna), xa.y, v);
+    v = fmaf((d * (float)scb) * xb.x, digits(cb), v);
+    return fmaf(-(dmin * (float)mnb), xb.y, v);
+  }
+};
+
+// Q6_K (reference layout, src/gguf/dequant.rs:165-199): w = (d * sc) * (q - 32).
+template <>
+struct KBuf<T_Q6K> {
+  static constexpr uint64_t kUnit = kUnitQ6K;
+  uint4 l0, l1, hq;
+  uint32_t sc, d;
+  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
+    l0 = *(const uint4*)(u + 16u * lane);
+    l1 = *(const uint4*)(u + (1024u + 16u * lane));
+    hq = *(const uint4*)(u + (2048u + 16u * lane));
+    sc = *(const uint32_t*)(u + (3072u + 4u * lane));
+    d = *(const uint16_t*)(u + (3328u + 2u * (lane & 15u)));
+  }
+  __device__ __forceinline__ float dot(const v4i* A, float4 xa, float4 xb, int) const {
+    const v4i z = {0, 0, 0, 0};
+    const float df = h2f(d);
+    const v4i c0 = mfma(A[0], six(l0.x, l0.y, hq.x), z);
+    const v4i c1 = mfma(A[1], six(l0.z, l0.w, hq.y), z);
+    const v4i c2 = mfma(A[2], six(l1.x, l1.y, hq.z), z);
+    const v4i c3 = mfma(A[3], six(l1.z, l1.w, hq.w), z);
+    float v = (df * cvtb(sc, 0)) * fmaf(xa.x, digits(c0), -32.f * xa.z);
+    v = fmaf(df * cvtb(sc, 1), fmaf(xa.x, digits(c1), -32.f * xa.w), v);
+    v = fmaf(df * cvtb(sc, 2), fmaf(xb.x, digits(c2), -32.f * xb.z), v);
+    return fmaf(df * cvtb(sc, 3), fmaf(xb.x, digits(c3), -32.f * xb.w), v);
+  }
+};
+
+template <int T>
+__device__ __forceinline__ const uint8_t* unit_ptr(const GemvSeg& sg, uint32_t nbr, uint32_t tile, uint32_t b) {
+  return sg.body + ((uint64_t)tile * nbr + b) * KBuf<T>::kUnit;
+}
+
+// ---------------------------------------------------------------------------
+// Prologue: x (optionally RMS-normalised) -> digit planes + group sums in LDS.
+// ---------------------------------------------------------------------------
+
+// rms_norm (src/ops.rs:162-167): scale = 1/sqrt(mean(x^2) + eps); x = (x*scale)*w.
+__device__ __forceinline__ float norm_scale(const MArgs& a, float ss, float* red, int lane, int wave) {
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) tot += red[w];
+  return 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+}
+
+// Chunk c = 8 consecutive elements (half of part c / 2); the 4 threads of a
+// 32-element group are consecutive lanes.  Every lane takes part in the
+// shuffles; only `ok` lanes write.
+__device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool ok, uint8_t* lds, float4* xsum) {
+  float m = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  int e;
+  (void)frexpf(m, &e);  // m < 2^e
+  e = e < -100 ? -100 : e;
+  const float inv = ldexpf(1.f, 22 - e), xs = ldexpf(1.f, e - 22);
+  uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int X = (int)rintf(v[k] * inv);  // |X| <= 2^22
+    const int X1 = (X + 128) >> 8, X2 = (X1 + 128) >> 8;
+    const int sh = 8 * (k >> 1), w = k & 1;  // even elements: word 0, odd: word 1
+    p0[w] |= (uint32_t)(X & 255) << sh;
+    p1[w] |= (uint32_t)(X1 & 255) << sh;
+    p2[w] |= (uint32_t)(X2 & 255) << sh;
+  }
+  const float s8 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  const float s16 = s8 + __shfl_xor(s8, 1, 64);
+  const float s16o = __shfl_xor(s16, 2, 64);
+  if (ok) {
+    uint8_t* dst = lds + (c >> 1) * kPartBytes + 8 * (c & 1);
+    *(uint2*)dst = make_uint2(p0[0], p0[1]);
+    *(uint2*)(dst + 16) = make_uint2(p1[0], p1[1]);
+    *(uint2*)(dst + 32) = make_uint2(p2[0], p2[1]);
+    if ((c & 3) == 0) xsum[c >> 2] = make_float4(xs, s16 + s16o, s16, s16o);
+  }
+}
+
+template <bool NORM>
+__device__ __forceinline__ void stage_digits(const MArgs& a, uint8_t* lds, float* red, int tid, int lane, int wave) {
+  constexpr int kB = NORM ? 2 : 4;  // chunks per thread per batch (x and w in registers)
+  const uint32_t nch = a.cols / 8;
+  const float4* x4 = (const float4*)a.x;
+  const float4* w4 = (const float4*)a.norm_w;
+  float4* xsum = (float4*)(lds + a.xs_off);
+  const bool single = nch <= (uint32_t)(kB * kThreads);
+  float scale = 1.f;
+  if (NORM && !single) {
+    float ss = 0.f;
+    for (uint32_t c = tid; c < nch; c += kThreads) {
+      const float4 u = x4[2 * c], v = x4[2 * c + 1];
+      ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
+      ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+    }
+    scale = norm_scale(a, ss, red, lane, wave);
+  }
+  for (uint32_t base = 0; base < nch; base += kB * kThreads) {
+    float4 xv[kB][2], wv[kB][2];
+#pragma unroll
+    for (int i = 0; i < kB; i++) {
+      const uint32_t c = min(base + tid + i * kThreads, nch - 1);  // clamped: loads stay unconditional
+      xv[i][0] = x4[2 * c];
+      xv[i][1] = x4[2 * c + 1];
+      if (NORM) {
+        wv[i][0] = w4[2 * c];
+        wv[i][1] = w4[2 * c + 1];
+      }
+    }
+    if (NORM && single) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < kB; i++) {
+        if (base + tid + i * kThreads < nch) {
+#pragma unroll
+          for (int hlf = 0; hlf < 2; hlf++) {
+            const float4 u = xv[i][hlf];
+            ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
+          }
+        }
+      }
+      scale = norm_scale(a, ss, red, lane, wave);
+    }
+#pragma unroll
+    for (int i = 0; i < kB; i++) {
+      const uint32_t c = base + tid + i * kThreads;
+      float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w, xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+      if (NORM) {
+        const float w[8] = {wv[i][0].x, wv[i][0].y, wv[i][0].z, wv[i][0].w,
+                            wv[i][1].x, wv[i][1].y, wv[i][1].z, wv[i][1].w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = (v[k] * scale) * w[k];
+      }
+      quantize_chunk(v, c, c < nch, lds, xsum);
+    }
+  }
+  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Main loop
+// ---------------------------------------------------------------------------
+
+template <class Epi, int NT>
+__device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, const MArgs& a, int s, uint32_t tile,
+                                     const float* acc, int lane) {
+  const float v = acc[0];
+  float partner = 0.f;
+  if (Epi::kPaired) partner = acc[NT - 1];
+  else if (Epi::kNeighbor) partner = __shfl_xor(v, 1, 64);
+  const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
+  if (lane < 16 && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner);
+}
+
+// The items of segment s owned by this wave's group (a.split waves of one
+// workgroup): tiles first, first + TG, ..., `iters` of them (the same count for
+// every wave of the workgroup, so that split reductions can use workgroup
+// barriers).  Wave j of the group takes blocks j, j + split, ... of each item.
+// `buf` arrives holding the loads of the wave's first D blocks.
+template <int T, int NT, int D, class Epi>
+__device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s,
+                                        KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t TG, uint32_t iters,
+                                        uint32_t j, const uint8_t* lds, uint32_t a_base, uint32_t a_step,
+                                        float* part, int lane, int wave) {
+  const uint32_t S = a.split, NB = a.steps, nbr = a.nbr, nt = a.ntiles[s];
+  const int g = lane >> 4;
+  const float4* xsum = (const float4*)(lds + a.xs_off) + g;
+  for (uint32_t k = 0; k < iters; k++) {
+    const uint32_t tile = first + k * TG;
+    const bool live = tile < nt;  // uniform over the wave
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.f;
+    for (uint32_t r = 0; r < NB; r += D) {
+#pragma unroll
+      for (int i = 0; i < D; i++) {
+        const uint32_t m = r + i, b = j + S * m;
+        const bool valid = live && b < nbr;
+        const uint32_t bc = min(b, nbr - 1);
+        const uint8_t* ap = lds + a_base + a_step * bc;
+        const v4i A[4] = {*(const v4i*)ap, *(const v4i*)(ap + kPartBytes), *(const v4i*)(ap + 8 * kPartBytes),
+                          *(const v4i*)(ap + 9 * kPartBytes)};
+        const float4 xa = xsum[8 * bc], xb = xsum[8 * bc + 4];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const float v = buf[i][t].dot(A, xa, xb, g);
+          acc[t] += valid ? v : 0.f;
+        }
+        // refill with block m + D of this item, or block i of the next one
+        uint32_t nm = m + D, ntl = tile;
+        if (nm >= NB) {
+          nm -= NB;
+          ntl += TG;
+        }
+        ntl = min(ntl, nt - 1);
+        const uint32_t nb = min(j + S * nm, nbr - 1);
+#pragma unroll
+        for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, ntl, nb), lane);
+        // keep the ring order: the next block's decode may not be hoisted above
+        // these loads (it would wait for every buffer at once)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      acc[t] += __shfl_xor(acc[t], 16, 64);
+      acc[t] += __shfl_xor(acc[t], 32, 64);
+    }
+    if (S > 1) {
+      // partial sums of the group's waves through LDS (double-buffered: one barrier per item)
+      float* pb = part + (k & 1) * (kWaves * 16 * NT);
+      if (lane < 16) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) pb[(wave * NT + t) * 16 + lane] = acc[t];
+      }
+      __syncthreads();
+      if (j == 0 && live) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          float v = 0.f;
+          for (uint32_t q = 0; q < S; q++) v += pb[((wave + q) * NT + t) * 16 + (lane & 15)];
+          acc[t] = v;
+        }
+        emit<Epi, NT>(epi, ws, a, s, tile, acc, lane);
+      }
+    } else if (live) {
+      emit<Epi, NT>(epi, ws, a, s, tile, acc, lane);
+    }
+  }
+}
+
+template <int T, int NT, int D>
+__device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t j,
+                                         int lane) {
+  const uint32_t tile = min(first, a.ntiles[s] - 1);
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    const uint32_t b = min(j + a.split * i, a.nbr - 1);
+#pragma unroll
+    for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane);
+  }
+}
+
+template <class Epi, int TA, int TB, int D>
+__global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
+  constexpr int NT = Epi::kPaired ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ float red[kWaves];
+  __shared__ float part[2 * kWaves * 16 * NT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t S = a.split, GPB = kWaves / S, TG = gridDim.x * GPB;
+  const uint32_t tg = blockIdx.x * GPB + wave / S, j = wave % S;
+  // A operand: lane i + 16g feeds row i of the 16x64 A tile within k-range g;
+  // rows 4g..4g+2 carry the digits of group g's part, the rest read zeros
+  const int ai = lane & 15, ag = lane >> 4;
+  const bool active = (ai >> 2) == ag && (ai & 3) < 3;
+  const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : a.zero_off;
+  const uint32_t a_step = active ? kBlockA : 0u;
+  typename Epi::Wave ws;
+  // items per group of this workgroup for segment s: the count of its busiest group
+  auto block_iters = [&](int s) -> uint32_t {
+    uint32_t n = 0;
+    for (uint32_t q = 0; q < GPB; q++) {
+      const uint32_t f0 = (blockIdx.x * GPB + q + TG - a.rot[s]) % TG;
+      if (f0 < a.ntiles[s]) n = max(n, (a.ntiles[s] - 1 - f0) / TG + 1);
+    }
+    return n;
+  };
+  {
+    const uint32_t first = (tg + TG - a.rot[0]) % TG;
+    KBuf<TA> buf[D][NT];
+    prefetch<TA, NT, D>(a, 0, buf, first, j, lane);  // in flight while x is staged
+    if (a.norm_w) stage_digits<true>(a, lds, red, tid, lane, wave);
+    else stage_digits<false>(a, lds, red, tid, lane, wave);
+    run_seg<TA, NT, D, Epi>(a, epi, ws, 0, buf, first, TG, block_iters(0), j, lds, a_base, a_step, part, lane,
+                            wave);
+  }
+  for (int s = 1; s < a.nseg; s++) {
+    const uint32_t first = (tg + TG - a.rot[s]) % TG;
+    const uint32_t iters = block_iters(s);
+    if (iters == 0) continue;
+    if (TA != TB && ((a.use_b >> s) & 1u)) {
+      KBuf<TB> buf[D][NT];
+      prefetch<TB, NT, D>(a, s, buf, first, j, lane);
+      run_seg<TB, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+    } else {
+      KBuf<TA> buf[D][NT];
+      prefetch<TA, NT, D>(a, s, buf, first, j, lane);
+      run_seg<TA, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+    }
+  }
+  epi.finish(ws, lane);
+}
+
+int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+    if (n <= 0) n = 256;
+  }
+  return n;
+}
+
+template <class Epi, int TA, int TB, int D>
+hipError_t go(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
+  static bool opted = false;
+  if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns
+    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    opted = true;
+  }
+  hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
+  return hipGetLastError();
+}
+
+template <class Epi, int D>
+hipError_t go_types(const MArgs& a, uint32_t ta, uint32_t tb, const Epi& epi, uint32_t blocks, size_t lds,
+                    hipStream_t st) {
+  if (ta == T_Q4K && tb == T_Q4K) return go<Epi, T_Q4K, T_Q4K, D>(a, epi, blocks, lds, st);
+  if (ta == T_Q6K && tb == T_Q6K) return go<Epi, T_Q6K, T_Q6K, D>(a, epi, blocks, lds, st);
+  if constexpr (!Epi::kPaired) {  // paired segments share one type
+    if (ta == T_Q4K && tb == T_Q6K) return go<Epi, T_Q4K, T_Q6K, D>(a, epi, blocks, lds, st);
+    if (ta == T_Q6K && tb == T_Q4K) return go<Epi, T_Q6K, T_Q4K, D>(a, epi, blocks, lds, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+template <class Epi>
+hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
+  constexpr int NT = Epi::kPaired ? 2 : 1;
+  if (L.nseg < 1 || L.nseg > 3 || L.cols == 0 || L.cols % 256) return hipErrorInvalidValue;
+  MArgs a{};
+  a.cols = L.cols;
+  a.nbr = L.cols / 256;
+  a.x = L.x;
+  a.norm_w = L.norm_w;
+  a.eps = L.eps;
+  for (int s = 0; s < L.nseg; s++) {
+    if (!mfma_type(L.seg[s].type) || L.seg[s].rows == 0) return hipErrorInvalidValue;
+    a.seg[s] = L.seg[s];
+  }
+  if (Epi::kPaired) {
+    if (L.nseg != 2 || L.seg[0].rows != L.seg[1].rows || L.seg[0].type != L.seg[1].type) return hipErrorInvalidValue;
+    a.nseg = 1;
+  } else {
+    a.nseg = L.nseg;
+  }
+  uint32_t total = 0;
+  for (int s = 0; s < a.nseg; s++) {
+    a.ntiles[s] = (uint32_t)((L.seg[s].rows + kTileRows - 1) / kTileRows);
+    total += a.ntiles[s];
+  }
+  a.xs_off = 3 * a.cols;                    // digit planes: 48 bytes per 16 elements
+  a.zero_off = a.xs_off + a.cols / 2;       // group sums: 16 bytes per 32 elements
+  const size_t lds = a.zero_off + kZeroBytes;
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const uint32_t per_cu = (uint32_t)std::max<size_t>(1, std::min<size_t>(kBlocksPerCu, (160 * 1024) / lds));
+  const uint32_t resident = per_cu * cu_count() * kWaves;
+  uint32_t split = 1;
+  while (split < (uint32_t)kWaves && split < a.nbr && total * split < resident) split *= 2;
+  a.split = split;
+  const uint32_t nbm = (a.nbr + split - 1) / split;
+  const int D = (NT == 2 || nbm <= 2) ? 2 : 4;
+  a.steps = (nbm + D - 1) / D * D;
+  const uint32_t blocks = std::min<uint32_t>((total * split + kWaves - 1) / kWaves, per_cu * cu_count());
+  const uint32_t TG = blocks * (kWaves / split);
+  uint32_t acc = 0;
+  for (int s = 0; s < a.nseg; s++) {
+    a.rot[s] = acc % TG;
+    acc += a.ntiles[s];
+  }
+  const uint32_t ta = L.seg[0].type;
+  uint32_t tb = ta;
+  for (int s = 1; s < a.nseg; s++)
+    if (L.seg[s].type != ta) {
+      tb = L.seg[s].type;
+      a.use_b |= 1u << s;
+    }
+  if constexpr (Epi::kPaired) {
+    return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
+  } else {
+    if (D == 2) return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
+    return go_types<Epi, 4>(a, ta, tb, epi, blocks, lds, st);
+  }
+}
+
+template hipError_t launch_mfma<EpiStore>(const GemvLaunch&, const EpiStore&, hipStream_t);
+template hipError_t launch_mfma<EpiResidual>(const GemvLaunch&, const EpiResidual&, hipStream_t);
+template hipError_t launch_mfma<EpiQkv>(const GemvLaunch&, const EpiQkv&, hipStream_t);
+template hipError_t launch_mfma<EpiSwiglu>(const GemvLaunch&, const EpiSwiglu&, hipStream_t);
+template hipError_t launch_mfma<EpiLogits>(const GemvLaunch&, const EpiLogits&, hipStream_t);
+
+}  // namespace ifx
