@@ -1,11 +1,14 @@
 // gemv_epi.h — row epilogues shared by the GEMV kernels (kern_gemv.hip,
 // kern_gemv_mfma.hip).
 //
-// A kernel calls row(ws, s, r, v, partner) once per real row r of segment s
-// of a finished tile, on the lane that holds the row's sum v.  `partner` is
-// the sum of row r ^ 1 (kNeighbor: the RoPE pair) or, for paired launches,
-// the second segment's sum of row r (gate/up).  finish(ws, lane) runs once
-// per wave at the end of the kernel, on every lane.
+// Per wave, a kernel calls begin(ws) once at its start (uniform state reads
+// issued early), pre(ws, s, r) when it starts an item, on the lane that will
+// own row r (global reads the epilogue needs, in flight while the item's
+// weights are decoded), and row(ws, s, r, v, partner, pre) once per real row
+// r of segment s of the finished item, on the lane that holds the row's sum v.
+// `partner` is the sum of row r ^ 1 (kNeighbor: the RoPE pair) or, for paired
+// launches, the second segment's sum of row r (gate/up).  finish(ws, lane)
+// runs once per wave at the end of the kernel, on every lane.
 // Compiled with -ffp-contract=off.
 #pragma once
 
@@ -18,7 +21,10 @@ struct EpiStore {
   float* y;
   uint32_t seg_out[3];  // output offset of each segment
   struct Wave {};
-  __device__ void row(Wave&, int s, uint32_t r, float v, float) const { y[seg_out[s] + r] = v; }
+  struct Pre {};
+  __device__ void begin(Wave&) const {}
+  __device__ Pre pre(const Wave&, int, uint32_t) const { return Pre{}; }
+  __device__ void row(Wave&, int s, uint32_t r, float v, float, const Pre&) const { y[seg_out[s] + r] = v; }
   __device__ void finish(Wave&, int) const {}
 };
 
@@ -27,7 +33,12 @@ struct EpiResidual {
   static constexpr bool kPaired = false, kNeighbor = false;
   float* h;
   struct Wave {};
-  __device__ void row(Wave&, int, uint32_t r, float v, float) const { h[r] = v + h[r]; }
+  struct Pre {
+    float h;
+  };
+  __device__ void begin(Wave&) const {}
+  __device__ Pre pre(const Wave&, int, uint32_t r) const { return Pre{h[r]}; }
+  __device__ void row(Wave&, int, uint32_t r, float v, float, const Pre& p) const { h[r] = v + p.h; }
   __device__ void finish(Wave&, int) const {}
 };
 
@@ -36,19 +47,34 @@ struct EpiResidual {
 struct EpiQkv {
   static constexpr bool kPaired = false, kNeighbor = true;
   QkvEpi e;
-  struct Wave {};
-  __device__ void row(Wave&, int s, uint32_t r, float v, float other) const {
+  struct Wave {
+    uint32_t len, pos;  // cache row of the new key/value, RoPE position
+  };
+  struct Pre {
+    float2 cs;  // (cos, sin) of the row's RoPE pair, q and k rows inside rope_dim
+  };
+  __device__ void begin(Wave& w) const {
+    w.len = e.state->len;
+    w.pos = e.state->rope_pos;
+  }
+  __device__ Pre pre(const Wave& w, int s, uint32_t r) const {
+    Pre p{make_float2(1.f, 0.f)};
+    const uint32_t i = r % e.head_dim;
+    if (s < 2 && i < e.rope_dim) p.cs = e.rope_cs[(uint64_t)w.pos * (e.rope_dim / 2) + i / 2];
+    return p;
+  }
+  __device__ void row(Wave& w, int s, uint32_t r, float v, float other, const Pre& p) const {
     if (s < 2) {
       const uint32_t i = r % e.head_dim;
       if (i < e.rope_dim) {
-        const float2 cs = e.rope_cs[(uint64_t)e.state->rope_pos * (e.rope_dim / 2) + i / 2];
+        const float2 cs = p.cs;
         v = (i & 1) ? (other * cs.y + v * cs.x) : (v * cs.x - other * cs.y);
       }
     }
     if (s == 0) {
       e.q_out[r] = v;
     } else {
-      const uint64_t off = (uint64_t)e.state->len * e.kv_dim + r;
+      const uint64_t off = (uint64_t)w.len * e.kv_dim + r;
       if (s == 1) e.k_cache[off] = v;
       else e.v_cache[off] = v;
     }
@@ -61,7 +87,10 @@ struct EpiSwiglu {
   static constexpr bool kPaired = true, kNeighbor = false;
   float* mid;
   struct Wave {};
-  __device__ void row(Wave&, int, uint32_t r, float g, float u) const {
+  struct Pre {};
+  __device__ void begin(Wave&) const {}
+  __device__ Pre pre(const Wave&, int, uint32_t) const { return Pre{}; }
+  __device__ void row(Wave&, int, uint32_t r, float g, float u, const Pre&) const {
     float c = fminf(fmaxf(g, -80.f), 80.f);
     if (g != g) c = g;
     const float sig = 1.0f / (1.0f + expf(-c));
@@ -89,7 +118,10 @@ struct EpiLogits {
     unsigned long long best = 0;
     bool nan = false;
   };
-  __device__ void row(Wave& w, int, uint32_t r, float v, float) const {
+  struct Pre {};
+  __device__ void begin(Wave&) const {}
+  __device__ Pre pre(const Wave&, int, uint32_t) const { return Pre{}; }
+  __device__ void row(Wave& w, int, uint32_t r, float v, float, const Pre&) const {
     logits[r] = v;
     if (v != v) w.nan = true;
     const unsigned long long k = argmax_key(v, r);

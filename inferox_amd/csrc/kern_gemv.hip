@@ -289,7 +289,8 @@ __device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, con
     if (rr.ok) {
       const float v = lane_acc(acc, lane);
       const float partner = P ? lane_acc(acc, lane + kR / 2) : (Epi::kNeighbor ? lane_acc(acc, lane ^ 1) : 0.f);
-      epi.row(ws, P ? 0 : s, (uint32_t)rr.row, v, partner);
+      const int es = P ? 0 : s;
+      epi.row(ws, es, (uint32_t)rr.row, v, partner, epi.pre(ws, es, (uint32_t)rr.row));
     }
   }
 }
@@ -467,6 +468,7 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv(KArgs a, Epi e
   const uint32_t S = a.split, GPB = kWaves / S, TG = gridDim.x * GPB;
   const uint32_t tg = blockIdx.x * GPB + wave / S, j = wave % S;
   typename Epi::Wave ws;
+  epi.begin(ws);
   // tiles per group of this workgroup for segment s: the count of its busiest group
   auto block_iters = [&](int s) -> uint32_t {
     uint32_t n = 0;
@@ -516,6 +518,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(KArgs a, Epi epi) {
   stage_x_generic(a, lds, red, tid, lane, wave);
   const uint32_t W = gridDim.x * kWaves, wid = blockIdx.x * kWaves + wave;
   typename Epi::Wave ws;
+  epi.begin(ws);
   for (int s = 0; s < a.nseg; s++) {
     for (uint32_t t = (wid + W - a.rot[s]) % W; t < a.ntiles[s]; t += W) {
       float acc[kR] = {0.f, 0.f, 0.f, 0.f};

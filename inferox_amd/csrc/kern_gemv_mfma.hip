@@ -223,26 +223,18 @@ __device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool 
   }
 }
 
+// The prologue in two halves, so that a workgroup issues its x (and norm
+// weight) loads before the weight prefetch: loads return in issue order, and
+// staging must not wait for the prefetched weights.
 template <bool NORM>
-__device__ __forceinline__ void stage_digits(const MArgs& a, uint8_t* lds, float* red, int tid, int lane, int wave) {
-  constexpr int kB = NORM ? 2 : 4;  // chunks per thread per batch (x and w in registers)
-  const uint32_t nch = a.cols / 8;
-  const float4* x4 = (const float4*)a.x;
-  const float4* w4 = (const float4*)a.norm_w;
-  float4* xsum = (float4*)(lds + a.xs_off);
-  const bool single = nch <= (uint32_t)(kB * kThreads);
-  float scale = 1.f;
-  if (NORM && !single) {
-    float ss = 0.f;
-    for (uint32_t c = tid; c < nch; c += kThreads) {
-      const float4 u = x4[2 * c], v = x4[2 * c + 1];
-      ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
-      ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
-    }
-    scale = norm_scale(a, ss, red, lane, wave);
-  }
-  for (uint32_t base = 0; base < nch; base += kB * kThreads) {
-    float4 xv[kB][2], wv[kB][2];
+struct XStage {
+  static constexpr int kB = NORM ? 2 : 4;  // chunks of 8 elements per thread per batch
+  float4 xv[kB][2], wv[kB][2];
+
+  __device__ __forceinline__ void load(const MArgs& a, uint32_t base, int tid) {
+    const uint32_t nch = a.cols / 8;
+    const float4* x4 = (const float4*)a.x;
+    const float4* w4 = (const float4*)a.norm_w;
 #pragma unroll
     for (int i = 0; i < kB; i++) {
       const uint32_t c = min(base + tid + i * kThreads, nch - 1);  // clamped: loads stay unconditional
@@ -253,20 +245,11 @@ __device__ __forceinline__ void stage_digits(const MArgs& a, uint8_t* lds, float
         wv[i][1] = w4[2 * c + 1];
       }
     }
-    if (NORM && single) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < kB; i++) {
-        if (base + tid + i * kThreads < nch) {
-#pragma unroll
-          for (int hlf = 0; hlf < 2; hlf++) {
-            const float4 u = xv[i][hlf];
-            ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
-          }
-        }
-      }
-      scale = norm_scale(a, ss, red, lane, wave);
-    }
+  }
+
+  __device__ __forceinline__ void quantize(const MArgs& a, uint32_t base, float scale, uint8_t* lds, int tid) {
+    const uint32_t nch = a.cols / 8;
+    float4* xsum = (float4*)(lds + a.xs_off);
 #pragma unroll
     for (int i = 0; i < kB; i++) {
       const uint32_t c = base + tid + i * kThreads;
@@ -280,9 +263,43 @@ __device__ __forceinline__ void stage_digits(const MArgs& a, uint8_t* lds, float
       quantize_chunk(v, c, c < nch, lds, xsum);
     }
   }
-  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
-  __syncthreads();
-}
+
+  // after load(a, 0, tid): norm scale, digit planes and group sums of all of x
+  __device__ __forceinline__ void finish(const MArgs& a, uint8_t* lds, float* red, int tid, int lane, int wave) {
+    const uint32_t nch = a.cols / 8, step = kB * kThreads;
+    float scale = 1.f;
+    if (NORM) {
+      float ss = 0.f;
+      if (nch <= step) {  // x is in registers
+#pragma unroll
+        for (int i = 0; i < kB; i++) {
+          if (tid + i * kThreads < nch) {
+#pragma unroll
+            for (int hlf = 0; hlf < 2; hlf++) {
+              const float4 u = xv[i][hlf];
+              ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
+            }
+          }
+        }
+      } else {
+        const float4* x4 = (const float4*)a.x;
+        for (uint32_t c = tid; c < nch; c += kThreads) {
+          const float4 u = x4[2 * c], v = x4[2 * c + 1];
+          ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
+          ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+        }
+      }
+      scale = norm_scale(a, ss, red, lane, wave);
+    }
+    quantize(a, 0, scale, lds, tid);
+    for (uint32_t base = step; base < nch; base += step) {
+      load(a, base, tid);
+      quantize(a, base, scale, lds, tid);
+    }
+    if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Main loop
@@ -290,13 +307,13 @@ __device__ __forceinline__ void stage_digits(const MArgs& a, uint8_t* lds, float
 
 template <class Epi, int NT>
 __device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, const MArgs& a, int s, uint32_t tile,
-                                     const float* acc, int lane) {
+                                     const float* acc, const typename Epi::Pre& pre, int lane) {
   const float v = acc[0];
   float partner = 0.f;
   if (Epi::kPaired) partner = acc[NT - 1];
   else if (Epi::kNeighbor) partner = __shfl_xor(v, 1, 64);
   const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
-  if (lane < 16 && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner);
+  if (lane < 16 && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner, pre);
 }
 
 // The items of segment s owned by this wave's group (a.split waves of one
@@ -315,6 +332,12 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
   for (uint32_t k = 0; k < iters; k++) {
     const uint32_t tile = first + k * TG;
     const bool live = tile < nt;  // uniform over the wave
+    // the epilogue's global reads, in flight while the item is decoded
+    typename Epi::Pre pre{};
+    {
+      const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
+      if (live && lane < 16 && r < a.seg[s].rows) pre = epi.pre(ws, Epi::kPaired ? 0 : s, r);
+    }
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.f;
@@ -368,28 +391,55 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
           for (uint32_t q = 0; q < S; q++) v += pb[((wave + q) * NT + t) * 16 + (lane & 15)];
           acc[t] = v;
         }
-        emit<Epi, NT>(epi, ws, a, s, tile, acc, lane);
+        emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
       }
     } else if (live) {
-      emit<Epi, NT>(epi, ws, a, s, tile, acc, lane);
+      emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
     }
   }
 }
 
+// Loads of the wave's blocks i0..i1-1 (ring slots) of the first item.
 template <int T, int NT, int D>
 __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t j,
-                                         int lane) {
+                                         int lane, int i0 = 0, int i1 = D) {
   const uint32_t tile = min(first, a.ntiles[s] - 1);
 #pragma unroll
   for (int i = 0; i < D; i++) {
+    if (i < i0 || i >= i1) continue;
     const uint32_t b = min(j + a.split * i, a.nbr - 1);
 #pragma unroll
     for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane);
   }
 }
 
-template <class Epi, int TA, int TB, int D>
-__global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
+// Segment s0 (the workgroup's first segment with work): x loads, the loads of
+// the wave's first block, staging, the loads of its next D - 1 blocks, then
+// the segment.  Weight loads issued before staging delay x behind them in the
+// memory queues (GPU-wide, not only per CU); one block each is enough to have
+// the first step's data arrive with x.
+template <bool NORM, int T, int NT, int D, class Epi>
+__device__ __forceinline__ void lead(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s0, uint32_t first,
+                                     uint32_t TG, uint32_t iters, uint32_t j, uint8_t* lds, float* red,
+                                     uint32_t a_base, uint32_t a_step, float* part, int tid, int lane, int wave) {
+  XStage<NORM> xs;
+  xs.load(a, 0, tid);
+  // every wave's x loads enter the CU's memory queues before any weight load
+  // (a bare barrier: nothing waits for the loads here)
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  KBuf<T> buf[D][NT];
+  prefetch<T, NT, D>(a, s0, buf, first, j, lane, 0, 1);
+  xs.finish(a, lds, red, tid, lane, wave);
+  prefetch<T, NT, D>(a, s0, buf, first, j, lane, 1, D);
+  run_seg<T, NT, D, Epi>(a, epi, ws, s0, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+}
+
+// D > 4 (a deep ring for launches of at most one workgroup per CU) trades
+// occupancy for registers: 2 waves per SIMD, up to 256 VGPRs.
+template <class Epi, int TA, int TB, int D, bool NORM>
+__global__ void __launch_bounds__(kThreads, D > 4 ? 2 : kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
   constexpr int NT = Epi::kPaired ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float red[kWaves];
@@ -404,6 +454,7 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
   const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : a.zero_off;
   const uint32_t a_step = active ? kBlockA : 0u;
   typename Epi::Wave ws;
+  epi.begin(ws);
   // items per group of this workgroup for segment s: the count of its busiest group
   auto block_iters = [&](int s) -> uint32_t {
     uint32_t n = 0;
@@ -413,16 +464,16 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
     }
     return n;
   };
-  {
-    const uint32_t first = (tg + TG - a.rot[0]) % TG;
-    KBuf<TA> buf[D][NT];
-    prefetch<TA, NT, D>(a, 0, buf, first, j, lane);  // in flight while x is staged
-    if (a.norm_w) stage_digits<true>(a, lds, red, tid, lane, wave);
-    else stage_digits<false>(a, lds, red, tid, lane, wave);
-    run_seg<TA, NT, D, Epi>(a, epi, ws, 0, buf, first, TG, block_iters(0), j, lds, a_base, a_step, part, lane,
-                            wave);
+  int s0 = 0;  // uniform over the workgroup
+  while (s0 < a.nseg && block_iters(s0) == 0) s0++;
+  if (s0 < a.nseg) {
+    const uint32_t first = (tg + TG - a.rot[s0]) % TG, iters = block_iters(s0);
+    if (TA != TB && ((a.use_b >> s0) & 1u))
+      lead<NORM, TB, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
+    else
+      lead<NORM, TA, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
   }
-  for (int s = 1; s < a.nseg; s++) {
+  for (int s = s0 + 1; s < a.nseg; s++) {
     const uint32_t first = (tg + TG - a.rot[s]) % TG;
     const uint32_t iters = block_iters(s);
     if (iters == 0) continue;
@@ -450,17 +501,23 @@ int cu_count() {
   return n;
 }
 
-template <class Epi, int TA, int TB, int D>
-hipError_t go(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
+template <class Epi, int TA, int TB, int D, bool NORM>
+hipError_t go_one(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
   static bool opted = false;
   if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns
-    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     opted = true;
   }
-  hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
+  hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D, NORM>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
   return hipGetLastError();
+}
+
+template <class Epi, int TA, int TB, int D>
+hipError_t go(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
+  if (a.norm_w) return go_one<Epi, TA, TB, D, true>(a, epi, blocks, lds, st);
+  return go_one<Epi, TA, TB, D, false>(a, epi, blocks, lds, st);
 }
 
 template <class Epi, int D>
@@ -468,7 +525,9 @@ hipError_t go_types(const MArgs& a, uint32_t ta, uint32_t tb, const Epi& epi, ui
                     hipStream_t st) {
   if (ta == T_Q4K && tb == T_Q4K) return go<Epi, T_Q4K, T_Q4K, D>(a, epi, blocks, lds, st);
   if (ta == T_Q6K && tb == T_Q6K) return go<Epi, T_Q6K, T_Q6K, D>(a, epi, blocks, lds, st);
-  if constexpr (!Epi::kPaired) {  // paired segments share one type
+  // mixed launches (a Q4_K_M layer's QKV: Q4_K q/k, Q6_K v) run the 2-deep
+  // ring: two buffer types in one kernel leave no registers for a deeper one
+  if constexpr (!Epi::kPaired && D == 2) {
     if (ta == T_Q4K && tb == T_Q6K) return go<Epi, T_Q4K, T_Q6K, D>(a, epi, blocks, lds, st);
     if (ta == T_Q6K && tb == T_Q4K) return go<Epi, T_Q6K, T_Q4K, D>(a, epi, blocks, lds, st);
   }
@@ -512,9 +571,12 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   while (split < (uint32_t)kWaves && split < a.nbr && total * split < resident) split *= 2;
   a.split = split;
   const uint32_t nbm = (a.nbr + split - 1) / split;
-  const int D = (NT == 2 || nbm <= 2) ? 2 : 4;
-  a.steps = (nbm + D - 1) / D * D;
   const uint32_t blocks = std::min<uint32_t>((total * split + kWaves - 1) / kWaves, per_cu * cu_count());
+  // ring depth: every block of an item in flight at once where registers allow
+  bool mixed = false;
+  for (int s = 1; s < a.nseg; s++) mixed |= L.seg[s].type != L.seg[0].type;
+  const int D = (NT == 2 || mixed || nbm <= 2) ? 2 : (nbm > 4 && blocks <= (uint32_t)cu_count()) ? 8 : 4;
+  a.steps = (nbm + D - 1) / D * D;
   const uint32_t TG = blocks * (kWaves / split);
   uint32_t acc = 0;
   for (int s = 0; s < a.nseg; s++) {
@@ -532,6 +594,7 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
   } else {
     if (D == 2) return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
+    if (D == 8) return go_types<Epi, 8>(a, ta, tb, epi, blocks, lds, st);
     return go_types<Epi, 4>(a, ta, tb, epi, blocks, lds, st);
   }
 }
