@@ -55,7 +55,6 @@ struct ifx_session {
   float *kc = nullptr, *vc = nullptr;
   float *hidden = nullptr, *q = nullptr, *attn = nullptr, *mid = nullptr, *logits = nullptr;
   float* partial = nullptr;
-  uint32_t* counters = nullptr;
   float2* rope_cs = nullptr;
   DevState* state = nullptr;
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
@@ -202,7 +201,7 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       return IFX_OK;
     }
     case 2: {
-      AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
+      AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
       IFX_HIP(launch_attn_decode(a, st));
       return IFX_OK;
@@ -452,7 +451,6 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   A((void**)&s->mid, F * 4);
   A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
   A((void**)&s->partial, (uint64_t)c.n_kv_heads * s->max_chunks * attn_partial_floats(G, c.head_dim) * 4);
-  A((void**)&s->counters, c.n_kv_heads * 4);
   A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
   A((void**)&s->state, sizeof(DevState));
   A((void**)&s->out_tokens, max_seq_len * 4);
@@ -482,7 +480,6 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   init.out_cap = (uint32_t)max_seq_len;
   if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(s->counters, 0, c.n_kv_heads * 4) != hipSuccess ||
       hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
       hipMemset(s->vc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
@@ -760,7 +757,7 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
     }
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
       hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
-      AttnArgs a{Q + t * D, kc, vc, A + t * D, s->partial, s->counters, s->state, (uint32_t)c.n_heads,
+      AttnArgs a{Q + t * D, kc, vc, A + t * D, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
       hip(launch_attn_decode(a, st));
     }

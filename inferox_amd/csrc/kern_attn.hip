@@ -8,9 +8,10 @@
 // cache rows for all `group` query heads that share it, so each K/V row is read
 // from HBM once per token.  All K and V loads of the chunk are issued before the
 // first wait, so a workgroup costs one memory round trip.  It writes a partial
-// record (unnormalised o, running max, sum) for its chunk; the last workgroup to
-// finish a kv head (agent-scope counter) merges the records with the usual
-// max-rescaling and resets the counter for the next launch.
+// record (unnormalised o, running max, sum) for its chunk.  A second launch,
+// one workgroup per query head, merges the records with the usual
+// max-rescaling (a kernel boundary publishes them: no counters or fences,
+// which cost more than the launch on this part).
 // The cache rows attended are [attn_lo, len] (or [attn_lo, attn_end)), read
 // from the session state, so the launch is identical for every token.
 #include "kernels.h"
@@ -24,10 +25,7 @@ constexpr int kChunk = 64;       // cache rows per workgroup (4 threads per row 
 constexpr int kMaxGroup = 8;
 constexpr int kMaxHd = 256;
 constexpr int kMaxMerge = 256;   // chunks per kv head (max_seq <= kMaxMerge * kChunk)
-constexpr int kMergeBatch = 24;  // partial rows loaded together per merging thread
-// true: the last workgroup of each kv head merges the chunk records (counter +
-// release/acquire); false: a second launch merges them
-constexpr bool kFusedMerge = false;
+constexpr int kMergeBatch = 8;   // partial o loads in flight per merging thread
 
 __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
   acc.x = fmaf(w, v.x, acc.x);
@@ -78,100 +76,6 @@ __device__ __forceinline__ float quad_sum(float v) {
 
 constexpr int kRowsPerWave = kChunk / (kThreads / 64);  // 16
 
-// Combines the chunk records of kv head hk into the attention output: weights
-// w_c = exp(m_c - M) / sum_c l_c w_c over the chunks c (the usual max rescaling).
-template <int HDT, int GT>
-__device__ __forceinline__ void merge_head(const AttnArgs& a, uint32_t hk, uint32_t nch, float* cw, float* lstat,
-                                           float4* red) {
-  constexpr int GM = GT > 0 ? GT : kMaxGroup;
-  const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
-  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
-  const uint32_t rec = attn_partial_floats(G, HD);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* base = a.partial + (uint64_t)hk * a.max_chunks * rec;
-  const uint32_t items = G * nc4;
-  const uint32_t nsplit = items >= (uint32_t)kThreads ? 1u : kThreads / items;
-  const uint32_t sp = tid / items, item0 = tid % items;
-  // first batch of partial o rows in flight while the chunk weights are formed
-  float4 ov[kMergeBatch];
-  if (sp < nsplit) {
-#pragma unroll
-    for (int k = 0; k < kMergeBatch; k++) {
-      const uint32_t cc = min(sp + nsplit * k, nch - 1);
-      ov[k] = ((const float4*)(base + (uint64_t)cc * rec))[item0];
-    }
-  }
-  // weights w_c = exp(m_c - M) and den = sum_c l_c w_c, one wave per query
-  // head; the loads are clamped to real chunks (no branches around them)
-#pragma unroll
-  for (int gg = 0; gg < (GM + 3) / 4; gg++) {
-    const uint32_t g = wave + 4 * gg;
-    if (g >= G) break;
-    float m[kMaxMerge / 64], l[kMaxMerge / 64];
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMaxMerge / 64; j++) {
-      const uint32_t cc = lane + 64 * j;
-      const uint64_t at = (uint64_t)min(cc, nch - 1) * rec + G * HD;
-      const float mv = base[at + g];
-      m[j] = cc < nch ? mv : -INFINITY;
-      l[j] = base[at + G + g];
-      M = fmaxf(M, m[j]);
-    }
-    M = wave_max_dpp(M);
-    float den = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMaxMerge / 64; j++) {
-      const uint32_t cc = lane + 64 * j;
-      const float w = cc < nch ? expf(m[j] - M) : 0.f;
-      cw[g * kMaxMerge + cc] = w;
-      den = fmaf(l[j], w, den);
-    }
-    den = wave_sum_dpp(den);
-    if (lane == 0) lstat[g] = den;
-  }
-  __syncthreads();
-  // o_g = sum_c w_c o_c / den: thread (split sp, float4 item), splits summed in LDS
-  for (uint32_t item = item0; item < items; item += kThreads) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (sp < nsplit) {
-      const uint32_t g = item / nc4;
-      for (uint32_t c0 = sp;; c0 += nsplit * kMergeBatch) {
-        if (item != item0 || c0 != sp) {
-#pragma unroll
-          for (int k = 0; k < kMergeBatch; k++) {
-            const uint32_t cc = min(c0 + nsplit * k, nch - 1);
-            ov[k] = ((const float4*)(base + (uint64_t)cc * rec))[item];
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < kMergeBatch; k++) {
-          const uint32_t cc = c0 + nsplit * k;
-          if (cc < nch) acc = fma4(cw[g * kMaxMerge + cc], ov[k], acc);
-        }
-        if (c0 + nsplit * kMergeBatch >= nch) break;
-      }
-    }
-    if (nsplit > 1) {
-      if (sp < nsplit) red[sp * items + item] = acc;
-    } else {
-      const float den = lstat[item / nc4];
-      ((float4*)(a.out + (uint64_t)hk * G * HD))[item] =
-          make_float4(acc.x / den, acc.y / den, acc.z / den, acc.w / den);
-    }
-  }
-  if (nsplit > 1) {
-    __syncthreads();
-    if ((uint32_t)tid < items) {
-      float4 acc = red[tid];
-      for (uint32_t q = 1; q < nsplit; q++) acc = add4(acc, red[q * items + tid]);
-      const float den = lstat[tid / nc4];
-      ((float4*)(a.out + (uint64_t)hk * G * HD))[tid] =
-          make_float4(acc.x / den, acc.y / den, acc.z / den, acc.w / den);
-    }
-  }
-}
-
 // HDT: the head dim when > 0 (register arrays sized exactly), 0 for any
 // multiple of 4 up to kMaxHd.  GT: the query heads per kv head when > 0, 0 for
 // any up to kMaxGroup.  With both fixed the unrolled loops carry no branches.
@@ -183,7 +87,7 @@ __device__ __forceinline__ void merge_head(const AttnArgs& a, uint32_t hk, uint3
 //   p . V   lane = columns 2l, 2l+1 (+128 j) of all 16 rows, the row weights
 //           broadcast with readlane: no cross-lane reduction.
 // The four waves are combined once through LDS into the chunk's record.
-template <int HDT, int GT, bool FUSED>
+template <int HDT, int GT>
 __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   constexpr int GM = GT > 0 ? GT : kMaxGroup;  // loop bound over query heads
   constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;      // float4 per head row
@@ -192,10 +96,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   __shared__ float4 qs[GM * NC4M];
   __shared__ float wst[kThreads / 64][2][GM];                      // per wave: max, sum
   __shared__ float2 wo[kThreads / 64][GM][NC4M * 2];               // per wave: unnormalised o
-  __shared__ float4 red[kThreads];                                 // merge: split partial sums
-  __shared__ float lstat[GM];
-  __shared__ float cw[GM * kMaxMerge];
-  __shared__ int is_last;
+  __shared__ __attribute__((aligned(16))) float es[kThreads / 64][kRowsPerWave][GM];  // per wave: row weights
 
   const uint32_t c = blockIdx.x, hk = blockIdx.y;
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
@@ -245,25 +146,37 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   const float rs = sqrtf((float)HD);
   float e_row[GM];  // exp(s - m_wave) of this lane's row, per query head
   float m_w[GM], l_w[GM];
+  // the query heads' dot products advance together: each LDS round trip for q
+  // feeds GM independent FMA chains (one chain per head would wait for every read)
+  float sg[GM];
+#pragma unroll
+  for (int g = 0; g < GM; g++) sg[g] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const uint32_t ch = kq + 4 * i;
+    if (ch < nc4) {
+      float4 qv[GM];
+#pragma unroll
+      for (int g = 0; g < GM; g++)
+        if (g < (int)G) qv[g] = qs[g * nc4 + ch];
+#pragma unroll
+      for (int g = 0; g < GM; g++) {
+        if (g < (int)G) {
+          sg[g] = fmaf(qv[g].x, kr[i].x, sg[g]);
+          sg[g] = fmaf(qv[g].y, kr[i].y, sg[g]);
+          sg[g] = fmaf(qv[g].z, kr[i].z, sg[g]);
+          sg[g] = fmaf(qv[g].w, kr[i].w, sg[g]);
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int g = 0; g < GM; g++) {
     e_row[g] = 0.f;
     m_w[g] = -INFINITY;
     l_w[g] = 0.f;
     if (g < (int)G) {
-      float sg = 0.f;
-#pragma unroll
-      for (int i = 0; i < KPT; i++) {
-        const uint32_t ch = kq + 4 * i;
-        if (ch < nc4) {
-          const float4 qv = qs[g * nc4 + ch];
-          sg = fmaf(qv.x, kr[i].x, sg);
-          sg = fmaf(qv.y, kr[i].y, sg);
-          sg = fmaf(qv.z, kr[i].z, sg);
-          sg = fmaf(qv.w, kr[i].w, sg);
-        }
-      }
-      const float sv = quad_sum(sg) / rs;
+      const float sv = quad_sum(sg[g]) / rs;
       m_w[g] = wave_max_dpp(row_ok ? sv : -INFINITY);
       e_row[g] = row_ok ? expf(sv - m_w[g]) : 0.f;
       l_w[g] = wave_sum_dpp(kq == 0 ? e_row[g] : 0.f);
@@ -271,6 +184,13 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   }
 
   // ---- o = sum_t e_t v_t over the wave's rows (src/model/forward.rs:401-409) ----
+  // The row weights go through LDS (written by each row's first lane, read
+  // back as broadcasts by the whole wave; LDS keeps a wave's accesses in order).
+  if (kq == 0) {
+#pragma unroll
+    for (int g = 0; g < GM; g++)
+      if (g < (int)G) es[wave][lane >> 2][g] = e_row[g];
+  }
   float2 o[GM][VJ];
 #pragma unroll
   for (int g = 0; g < GM; g++)
@@ -278,14 +198,16 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
     for (int jj = 0; jj < VJ; jj++) o[g][jj] = make_float2(0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; r++) {
+    float e[GM];
+#pragma unroll
+    for (int g = 0; g < GM; g++) e[g] = es[wave][r][g];
 #pragma unroll
     for (int g = 0; g < GM; g++) {
       if (g < (int)G) {
-        const float e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_row[g]), 4 * r));
 #pragma unroll
         for (int jj = 0; jj < VJ; jj++) {
-          o[g][jj].x = fmaf(e, vr[r][jj].x, o[g][jj].x);
-          o[g][jj].y = fmaf(e, vr[r][jj].y, o[g][jj].y);
+          o[g][jj].x = fmaf(e[g], vr[r][jj].x, o[g][jj].x);
+          o[g][jj].y = fmaf(e[g], vr[r][jj].y, o[g][jj].y);
         }
       }
     }
@@ -336,40 +258,88 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
     part[G * HD + G + tid] = L;
   }
 
-  if (!FUSED) return;
-  // ---- the last workgroup of this kv head merges all chunks ----
-  // Every wave waits until its partial stores have reached L2; after the
-  // barrier one agent-scope release (an L2 write-back) by wave 0 publishes the
-  // whole record before the counter increment.  One write-back per workgroup
-  // instead of one per wave: these serialise per L2 and dominate otherwise.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (wave == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(&a.counters[hk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (old == nch - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  merge_head<HDT, GT>(a, hk, nch, cw, lstat, red);
-  if (tid == 0) __hip_atomic_store(&a.counters[hk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The merge as its own launch (one workgroup per kv head): the kernel boundary
-// publishes the chunk records, so no counter, fence or L2 write-back is needed.
+// Combines the chunk records of query head h = blockIdx.x (kv head h / G):
+// o_h = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - M), M = max_c m_c
+// (softmax over all cached rows, src/model/forward.rs:398-409, taken chunk by
+// chunk).  Thread (split sp, float4 column): the chunks sp, sp + nsplit, ...;
+// the first batch of o loads is in flight while wave 0 forms the weights.
 template <int HDT, int GT>
 __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
-  constexpr int GM = GT > 0 ? GT : kMaxGroup;
+  __shared__ float cw[kMaxMerge];
+  __shared__ float den_s;
   __shared__ float4 red[kThreads];
-  __shared__ float lstat[GM];
-  __shared__ float cw[GM * kMaxMerge];
+  const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
+  const uint32_t h = blockIdx.x, hk = h / G, g = h % G;
   const uint32_t lo = a.state->attn_lo;
   const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
   const uint32_t nrows = hi > lo ? hi - lo : 0;
   const uint32_t nch = (nrows + kChunk - 1) / kChunk;
   if (nch == 0) return;
-  merge_head<HDT, GT>(a, blockIdx.x, nch, cw, lstat, red);
+  const uint32_t rec = attn_partial_floats(G, HD);
+  const float* base = a.partial + (uint64_t)hk * a.max_chunks * rec;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t nsplit = kThreads / nc4, sp = tid / nc4, col = tid % nc4;
+  const bool worker = sp < nsplit;  // nc4 need not divide the workgroup
+  float4 ov[kMergeBatch];
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; k++) {
+    const uint32_t c = min(min(sp, nsplit - 1) + nsplit * k, nch - 1);  // clamped: loads stay unconditional
+    ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+  }
+  if (wave == 0) {
+    float m[kMaxMerge / 64], l[kMaxMerge / 64];
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMaxMerge / 64; j++) {
+      const uint32_t c = lane + 64 * j;
+      const uint64_t at = (uint64_t)min(c, nch - 1) * rec + G * HD;
+      const float mv = base[at + g];
+      m[j] = c < nch ? mv : -INFINITY;
+      l[j] = base[at + G + g];
+      M = fmaxf(M, m[j]);
+    }
+    M = wave_max_dpp(M);
+    float den = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxMerge / 64; j++) {
+      const uint32_t c = lane + 64 * j;
+      const float w = c < nch ? expf(m[j] - M) : 0.f;
+      cw[c] = w;
+      den = fmaf(l[j], w, den);
+    }
+    den = wave_sum_dpp(den);
+    if (lane == 0) den_s = den;
+  }
+  __syncthreads();
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (worker) {
+    for (uint32_t c0 = sp;; c0 += nsplit * kMergeBatch) {
+      if (c0 != sp) {
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; k++) {
+          const uint32_t c = min(c0 + nsplit * k, nch - 1);
+          ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; k++) {
+        const uint32_t c = c0 + nsplit * k;
+        if (c < nch) acc = fma4(cw[c], ov[k], acc);
+      }
+      if (c0 + nsplit * kMergeBatch >= nch) break;
+    }
+  }
+  red[tid] = acc;
+  __syncthreads();
+  if ((uint32_t)tid < nc4) {
+    float4 o = red[tid];
+    for (uint32_t q = 1; q < nsplit; q++) o = add4(o, red[q * nc4 + tid]);
+    const float den = den_s;
+    ((float4*)(a.out + (uint64_t)h * HD))[tid] = make_float4(o.x / den, o.y / den, o.z / den, o.w / den);
+  }
 }
 
 }  // namespace
@@ -383,9 +353,8 @@ hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
   const uint32_t G = a.n_heads / a.n_kv_heads;
 #define IFX_ATTN(HD_, G_)                                                                          \
   do {                                                                                             \
-    hipLaunchKernelGGL((k_attn_decode<HD_, G_, kFusedMerge>), grid, dim3(kThreads), 0, st, a);    \
-    if (!kFusedMerge)                                                                              \
-      hipLaunchKernelGGL((k_attn_merge<HD_, G_>), dim3(a.n_kv_heads), dim3(kThreads), 0, st, a);  \
+    hipLaunchKernelGGL((k_attn_decode<HD_, G_>), grid, dim3(kThreads), 0, st, a);                 \
+    hipLaunchKernelGGL((k_attn_merge<HD_, G_>), dim3(a.n_heads), dim3(kThreads), 0, st, a);       \
   } while (0)
   if (a.head_dim == 128 && G == 4) IFX_ATTN(128, 4);        // Llama-3 8B
   else if (a.head_dim == 128 && G == 8) IFX_ATTN(128, 8);   // Llama-3 70B

@@ -101,7 +101,6 @@ struct AttnArgs {
   const float* v_cache;
   float* out;            // [n_heads * head_dim]
   float* partial;        // [n_kv][max_chunks][attn_partial_floats(group, head_dim)]
-  uint32_t* counters;    // [n_kv], zero between launches
   const DevState* state;
   uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk;
 };
