@@ -177,17 +177,6 @@ __device__ __forceinline__ const uint8_t* unit_ptr(const GemvSeg& sg, uint32_t n
 // Prologue: x (optionally RMS-normalised) -> digit planes + group sums in LDS.
 // ---------------------------------------------------------------------------
 
-// rms_norm (src/ops.rs:162-167): scale = 1/sqrt(mean(x^2) + eps); x = (x*scale)*w.
-__device__ __forceinline__ float norm_scale(const MArgs& a, float ss, float* red, int lane, int wave) {
-  ss = wave_sum(ss);
-  if (lane == 0) red[wave] = ss;
-  __syncthreads();
-  float tot = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves; w++) tot += red[w];
-  return 1.0f / sqrtf(tot / (float)a.cols + a.eps);
-}
-
 // Chunk c = 8 consecutive elements (half of part c / 2); the 4 threads of a
 // 32-element group are consecutive lanes.  Every lane takes part in the
 // shuffles; only `ok` lanes write.
@@ -264,10 +253,13 @@ struct XStage {
     }
   }
 
-  // after load(a, 0, tid): norm scale, digit planes and group sums of all of x
-  __device__ __forceinline__ void finish(const MArgs& a, uint8_t* lds, float* red, int tid, int lane, int wave) {
+  // after load(a, 0, tid): digit planes and group sums of all of x (with the
+  // norm: of x * w), and the norm scale, returned (1 without the norm).
+  // rms_norm's scale (src/ops.rs:162-167) is one scalar per vector, so the
+  // kernel applies it to each row's dot product instead of to x: the
+  // quantization does not wait for the workgroup reduction of x . x.
+  __device__ __forceinline__ float finish(const MArgs& a, uint8_t* lds, float* red, int tid, int lane, int wave) {
     const uint32_t nch = a.cols / 8, step = kB * kThreads;
-    float scale = 1.f;
     if (NORM) {
       float ss = 0.f;
       if (nch <= step) {  // x is in registers
@@ -289,15 +281,21 @@ struct XStage {
           ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
         }
       }
-      scale = norm_scale(a, ss, red, lane, wave);
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
     }
-    quantize(a, 0, scale, lds, tid);
+    quantize(a, 0, 1.f, lds, tid);
     for (uint32_t base = step; base < nch; base += step) {
       load(a, base, tid);
-      quantize(a, base, scale, lds, tid);
+      quantize(a, base, 1.f, lds, tid);
     }
     if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
+    if (!NORM) return 1.f;
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) tot += red[w];
+    return 1.0f / sqrtf(tot / (float)a.cols + a.eps);
   }
 };
 
@@ -325,7 +323,7 @@ template <int T, int NT, int D, class Epi>
 __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s,
                                         KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t TG, uint32_t iters,
                                         uint32_t j, const uint8_t* lds, uint32_t a_base, uint32_t a_step,
-                                        float* part, int lane, int wave) {
+                                        float* part, float nscale, int lane, int wave) {
   const uint32_t S = a.split, NB = a.steps, nbr = a.nbr, nt = a.ntiles[s];
   const int g = lane >> 4;
   const float4* xsum = (const float4*)(lds + a.xs_off) + g;
@@ -389,11 +387,13 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
         for (int t = 0; t < NT; t++) {
           float v = 0.f;
           for (uint32_t q = 0; q < S; q++) v += pb[((wave + q) * NT + t) * 16 + (lane & 15)];
-          acc[t] = v;
+          acc[t] = v * nscale;
         }
         emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
       }
     } else if (live) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) acc[t] *= nscale;
       emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
     }
   }
@@ -419,7 +419,7 @@ __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D
 // memory queues (GPU-wide, not only per CU); one block each is enough to have
 // the first step's data arrive with x.
 template <bool NORM, int T, int NT, int D, class Epi>
-__device__ __forceinline__ void lead(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s0, uint32_t first,
+__device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s0, uint32_t first,
                                      uint32_t TG, uint32_t iters, uint32_t j, uint8_t* lds, float* red,
                                      uint32_t a_base, uint32_t a_step, float* part, int tid, int lane, int wave) {
   XStage<NORM> xs;
@@ -431,9 +431,10 @@ __device__ __forceinline__ void lead(const MArgs& a, const Epi& epi, typename Ep
   __builtin_amdgcn_sched_barrier(0);
   KBuf<T> buf[D][NT];
   prefetch<T, NT, D>(a, s0, buf, first, j, lane, 0, 1);
-  xs.finish(a, lds, red, tid, lane, wave);
+  const float nscale = xs.finish(a, lds, red, tid, lane, wave);
   prefetch<T, NT, D>(a, s0, buf, first, j, lane, 1, D);
-  run_seg<T, NT, D, Epi>(a, epi, ws, s0, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+  run_seg<T, NT, D, Epi>(a, epi, ws, s0, buf, first, TG, iters, j, lds, a_base, a_step, part, nscale, lane, wave);
+  return nscale;
 }
 
 // D > 4 (a deep ring for launches of at most one workgroup per CU) trades
@@ -466,25 +467,27 @@ __global__ void __launch_bounds__(kThreads, D > 4 ? 2 : kWavesPerSimd) k_gemv_mf
   };
   int s0 = 0;  // uniform over the workgroup
   while (s0 < a.nseg && block_iters(s0) == 0) s0++;
+  float nscale = 1.f;
   if (s0 < a.nseg) {
     const uint32_t first = (tg + TG - a.rot[s0]) % TG, iters = block_iters(s0);
     if (TA != TB && ((a.use_b >> s0) & 1u))
-      lead<NORM, TB, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
+      nscale = lead<NORM, TB, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
     else
-      lead<NORM, TA, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
+      nscale = lead<NORM, TA, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
   }
-  for (int s = s0 + 1; s < a.nseg; s++) {
+  // paired launches have one logical segment: no later segments to run
+  for (int s = s0 + 1; !Epi::kPaired && s < a.nseg; s++) {
     const uint32_t first = (tg + TG - a.rot[s]) % TG;
     const uint32_t iters = block_iters(s);
     if (iters == 0) continue;
     if (TA != TB && ((a.use_b >> s) & 1u)) {
       KBuf<TB> buf[D][NT];
       prefetch<TB, NT, D>(a, s, buf, first, j, lane);
-      run_seg<TB, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+      run_seg<TB, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, nscale, lane, wave);
     } else {
       KBuf<TA> buf[D][NT];
       prefetch<TA, NT, D>(a, s, buf, first, j, lane);
-      run_seg<TA, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, lane, wave);
+      run_seg<TA, NT, D, Epi>(a, epi, ws, s, buf, first, TG, iters, j, lds, a_base, a_step, part, nscale, lane, wave);
     }
   }
   epi.finish(ws, lane);
