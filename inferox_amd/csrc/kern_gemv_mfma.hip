@@ -85,9 +85,10 @@ __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// q . X from the three digit sums (exact int32 each; one f32 rounding per step)
+// q . X from the three digit sums: c0 + 256 c1 is exact in int32 (|c| < 2^17
+// per digit) and rounds once on conversion, as the fma it replaces did
 __device__ __forceinline__ float digits(v4i c) {
-  return fmaf(65536.f, (float)c[2], fmaf(256.f, (float)c[1], (float)c[0]));
+  return fmaf(65536.f, (float)c[2], (float)(c[0] + c[1] * 256));
 }
 
 // 16 Q4_K nibbles (8 bytes) -> 16 bytes in the A/B element order
@@ -105,8 +106,8 @@ __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> 
 
 // One (tile, block) unit of a segment in registers.  dot() returns this lane's
 // share of row (lane & 15)'s dot product over the block: sub-blocks g and
-// g + 4 (g = lane >> 4).  xa / xb: {scale, sum32, sum16 (part 0), sum16
-// (part 1)} of x over those sub-blocks.
+// g + 4 (g = lane >> 4).  xa / xb: {scale, sum32, -32 sum16 (part 0),
+// -32 sum16 (part 1)} of x over those sub-blocks.
 template <int T>
 struct KBuf;
 
@@ -161,10 +162,10 @@ struct KBuf<T_Q6K> {
     const v4i c1 = mfma(A[1], six(l0.z, l0.w, hq.y), z);
     const v4i c2 = mfma(A[2], six(l1.x, l1.y, hq.z), z);
     const v4i c3 = mfma(A[3], six(l1.z, l1.w, hq.w), z);
-    float v = (df * cvtb(sc, 0)) * fmaf(xa.x, digits(c0), -32.f * xa.z);
-    v = fmaf(df * cvtb(sc, 1), fmaf(xa.x, digits(c1), -32.f * xa.w), v);
-    v = fmaf(df * cvtb(sc, 2), fmaf(xb.x, digits(c2), -32.f * xb.z), v);
-    return fmaf(df * cvtb(sc, 3), fmaf(xb.x, digits(c3), -32.f * xb.w), v);
+    float v = (df * cvtb(sc, 0)) * fmaf(xa.x, digits(c0), xa.z);
+    v = fmaf(df * cvtb(sc, 1), fmaf(xa.x, digits(c1), xa.w), v);
+    v = fmaf(df * cvtb(sc, 2), fmaf(xb.x, digits(c2), xb.z), v);
+    return fmaf(df * cvtb(sc, 3), fmaf(xb.x, digits(c3), xb.w), v);
   }
 };
 
@@ -208,7 +209,7 @@ __device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool 
     *(uint2*)dst = make_uint2(p0[0], p0[1]);
     *(uint2*)(dst + 16) = make_uint2(p1[0], p1[1]);
     *(uint2*)(dst + 32) = make_uint2(p2[0], p2[1]);
-    if ((c & 3) == 0) xsum[c >> 2] = make_float4(xs, s16 + s16o, s16, s16o);
+    if ((c & 3) == 0) xsum[c >> 2] = make_float4(xs, s16 + s16o, -32.f * s16, -32.f * s16o);
   }
 }
 
@@ -437,10 +438,8 @@ __device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename E
   return nscale;
 }
 
-// D > 4 (a deep ring for launches of at most one workgroup per CU) trades
-// occupancy for registers: 2 waves per SIMD, up to 256 VGPRs.
 template <class Epi, int TA, int TB, int D, bool NORM>
-__global__ void __launch_bounds__(kThreads, D > 4 ? 2 : kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
+__global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
   constexpr int NT = Epi::kPaired ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float red[kWaves];
@@ -575,10 +574,10 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   a.split = split;
   const uint32_t nbm = (a.nbr + split - 1) / split;
   const uint32_t blocks = std::min<uint32_t>((total * split + kWaves - 1) / kWaves, per_cu * cu_count());
-  // ring depth: every block of an item in flight at once where registers allow
+  // ring depth (a deeper ring at lower occupancy measured slower)
   bool mixed = false;
   for (int s = 1; s < a.nseg; s++) mixed |= L.seg[s].type != L.seg[0].type;
-  const int D = (NT == 2 || mixed || nbm <= 2) ? 2 : (nbm > 4 && blocks <= (uint32_t)cu_count()) ? 8 : 4;
+  const int D = (NT == 2 || mixed || nbm <= 2) ? 2 : 4;
   a.steps = (nbm + D - 1) / D * D;
   const uint32_t TG = blocks * (kWaves / split);
   uint32_t acc = 0;
@@ -597,7 +596,6 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
   } else {
     if (D == 2) return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
-    if (D == 8) return go_types<Epi, 8>(a, ta, tb, epi, blocks, lds, st);
     return go_types<Epi, 4>(a, ta, tb, epi, blocks, lds, st);
   }
 }
