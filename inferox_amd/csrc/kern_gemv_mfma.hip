@@ -32,7 +32,7 @@
 //     sub-block), so the decode costs about one VALU instruction per weight
 //     per lane instead of four for the f32 dot.
 //
-// Work decomposition: persistent workgroups of 8 waves (2 per CU).  An item is
+// Work decomposition: persistent workgroups of 8 waves (1 or 2 per CU).  An item is
 // one 16-row tile (two for paired gate/up launches, sharing the A reads); its
 // blocks are split over `split` waves and reduced through LDS.  Each wave
 // keeps the loads of D blocks in flight in a ring: block i is computed, then
@@ -53,8 +53,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kBlocksPerCu = 2;
-constexpr int kWavesPerSimd = kBlocksPerCu * kWaves / 4;  // 4: at most 128 VGPRs
+// Up to two workgroups per CU (at most 128 VGPRs).  Launches use one per CU
+// except the mixed-type QKV launch: with 16 waves per CU the loads in flight
+// (~55 MB GPU-wide for the output matrix) exceed what HBM serves efficiently
+// (8 waves stream the 431 MB output matrix in 86 us instead of 95 us), while
+// the QKV launch, two short segments per wave, gains from the second one.
+constexpr int kMaxBlocksPerCu = 2;
+constexpr int kWavesPerSimd = kMaxBlocksPerCu * kWaves / 4;  // 4
 constexpr uint32_t kPartBytes = 48;   // 3 digit planes x 16 bytes per 16-element part
 constexpr uint32_t kBlockA = 16 * kPartBytes;  // A bytes of one 256-element block
 constexpr uint32_t kZeroBytes = 512;  // read by the lanes that feed zero A rows
@@ -111,6 +116,11 @@ __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> 
 template <int T>
 struct KBuf;
 
+// Weight loads (plain: nontemporal loads measured slower overall, faster only
+// on the 431 MB output matrix)
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *(const uint4*)p; }
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *(const uint32_t*)p; }
+
 // Q4_K (src/gguf/dequant.rs:133-161): scales/mins of sub-blocks s < 4 are the
 // low 6 bits of bytes s / s + 4; of s >= 4, the nibbles of byte s + 4 with the
 // top bits of bytes s - 4 / s (dequant.rs:141-149).
@@ -121,9 +131,9 @@ struct KBuf<T_Q4K> {
   // u: wave-uniform unit base; 32-bit unsigned lane offsets keep the
   // scalar-base addressing form (no 64-bit address per lane)
   __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
-    h = *(const uint4*)(u + 16u * (lane & 15u));
-    q0 = *(const uint4*)(u + (256u + 16u * lane));
-    q1 = *(const uint4*)(u + (1280u + 16u * lane));
+    h = ld16(u + 16u * (lane & 15u));
+    q0 = ld16(u + (256u + 16u * lane));
+    q1 = ld16(u + (1280u + 16u * lane));
   }
   __device__ __forceinline__ float dot(const v4i* A, float4 xa, float4 xb, int g) const {
     const v4i z = {0, 0, 0, 0};
@@ -149,15 +159,17 @@ struct KBuf<T_Q6K> {
   uint4 l0, l1, hq;
   uint32_t sc, d;
   __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
-    l0 = *(const uint4*)(u + 16u * lane);
-    l1 = *(const uint4*)(u + (1024u + 16u * lane));
-    hq = *(const uint4*)(u + (2048u + 16u * lane));
-    sc = *(const uint32_t*)(u + (3072u + 4u * lane));
-    d = *(const uint16_t*)(u + (3328u + 2u * (lane & 15u)));
+    l0 = ld16(u + 16u * lane);
+    l1 = ld16(u + (1024u + 16u * lane));
+    hq = ld16(u + (2048u + 16u * lane));
+    sc = ld4(u + (3072u + 4u * lane));
+    // the dword holding rows 2k, 2k+1's d: a 16-bit load would be
+    // zero-extended where the ring slot is carried, waiting for the slot
+    d = ld4(u + (3328u + 4u * ((lane & 15u) >> 1)));
   }
   __device__ __forceinline__ float dot(const v4i* A, float4 xa, float4 xb, int) const {
     const v4i z = {0, 0, 0, 0};
-    const float df = h2f(d);
+    const float df = h2f(d >> (16u * (__lane_id() & 1u)));
     const v4i c0 = mfma(A[0], six(l0.x, l0.y, hq.x), z);
     const v4i c1 = mfma(A[1], six(l0.z, l0.w, hq.y), z);
     const v4i c2 = mfma(A[2], six(l1.x, l1.y, hq.z), z);
@@ -411,6 +423,10 @@ __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D
     const uint32_t b = min(j + a.split * i, a.nbr - 1);
 #pragma unroll
     for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane);
+    // issue the slots in ring order: the loop's waits assume slot i is older
+    // than slot i + 1 on every path into it (reordered prefetches made each
+    // step wait for the whole ring)
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -567,7 +583,10 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   a.zero_off = a.xs_off + a.cols / 2;       // group sums: 16 bytes per 32 elements
   const size_t lds = a.zero_off + kZeroBytes;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  const uint32_t per_cu = (uint32_t)std::max<size_t>(1, std::min<size_t>(kBlocksPerCu, (160 * 1024) / lds));
+  bool mixed = false;
+  for (int s = 1; s < a.nseg; s++) mixed |= L.seg[s].type != L.seg[0].type;
+  const size_t want = mixed ? kMaxBlocksPerCu : 1;
+  const uint32_t per_cu = (uint32_t)std::max<size_t>(1, std::min<size_t>(want, (160 * 1024) / lds));
   const uint32_t resident = per_cu * cu_count() * kWaves;
   uint32_t split = 1;
   while (split < (uint32_t)kWaves && split < a.nbr && total * split < resident) split *= 2;
@@ -575,8 +594,6 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   const uint32_t nbm = (a.nbr + split - 1) / split;
   const uint32_t blocks = std::min<uint32_t>((total * split + kWaves - 1) / kWaves, per_cu * cu_count());
   // ring depth (a deeper ring at lower occupancy measured slower)
-  bool mixed = false;
-  for (int s = 1; s < a.nseg; s++) mixed |= L.seg[s].type != L.seg[0].type;
   const int D = (NT == 2 || mixed || nbm <= 2) ? 2 : 4;
   a.steps = (nbm + D - 1) / D * D;
   const uint32_t TG = blocks * (kWaves / split);
