@@ -110,6 +110,19 @@ int ifx_session_clear(ifx_session* s);                 /* KvCache::clear (cache.
 int ifx_session_len(const ifx_session* s, uint64_t* len);  /* KvCache::len (cache.rs:31-33) */
 int ifx_session_set_rope_mode(ifx_session* s, int mode);
 
+/* Prefill path of a session.  Model::prefill (src/model/forward.rs:496-538)
+ * runs chunks of at least min_rows ids (default 64; 0 = never) layer by layer
+ * as dequant-to-LDS GEMMs on the fp16 matrix cores and a batched causal
+ * attention, when the model is eligible (ifx_model_batched_prefill); shorter
+ * chunks replay the decode step per id.  Both give the reference's semantics
+ * (chunk-relative RoPE, chunk-only attention, logits of every row) within
+ * f32-level rounding. */
+int ifx_session_set_prefill_batch(ifx_session* s, uint64_t min_rows);
+/* *eligible = 1 if every layer matrix and the output matrix have a type the
+ * prefill GEMM reads (Q4_K, Q6_K, Q8_0, Q4_0) with elements inside the fp16
+ * range, and the head dim is one the prefill attention is built for. */
+int ifx_model_batched_prefill(const ifx_model* m, int* eligible);
+
 /* Model::decode_step (src/model/forward.rs:543-586).  logits_out: host buffer of
  * vocab_size floats, or NULL to leave the logits on the device. */
 int ifx_decode_step(ifx_session* s, uint32_t token, float* logits_out);

@@ -42,6 +42,8 @@ SIGNATURES = {
     "ifx_session_clear": (i32, [vp]),
     "ifx_session_len": (i32, [vp, P(u64)]),
     "ifx_session_set_rope_mode": (i32, [vp, i32]),
+    "ifx_session_set_prefill_batch": (i32, [vp, u64]),
+    "ifx_model_batched_prefill": (i32, [vp, P(i32)]),
     "ifx_decode_step": (i32, [vp, u32, vp]),
     "ifx_prefill": (i32, [vp, vp, u64, vp]),
     "ifx_forward": (i32, [vp, vp, u64, vp]),

@@ -120,7 +120,16 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
     }
     e = hipMemcpy(t->L.body, stage.data(), body, hipMemcpyHostToDevice);
     if (e == hipSuccess && scal) e = hipMemcpy(t->L.scal, stage.data() + body, scal, hipMemcpyHostToDevice);
+    std::mutex mu;
+    float bound = 0.f;
+    parallel_ranges(t->L.n_blocks, 65536, [&](uint64_t b0, uint64_t b1) {
+      const float v = block_abs_bound(type, src, b0, b1);
+      std::lock_guard<std::mutex> g(mu);
+      bound = (v > bound || v != v) ? v : bound;
+    });
+    t->L.abs_bound = bound;
   }
+  if (type == T_F32 || type == T_F16) t->L.abs_bound = INFINITY;
   if (e != hipSuccess) {
     (void)hipFree(t->alloc);
     delete t;
@@ -266,6 +275,23 @@ int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream) {
 int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream) {
   IFX_TRY(device_init());
   if (!w || (m && (!a || !c))) return set_error(IFX_E_INVALID_ARG, "null argument");
+  // two rows or more: the prefill GEMM (fp16 matrix cores, hi/lo operand pairs)
+  // for the types and magnitudes it takes; the GEMV row by row otherwise
+  if (m >= 2 && m <= 0xffffffffull && gemm_type(w->L.type) && w->L.abs_bound <= 32768.f && w->L.cols % 32 == 0) {
+    hipStream_t st = stream_of(stream);
+    uint32_t* rmax = nullptr;
+    IFX_HIP(hipMallocAsync((void**)&rmax, m * 4, st));
+    hipError_t e = launch_rowmax(a, (uint32_t)m, (uint32_t)w->L.cols, (uint32_t)w->L.cols, rmax, st);
+    if (e == hipSuccess) {
+      const GemmIn in{a, rmax, (uint32_t)m, (uint32_t)w->L.cols};
+      const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols};
+      e = gemm_store(in, gw, c, (uint32_t)w->L.rows, st);
+    }
+    const hipError_t ef = hipFreeAsync(rmax, st);
+    IFX_HIP(e);
+    IFX_HIP(ef);
+    return IFX_OK;
+  }
   for (uint64_t i = 0; i < m; i++) {
     GemvLaunch L;
     L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows};

@@ -45,6 +45,7 @@ struct ifx_model {
   std::vector<void*> norm_allocs;
   uint64_t dev_bytes = 0, gguf_bytes = 0;
   bool dims_ok = false;
+  bool gemm_ok = false;  // every layer matrix and the output fit the batched prefill GEMM
 };
 
 struct ifx_session {
@@ -64,6 +65,16 @@ struct ifx_session {
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
   std::vector<void*> allocs;
+  // batched prefill: chunks of at least batch_min rows (0: never) run layer by
+  // layer through the GEMMs; the workspace grows to the largest chunk seen
+  uint64_t batch_min = 64;
+  struct {
+    uint64_t cap = 0, logit_rows = 0;
+    void* alloc = nullptr;
+    void* logits = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *a = nullptr, *mid = nullptr;
+    uint32_t* rmax = nullptr;
+  } ws;
 };
 
 namespace {
@@ -145,6 +156,26 @@ int check_dims(const ifx_model* m) {
 GemvSeg seg_of(const ifx_tensor* t) {
   return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows};
 }
+
+// The batched prefill GEMM takes the quantized types whose elements stay in
+// the fp16 range (their hi/lo split, kern_gemm.hip), 32-column blocks, and a
+// head dim the prefill attention kernel is built for.
+constexpr float kGemmAbsMax = 32768.f;
+bool gemm_tensor_ok(const ifx_tensor* t) {
+  return t && gemm_type(t->L.type) && t->L.abs_bound <= kGemmAbsMax && t->L.cols % 32 == 0;
+}
+bool gemm_eligible(const ifx_model* m) {
+  const ifx_config& c = m->cfg;
+  if (!attn_prefill_head_dim((uint32_t)c.head_dim) || c.hidden_size != c.n_heads * c.head_dim ||
+      c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.rope_dim > c.head_dim || c.rope_dim % 2)
+    return false;
+  if (!gemm_tensor_ok(m->output)) return false;
+  for (const LayerDev& L : m->layers)
+    for (const ifx_tensor* t : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+      if (!gemm_tensor_ok(t)) return false;
+  return true;
+}
+GemmW gw(const ifx_tensor* t) { return GemmW{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.cols}; }
 
 // Kernel classes of one step (ifx_session_profile): 0 embed, 1 qkv + rope +
 // kv-append, 2 attention (partials + merge), 3 attn_output + residual,
@@ -292,6 +323,106 @@ int state_op(ifx_session* s, uint32_t kind, uint32_t value, uint32_t len) {
   return IFX_OK;
 }
 
+// Prefill workspace for chunks of up to n rows (grows, never shrinks).
+int ensure_ws(ifx_session* s, uint64_t n) {
+  if (n <= s->ws.cap) return IFX_OK;
+  const ifx_config& c = s->m->cfg;
+  const uint64_t D = c.hidden_size, F = c.intermediate_size;
+  auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
+  const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), br = al(n * 4);
+  if (s->ws.alloc) {
+    IFX_HIP(hipStreamSynchronize(s->stream));
+    IFX_HIP(hipFree(s->ws.alloc));
+    s->ws.alloc = nullptr;
+    s->ws.cap = 0;
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, 4 * bx + bm + br) != hipSuccess)
+    return set_error(IFX_E_OOM, "prefill workspace of %llu rows", (unsigned long long)n);
+  uint8_t* b = (uint8_t*)p;
+  s->ws.x = (float*)b;
+  s->ws.q = (float*)(b + bx);
+  s->ws.att = (float*)(b + 2 * bx);
+  s->ws.a = (float*)(b + 3 * bx);
+  s->ws.mid = (float*)(b + 4 * bx);
+  s->ws.rmax = (uint32_t*)(b + 4 * bx + bm);
+  s->ws.alloc = p;
+  s->ws.cap = n;
+  return IFX_OK;
+}
+
+// Model::prefill (src/model/forward.rs:496-538) as whole-chunk GEMMs, layer by
+// layer (Layer::prefill, src/model/forward.rs:215-337): the n ids at
+// s->feed_ids (device) write K/V rows start .. start + n - 1; query t attends
+// to rows start .. start + t (causal) or to all n rows (Layer::forward's
+// non-causal attention, src/model/forward.rs:62-207).  RoPE positions are
+// chunk-relative (0 .. n - 1) or, in ABSOLUTE mode, start + t.  The last row
+// then takes the decode head (final RMSNorm, logits, argmax) and the state
+// records its greedy pick as a step does; logits_out (host, n x vocab) gets
+// every row's logits when non-null.
+int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, float* logits_out) {
+  ifx_model* m = s->m;
+  const ifx_config& c = m->cfg;
+  IFX_TRY(ensure_ws(s, n));
+  hipStream_t st = s->stream;
+  const uint32_t N = (uint32_t)n, D = (uint32_t)c.hidden_size, F = (uint32_t)c.intermediate_size;
+  const uint32_t hd = (uint32_t)c.head_dim, rd = (uint32_t)c.rope_dim;
+  const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim), row0 = (uint32_t)start;
+  const uint32_t pos0 = s->rope_mode == IFX_ROPE_ABSOLUTE ? row0 : 0u;
+  auto& w = s->ws;
+  IFX_HIP(launch_embed_rows(devw(m->embd), s->feed_ids, n, w.x, st));
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    const LayerDev& L = m->layers[l];
+    float* kc = s->kc + l * s->max_seq * kvd;
+    float* vc = s->vc + l * s->max_seq * kvd;
+    IFX_HIP(launch_rmsnorm_rows_to(w.x, L.attn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
+    const GemmIn in{w.a, w.rmax, N, D};
+    IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, 0, pos0, hd, rd, s->rope_cs, st));
+    IFX_HIP(gemm_rope(in, gw(L.k), kc, kvd, row0, pos0, hd, rd, s->rope_cs, st));
+    IFX_HIP(gemm_rows(in, gw(L.v), vc, kvd, row0, st));
+    const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd, causal};
+    IFX_HIP(launch_attn_prefill(aa, st));
+    IFX_HIP(launch_rowmax(w.att, N, D, D, w.rmax, st));
+    IFX_HIP(gemm_residual(GemmIn{w.att, w.rmax, N, D}, gw(L.o), w.x, D, st));
+    IFX_HIP(launch_rmsnorm_rows_to(w.x, L.ffn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
+    IFX_HIP(gemm_swiglu(GemmIn{w.a, w.rmax, N, D}, gw(L.gate), gw(L.up), w.mid, F, st));
+    IFX_HIP(launch_rowmax(w.mid, N, F, F, w.rmax, st));
+    IFX_HIP(gemm_residual(GemmIn{w.mid, w.rmax, N, F}, gw(L.down), w.x, D, st));
+  }
+  // the last row's greedy pick, recorded as a step records it (k_finalize)
+  IFX_TRY(state_op(s, STATE_BATCH, 0, N));
+  GemvLaunch gh;
+  gh.seg[0] = seg_of(m->output);
+  gh.nseg = 1;
+  gh.cols = D;
+  gh.x = w.x + (n - 1) * D;
+  gh.norm_w = m->out_norm;
+  gh.eps = c.norm_eps;
+  IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
+  IFX_HIP(launch_finalize(s->state, st));
+  if (logits_out) {
+    const uint64_t V = c.vocab_size, rows = std::min<uint64_t>(n, 512);
+    if (w.logit_rows < rows) {
+      if (w.logits) {
+        IFX_HIP(hipStreamSynchronize(st));
+        IFX_HIP(hipFree(w.logits));
+        w.logits = nullptr;
+        w.logit_rows = 0;
+      }
+      if (hipMalloc(&w.logits, rows * V * 4) != hipSuccess)
+        return set_error(IFX_E_OOM, "prefill logits buffer of %llu rows", (unsigned long long)rows);
+      w.logit_rows = rows;
+    }
+    for (uint64_t r0 = 0; r0 < n; r0 += rows) {
+      const uint32_t nr = (uint32_t)std::min<uint64_t>(rows, n - r0);
+      IFX_HIP(launch_rmsnorm_rows_to(w.x + r0 * D, m->out_norm, nr, D, c.norm_eps, w.a, w.rmax, st));
+      IFX_HIP(gemm_store(GemmIn{w.a, w.rmax, nr, D}, gw(m->output), (float*)w.logits, (uint32_t)V, st));
+      IFX_HIP(hipMemcpyAsync(logits_out + r0 * V, w.logits, (size_t)nr * V * 4, hipMemcpyDeviceToHost, st));
+    }
+  }
+  return IFX_OK;
+}
+
 int check_vocab(const ifx_model* m) {
   const ifx_config& c = m->cfg;
   if (m->embd->L.rows < c.vocab_size || m->output->L.rows != c.vocab_size)
@@ -300,9 +431,12 @@ int check_vocab(const ifx_model* m) {
   return IFX_OK;
 }
 
+
 void session_free(ifx_session* s) {
   if (!s) return;
   if (s->stream) (void)hipStreamSynchronize(s->stream);
+  if (s->ws.alloc) (void)hipFree(s->ws.alloc);
+  if (s->ws.logits) (void)hipFree(s->ws.logits);
   if (s->exec) (void)hipGraphExecDestroy(s->exec);
   if (s->ev0) (void)hipEventDestroy(s->ev0);
   if (s->ev1) (void)hipEventDestroy(s->ev1);
@@ -409,6 +543,7 @@ int ifx_model_open(const char* path, ifx_model** out) {
                      (unsigned long long)l);
   }
   if (rc != IFX_OK) { model_free(m); return rc; }
+  m->gemm_ok = gemm_eligible(m);
   *out = m;
   return IFX_OK;
 }
@@ -507,6 +642,18 @@ int ifx_session_len(const ifx_session* s, uint64_t* len) {
   return IFX_OK;
 }
 
+int ifx_session_set_prefill_batch(ifx_session* s, uint64_t min_rows) {
+  if (!s) return set_error(IFX_E_INVALID_ARG, "null session");
+  s->batch_min = min_rows;
+  return IFX_OK;
+}
+
+int ifx_model_batched_prefill(const ifx_model* m, int* eligible) {
+  if (!m || !eligible) return set_error(IFX_E_INVALID_ARG, "null argument");
+  *eligible = m->gemm_ok ? 1 : 0;
+  return IFX_OK;
+}
+
 int ifx_session_set_rope_mode(ifx_session* s, int mode) {
   if (!s || (mode != IFX_ROPE_REFERENCE && mode != IFX_ROPE_ABSOLUTE))
     return set_error(IFX_E_INVALID_ARG, "bad rope mode");
@@ -543,6 +690,16 @@ int ifx_prefill(ifx_session* s, const uint32_t* ids, uint64_t n, float* logits_o
   IFX_TRY(check_vocab(m));
   if (s->len + n > s->max_seq) return set_error(IFX_E_KV_FULL, "prefill of %llu rows overflows the KV cache", (unsigned long long)n);
   IFX_HIP(hipMemcpyAsync(s->feed_ids, ids, n * 4, hipMemcpyHostToDevice, s->stream));
+  if (s->batch_min && n >= s->batch_min && m->gemm_ok) {
+    IFX_HIP(hipEventRecord(s->ev0, s->stream));
+    IFX_TRY(batched_prefill(s, n, s->len, true, logits_out));
+    IFX_HIP(hipEventRecord(s->ev1, s->stream));
+    IFX_HIP(hipStreamSynchronize(s->stream));
+    (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
+    s->len += n;
+    s->steps += n;
+    return IFX_OK;
+  }
   IFX_TRY(state_op(s, STATE_PREFILL, 0, (uint32_t)n));
   IFX_HIP(hipEventRecord(s->ev0, s->stream));
   const size_t V = m->cfg.vocab_size;
@@ -726,6 +883,15 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
   IFX_TRY(check_vocab(m));
   ifx_session* s = nullptr;
   IFX_TRY(ifx_session_create(m, n, &s));
+  if (m->gemm_ok && n >= s->batch_min) {
+    int rc = IFX_OK;
+    if (hipMemcpyAsync(s->feed_ids, ids, n * 4, hipMemcpyHostToDevice, s->stream) != hipSuccess)
+      rc = set_error(IFX_E_HIP, "forward: id upload failed");
+    if (rc == IFX_OK) rc = batched_prefill(s, n, 0, false, logits_out);
+    if (rc == IFX_OK && hipStreamSynchronize(s->stream) != hipSuccess) rc = set_error(IFX_E_HIP, "forward: sync failed");
+    session_free(s);
+    return rc;
+  }
   const ifx_config& c = m->cfg;
   const uint64_t D = c.hidden_size, F = c.intermediate_size, kvd = c.n_kv_heads * c.head_dim;
   const size_t V = c.vocab_size;

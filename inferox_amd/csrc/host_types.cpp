@@ -2,6 +2,7 @@
 // GGUF blocks into the device layout described in ifx_common.h.
 #include <stdarg.h>
 #include <stdio.h>
+#include <math.h>
 #include <string.h>
 
 #include "ifx_common.h"
@@ -164,6 +165,33 @@ void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t col
       }
       pack_unit(type, blk, body + (t * nbr + b) * unit);
     }
+}
+
+static float host_f16(const uint8_t* p) {
+  const uint32_t h = (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+  const uint32_t e = (h >> 10) & 31u, f = h & 1023u;
+  float v;
+  if (e == 31) v = f ? NAN : INFINITY;
+  else if (e == 0) v = ldexpf((float)f, -24);
+  else v = ldexpf((float)(f | 1024u), (int)e - 25);
+  return (h & 0x8000u) ? -v : v;
+}
+
+float block_abs_bound(uint32_t type, const uint8_t* src, uint64_t b0, uint64_t b1) {
+  float m = 0.f;
+  for (uint64_t b = b0; b < b1; b++) {
+    float v;
+    switch (type) {
+      case T_Q4K: v = fabsf(host_f16(src + 144 * b)) * 945.f + fabsf(host_f16(src + 144 * b + 2)) * 63.f; break;
+      case T_Q6K: v = fabsf(host_f16(src + 210 * b)) * 8160.f; break;
+      case T_Q8_0: v = fabsf(host_f16(src + 34 * b)) * 128.f; break;
+      case T_Q4_0: v = fabsf(host_f16(src + 18 * b)) * 8.f; break;
+      default: return INFINITY;
+    }
+    if (!(v <= 3.0e38f)) return INFINITY;
+    m = v > m ? v : m;
+  }
+  return m;
 }
 
 }  // namespace ifx

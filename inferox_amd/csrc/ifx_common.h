@@ -81,6 +81,7 @@ struct DevLayout {
   uint8_t* scal = nullptr;    // device: scale array (Q4_0/Q8_0/Q6_K/Q8_K), else null
   uint64_t body_bytes = 0, scal_bytes = 0;
   uint64_t gguf_bytes = 0;    // stored GGUF bytes of the same matrix
+  float abs_bound = 0.f;      // bound on |element| from the block scales (inf: unbounded or non-finite)
 };
 
 // Host-side repack of one matrix from GGUF block bytes into the device layout
@@ -92,6 +93,10 @@ void repack_to_device_layout(uint32_t type, const uint8_t* src, uint64_t n_block
 // matrix's body; src is the whole matrix's GGUF bytes).
 void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t cols, uint64_t t0, uint64_t t1,
                   uint8_t* body);
+// Bound on |element| over GGUF blocks [b0, b1) of a quantized type, from the
+// block scales alone (Q4_K: |d| 63 15 + |dmin| 63; Q6_K: |d| 255 32; Q8_0:
+// |d| 128; Q4_0: |d| 8); +inf for F32/F16/Q8_K or a non-finite scale.
+float block_abs_bound(uint32_t type, const uint8_t* src, uint64_t b0, uint64_t b1);
 
 }  // namespace ifx
 

@@ -205,6 +205,16 @@ __global__ void k_state(DevState* s, StateOp op) {
       s->attn_end = 0;
       s->rope_pos = s->rope_mode == IFX_ROPE_ABSOLUTE ? s->len : 0u;
       break;
+    case STATE_BATCH:  // a batched prefill of op.len rows wrote its K/V rows: the next
+                       // finalize records the last row's greedy pick as a step would
+      s->len += op.len - 1u;
+      s->step += op.len - 1u;
+      s->prefill = 0;
+      s->attn_lo = 0;
+      s->attn_end = 0;
+      s->argmax_key = 0ull;
+      s->status = IFX_OK;
+      break;
     case STATE_TOKEN_AT:  // non-causal forward: token op.value of a chunk of op.len rows
       s->len = op.value;
       s->prefill = 0;

@@ -73,6 +73,55 @@ hipError_t gemv_swiglu(const GemvLaunch& L, float* mid, hipStream_t st);
 hipError_t gemv_logits(const GemvLaunch& L, float* logits, DevState* state, hipStream_t st);
 int gemv_supported(uint32_t type);
 
+// ---- batched prefill GEMM (kern_gemm.hip) ----
+// A weight matrix as the GEMM reads it (the device layout of ifx_common.h).
+struct GemmW {
+  const uint8_t* body;
+  const uint8_t* scal;
+  uint32_t type;
+  uint32_t rows;
+  uint64_t cols;
+};
+// The f32 activation operand: m rows of stride lda, and per row the float bits
+// of its largest magnitude (the GEMM scales each row into the fp16 range).
+struct GemmIn {
+  const float* a;
+  const uint32_t* rowmax;
+  uint32_t m, lda;
+};
+bool gemm_type(uint32_t type);
+// y[t * ldy + n] = (A W^T)[t][n]
+hipError_t gemm_store(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, hipStream_t st);
+// x[t * ldx + n] += (A W^T)[t][n]
+hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ldx, hipStream_t st);
+// RoPE at position pos0 + t, rows written to y + (row0 + t) * ldy
+hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, uint32_t pos0,
+                     uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st);
+// rows written to y + (row0 + t) * ldy (the V cache append)
+hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, hipStream_t st);
+// mid[t * ld + n] = swiglu(gate row n . A[t], up row n . A[t])
+hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,
+                       hipStream_t st);
+hipError_t launch_rowmax(const float* x, uint32_t rows, uint32_t ld, uint32_t cols, uint32_t* out, hipStream_t st);
+// y = rms_norm(x) row by row (src/ops.rs:155-180), rowmax[t] = bits of max |y[t][:]|
+hipError_t launch_rmsnorm_rows_to(const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* y,
+                                  uint32_t* rowmax, hipStream_t st);
+
+// ---- batched prefill attention (kern_attn_prefill.hip) ----
+// Attention of n query rows over the chunk's keys (src/model/forward.rs:
+// 215-337): query t (q row t) attends to cache rows row0 .. row0 + t
+// (causal) or row0 .. row0 + n - 1; out[t] f32, the row's max |out| in rowmax.
+struct AttnPrefillArgs {
+  const float* q;        // [n][n_heads * head_dim]
+  const float* k_cache;  // layer base [max_seq][kv_dim]
+  const float* v_cache;
+  float* out;            // [n][n_heads * head_dim]
+  uint32_t n, row0, n_heads, n_kv_heads, head_dim;
+  bool causal;
+};
+bool attn_prefill_head_dim(uint32_t head_dim);
+hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t st);
+
 // ---- small ops (kern_ops.hip) ----
 hipError_t launch_matmul_t_f32(const float* a, const float* b, float* c, uint64_t m, uint64_t n,
                                uint64_t k, hipStream_t st);
@@ -85,7 +134,7 @@ hipError_t launch_rope(float* x, uint64_t seq, uint64_t heads, uint64_t hd, uint
                        float base, uint64_t pos0, hipStream_t st);
 hipError_t launch_argmax(const float* x, uint64_t n, uint32_t* out, int* status, hipStream_t st);
 hipError_t launch_finalize(DevState* state, hipStream_t st);
-enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT };
+enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT, STATE_BATCH };
 struct StateOp {
   uint32_t kind;
   uint32_t value;

@@ -73,6 +73,11 @@ class GpuModel:
             _native.lib().ifx_model_close(self.h)
             self.h = None
 
+    def batched_prefill(self) -> bool:
+        e = C.c_int()
+        check(_native.lib().ifx_model_batched_prefill(self.h, C.byref(e)), "batched_prefill")
+        return bool(e.value)
+
     def session(self, max_seq: int) -> "GpuSession":
         return GpuSession(self, max_seq)
 
@@ -111,6 +116,9 @@ class GpuSession:
 
     def set_rope_mode(self, mode: int):
         check(_native.lib().ifx_session_set_rope_mode(self.h, mode), "rope_mode")
+
+    def set_prefill_batch(self, min_rows: int):
+        check(_native.lib().ifx_session_set_prefill_batch(self.h, min_rows), "prefill_batch")
 
     def decode_step(self, token: int, want_logits=True):
         out = np.zeros(self.model.vocab, np.float32) if want_logits else None
