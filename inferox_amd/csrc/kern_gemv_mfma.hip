@@ -431,10 +431,9 @@ __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D
 }
 
 // Segment s0 (the workgroup's first segment with work): x loads, the loads of
-// the wave's first block, staging, the loads of its next D - 1 blocks, then
-// the segment.  Weight loads issued before staging delay x behind them in the
-// memory queues (GPU-wide, not only per CU); one block each is enough to have
-// the first step's data arrive with x.
+// the wave's first D blocks (issued after x, so x is not queued behind them),
+// staging, then the segment.  With the whole ring in flight during staging the
+// 9.4 MB attn_output launch takes 5.4 us instead of 5.8 us.
 template <bool NORM, int T, int NT, int D, class Epi>
 __device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s0, uint32_t first,
                                      uint32_t TG, uint32_t iters, uint32_t j, uint8_t* lds, float* red,
@@ -447,9 +446,8 @@ __device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename E
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   KBuf<T> buf[D][NT];
-  prefetch<T, NT, D>(a, s0, buf, first, j, lane, 0, 1);
+  prefetch<T, NT, D>(a, s0, buf, first, j, lane, 0, D);
   const float nscale = xs.finish(a, lds, red, tid, lane, wave);
-  prefetch<T, NT, D>(a, s0, buf, first, j, lane, 1, D);
   run_seg<T, NT, D, Epi>(a, epi, ws, s0, buf, first, TG, iters, j, lds, a_base, a_step, part, nscale, lane, wave);
   return nscale;
 }
