@@ -280,16 +280,21 @@ int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, voi
   if (m >= 2 && m <= 0xffffffffull && gemm_type(w->L.type) && w->L.abs_bound <= 32768.f && w->L.cols % 32 == 0) {
     hipStream_t st = stream_of(stream);
     uint32_t* rmax = nullptr;
+    float* part = nullptr;
+    const uint64_t part_bytes = 64ull << 20;  // split-K partial tiles of short inputs
     IFX_HIP(hipMallocAsync((void**)&rmax, m * 4, st));
-    hipError_t e = launch_rowmax(a, (uint32_t)m, (uint32_t)w->L.cols, (uint32_t)w->L.cols, rmax, st);
+    hipError_t e = hipMallocAsync((void**)&part, part_bytes, st);
+    if (e == hipSuccess) e = launch_rowmax(a, (uint32_t)m, (uint32_t)w->L.cols, (uint32_t)w->L.cols, rmax, st);
     if (e == hipSuccess) {
-      const GemmIn in{a, rmax, (uint32_t)m, (uint32_t)w->L.cols};
+      const GemmIn in{a, rmax, (uint32_t)m, (uint32_t)w->L.cols, part, part_bytes};
       const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols};
       e = gemm_store(in, gw, c, (uint32_t)w->L.rows, st);
     }
     const hipError_t ef = hipFreeAsync(rmax, st);
+    const hipError_t ep = part ? hipFreeAsync(part, st) : hipSuccess;
     IFX_HIP(e);
     IFX_HIP(ef);
+    IFX_HIP(ep);
     return IFX_OK;
   }
   for (uint64_t i = 0; i < m; i++) {

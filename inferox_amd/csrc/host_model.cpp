@@ -73,6 +73,7 @@ struct ifx_session {
     void* alloc = nullptr;
     void* logits = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *a = nullptr, *mid = nullptr;
+    float* part = nullptr;  // split-K partial tiles of the GEMMs
     uint32_t* rmax = nullptr;
   } ws;
 };
@@ -323,13 +324,15 @@ int state_op(ifx_session* s, uint32_t kind, uint32_t value, uint32_t len) {
   return IFX_OK;
 }
 
-// Prefill workspace for chunks of up to n rows (grows, never shrinks).
+// Prefill workspace for chunks of up to n rows (grows, never shrinks), plus a
+// fixed buffer for the split-K partial tiles of short chunks.
+constexpr uint64_t kSplitPartBytes = 64ull << 20;
 int ensure_ws(ifx_session* s, uint64_t n) {
   if (n <= s->ws.cap) return IFX_OK;
   const ifx_config& c = s->m->cfg;
   const uint64_t D = c.hidden_size, F = c.intermediate_size;
   auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
-  const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), br = al(n * 4);
+  const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), br = al(n * 4), bp = kSplitPartBytes;
   if (s->ws.alloc) {
     IFX_HIP(hipStreamSynchronize(s->stream));
     IFX_HIP(hipFree(s->ws.alloc));
@@ -337,7 +340,7 @@ int ensure_ws(ifx_session* s, uint64_t n) {
     s->ws.cap = 0;
   }
   void* p = nullptr;
-  if (hipMalloc(&p, 4 * bx + bm + br) != hipSuccess)
+  if (hipMalloc(&p, 4 * bx + bm + br + bp) != hipSuccess)
     return set_error(IFX_E_OOM, "prefill workspace of %llu rows", (unsigned long long)n);
   uint8_t* b = (uint8_t*)p;
   s->ws.x = (float*)b;
@@ -346,6 +349,7 @@ int ensure_ws(ifx_session* s, uint64_t n) {
   s->ws.a = (float*)(b + 3 * bx);
   s->ws.mid = (float*)(b + 4 * bx);
   s->ws.rmax = (uint32_t*)(b + 4 * bx + bm);
+  s->ws.part = (float*)(b + 4 * bx + bm + br);
   s->ws.alloc = p;
   s->ws.cap = n;
   return IFX_OK;
@@ -376,18 +380,18 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     float* kc = s->kc + l * s->max_seq * kvd;
     float* vc = s->vc + l * s->max_seq * kvd;
     IFX_HIP(launch_rmsnorm_rows_to(w.x, L.attn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
-    const GemmIn in{w.a, w.rmax, N, D};
+    const GemmIn in{w.a, w.rmax, N, D, w.part, kSplitPartBytes};
     IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, 0, pos0, hd, rd, s->rope_cs, st));
     IFX_HIP(gemm_rope(in, gw(L.k), kc, kvd, row0, pos0, hd, rd, s->rope_cs, st));
     IFX_HIP(gemm_rows(in, gw(L.v), vc, kvd, row0, st));
     const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd, causal};
     IFX_HIP(launch_attn_prefill(aa, st));
     IFX_HIP(launch_rowmax(w.att, N, D, D, w.rmax, st));
-    IFX_HIP(gemm_residual(GemmIn{w.att, w.rmax, N, D}, gw(L.o), w.x, D, st));
+    IFX_HIP(gemm_residual(GemmIn{w.att, w.rmax, N, D, w.part, kSplitPartBytes}, gw(L.o), w.x, D, st));
     IFX_HIP(launch_rmsnorm_rows_to(w.x, L.ffn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
-    IFX_HIP(gemm_swiglu(GemmIn{w.a, w.rmax, N, D}, gw(L.gate), gw(L.up), w.mid, F, st));
+    IFX_HIP(gemm_swiglu(GemmIn{w.a, w.rmax, N, D, w.part, kSplitPartBytes}, gw(L.gate), gw(L.up), w.mid, F, st));
     IFX_HIP(launch_rowmax(w.mid, N, F, F, w.rmax, st));
-    IFX_HIP(gemm_residual(GemmIn{w.mid, w.rmax, N, F}, gw(L.down), w.x, D, st));
+    IFX_HIP(gemm_residual(GemmIn{w.mid, w.rmax, N, F, w.part, kSplitPartBytes}, gw(L.down), w.x, D, st));
   }
   // the last row's greedy pick, recorded as a step records it (k_finalize)
   IFX_TRY(state_op(s, STATE_BATCH, 0, N));
@@ -416,7 +420,8 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     for (uint64_t r0 = 0; r0 < n; r0 += rows) {
       const uint32_t nr = (uint32_t)std::min<uint64_t>(rows, n - r0);
       IFX_HIP(launch_rmsnorm_rows_to(w.x + r0 * D, m->out_norm, nr, D, c.norm_eps, w.a, w.rmax, st));
-      IFX_HIP(gemm_store(GemmIn{w.a, w.rmax, nr, D}, gw(m->output), (float*)w.logits, (uint32_t)V, st));
+      IFX_HIP(gemm_store(GemmIn{w.a, w.rmax, nr, D, w.part, kSplitPartBytes}, gw(m->output), (float*)w.logits,
+                         (uint32_t)V, st));
       IFX_HIP(hipMemcpyAsync(logits_out + r0 * V, w.logits, (size_t)nr * V * 4, hipMemcpyDeviceToHost, st));
     }
   }

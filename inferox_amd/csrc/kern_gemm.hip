@@ -30,6 +30,8 @@
 // v_mfma_f32_16x16x32_f16: lane i + 16g holds A[i][8g..8g+7] and
 // B[8g..8g+7][i]; C[4g + r][i] arrives in lane i + 16g, register r.
 // Compiled with -ffp-contract=off: the dequant keeps the reference's roundings.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace ifx {
@@ -50,6 +52,9 @@ struct GemmArgs {
   uint32_t m, lda, k;     // k = cols of the weight matrix, a multiple of 32
   GemmW w0, w1;           // w1: the second matrix of a paired launch (gate/up)
   uint32_t n;             // output columns: rows of w0 (paired: of each)
+  uint32_t ksplit;        // K ranges over grid.z; > 1: partial tiles to `part`
+  uint32_t kps;           // 32-wide K steps per range
+  float* part;            // [ksplit][m][ncols], ncols = n (paired: 2n, up after gate)
 };
 
 // ---------------------------------------------------------------------------
@@ -319,13 +324,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
   for (int j = 0; j < 4; j++)
     wcol[j] = kPaired ? (j < 2 ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
 
-  const uint32_t nk = a.k / kBK;
-  load_step(0);
-  for (uint32_t ks = 0; ks < nk; ks++) {
+  // this workgroup's K steps [ks0, ks1)
+  const uint32_t ks0 = blockIdx.z * a.kps, ks1 = min(a.k / kBK, ks0 + a.kps);
+  load_step(ks0 * kBK);
+  for (uint32_t ks = ks0; ks < ks1; ks++) {
     const int buf = ks & 1;
     stage(buf);
     __syncthreads();
-    if (ks + 1 < nk) load_step((ks + 1) * kBK);
+    if (ks + 1 < ks1) load_step((ks + 1) * kBK);
     h8 bh[4], bl[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -350,6 +356,23 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
       const int tl = wm * 64 + 16 * i + 4 * fg + r;
       const uint32_t t = m0 + (uint32_t)tl;
       const float inv = ldexpf(1.0f, rexp[tl] - 14);
+      if (a.ksplit > 1) {  // partial tile of this K range; the reduce applies the epilogue
+        const uint32_t ncols = kPaired ? 2 * a.n : a.n;
+        float* pr = a.part + ((uint64_t)blockIdx.z * a.m + t) * ncols;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          uint32_t n, col;
+          if (kPaired) {
+            n = n0 + (uint32_t)(wn * 32 + 16 * (j & 1) + fi);
+            col = n + (j >= 2 ? a.n : 0u);
+          } else {
+            n = n0 + (uint32_t)(wcol[j] + fi);
+            col = n;
+          }
+          if (t < a.m && n < a.n) pr[col] = acc[i][j][r] * inv;
+        }
+        continue;
+      }
       if (kPaired) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -370,11 +393,33 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
   }
 }
 
+// Sum of the K-range partials of output (t, n) in range order, then the
+// epilogue: partner = column n ^ 1 (RoPE) or the up value of n (paired).
+template <class Ep>
+__global__ void k_gemm_reduce(GemmArgs a, Ep ep) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (uint64_t)a.m * a.n) return;
+  const uint32_t t = (uint32_t)(idx / a.n), n = (uint32_t)(idx % a.n);
+  const uint32_t ncols = EpTraits<Ep>::kPaired ? 2 * a.n : a.n;
+  float v = 0.f, partner = 0.f;
+  for (uint32_t z = 0; z < a.ksplit; z++) {
+    const float* pr = a.part + ((uint64_t)z * a.m + t) * ncols;
+    v += pr[n];
+    if (EpTraits<Ep>::kPaired) partner += pr[n + a.n];
+    else if (EpTraits<Ep>::kNeighbor && (n ^ 1u) < a.n) partner += pr[n ^ 1u];
+  }
+  ep(t, n, v, partner);
+}
+
 template <int T, class Ep>
 hipError_t go(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   const uint32_t bn = EpTraits<Ep>::kPaired ? kBN / 2 : kBN;
-  dim3 grid((a.n + bn - 1) / bn, (a.m + kBM - 1) / kBM);
+  dim3 grid((a.n + bn - 1) / bn, (a.m + kBM - 1) / kBM, a.ksplit);
   hipLaunchKernelGGL((k_gemm<T, Ep>), grid, dim3(kThreads), 0, st, a, ep);
+  if (a.ksplit > 1) {
+    const uint64_t total = (uint64_t)a.m * a.n;
+    hipLaunchKernelGGL((k_gemm_reduce<Ep>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, ep);
+  }
   return hipGetLastError();
 }
 
@@ -385,6 +430,7 @@ hipError_t dispatch(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   if (EpTraits<Ep>::kPaired && (a.w1.type != a.w0.type || a.w1.rows != a.w0.rows || a.w1.cols != a.w0.cols))
     return hipErrorInvalidValue;
   if (a.w0.cols != a.k) return hipErrorInvalidValue;
+  if (a.ksplit == 0 || a.kps == 0) return hipErrorInvalidValue;
   switch (a.w0.type) {
     case T_Q4K: return go<T_Q4K, Ep>(a, ep, st);
     case T_Q6K: return go<T_Q6K, Ep>(a, ep, st);
@@ -394,7 +440,11 @@ hipError_t dispatch(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   }
 }
 
-GemmArgs args_of(const GemmIn& in, const GemmW& w) {
+// Tiles of fewer than two workgroups per CU split K over grid.z (at least 8
+// steps per range), as far as the partial buffer holds them.
+constexpr uint32_t kTargetWgs = 512, kMinStepsPerSplit = 8;
+
+GemmArgs args_of(const GemmIn& in, const GemmW& w, bool paired) {
   GemmArgs a{};
   a.a = in.a;
   a.rowmax = in.rowmax;
@@ -404,6 +454,17 @@ GemmArgs args_of(const GemmIn& in, const GemmW& w) {
   a.w0 = w;
   a.w1 = w;
   a.n = w.rows;
+  const uint32_t nk = a.k / kBK, bn = paired ? kBN / 2 : kBN;
+  const uint64_t tiles = (uint64_t)((a.n + bn - 1) / bn) * ((a.m + kBM - 1) / kBM);
+  uint32_t split = 1;
+  if (in.part && tiles < kTargetWgs) {
+    split = (uint32_t)std::min<uint64_t>((kTargetWgs + tiles - 1) / tiles, std::max<uint32_t>(1, nk / kMinStepsPerSplit));
+    const uint64_t per = (uint64_t)a.m * a.n * (paired ? 2 : 1) * 4;
+    split = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>({split, in.part_bytes / per, 64}));
+  }
+  a.kps = (nk + split - 1) / split;
+  a.ksplit = (nk + a.kps - 1) / a.kps;
+  a.part = a.ksplit > 1 ? in.part : nullptr;
   return a;
 }
 
@@ -466,26 +527,26 @@ __global__ void k_rmsnorm_rows(const float* x, const float* w, uint32_t n, float
 bool gemm_type(uint32_t t) { return t == T_Q4K || t == T_Q6K || t == T_Q8_0 || t == T_Q4_0; }
 
 hipError_t gemm_store(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, hipStream_t st) {
-  return dispatch(args_of(in, w), EpStore{y, ldy}, st);
+  return dispatch(args_of(in, w, false), EpStore{y, ldy}, st);
 }
 
 hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ldx, hipStream_t st) {
-  return dispatch(args_of(in, w), EpResid{x, ldx}, st);
+  return dispatch(args_of(in, w, false), EpResid{x, ldx}, st);
 }
 
 hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, uint32_t pos0,
                      uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st) {
   if (head_dim == 0 || head_dim % 2 || rope_dim % 2 || rope_dim > head_dim) return hipErrorInvalidValue;
-  return dispatch(args_of(in, w), EpRope{y, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs}, st);
+  return dispatch(args_of(in, w, false), EpRope{y, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs}, st);
 }
 
 hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, hipStream_t st) {
-  return dispatch(args_of(in, w), EpRows{y, ldy, row0}, st);
+  return dispatch(args_of(in, w, false), EpRows{y, ldy, row0}, st);
 }
 
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,
                        hipStream_t st) {
-  GemmArgs a = args_of(in, gate);
+  GemmArgs a = args_of(in, gate, true);
   a.w1 = up;
   return dispatch(a, EpSwiglu{mid, ld}, st);
 }

@@ -88,6 +88,8 @@ struct GemmIn {
   const float* a;
   const uint32_t* rowmax;
   uint32_t m, lda;
+  float* part = nullptr;     // optional workspace for split-K partial tiles
+  uint64_t part_bytes = 0;
 };
 bool gemm_type(uint32_t type);
 // y[t * ldy + n] = (A W^T)[t][n]
