@@ -36,7 +36,7 @@ CTX = 2048
 METRIC = "decode tok/s, 8B Q4_K_M bs=1, 1×MI355X; % of HBM-BW roofline"
 KCLASS = ["embed", "qkv_gemv", "attention", "attn_output_gemv", "ffn_gate_up_gemv", "ffn_down_gemv",
           "output_head_gemv", "finalize"]
-KERNEL_NAMES = {1: "k_gemv_mfma<EpiQkv, Q4_K, Q6_K>", 2: "k_attn_decode<128, 4> + k_attn_merge<128, 4>",
+KERNEL_NAMES = {1: "k_gemv_mfma<EpiQkv, Q4_K, Q6_K>", 2: "k_attn_decode<128, G> + k_attn_merge<128, G>",
                 3: "k_gemv_mfma<EpiResidual, Q4_K>", 4: "k_gemv_mfma<EpiSwiglu, Q4_K>",
                 5: "k_gemv_mfma<EpiResidual, Q6_K>", 6: "k_gemv_mfma<EpiLogits, Q6_K>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
@@ -50,11 +50,15 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--model", choices=["8b", "70b"], default="8b",
+                    help="8b: Llama-3-8B shape, 2048-token context (the headline); 70b: Llama-3-70B shape, "
+                         "8192-token context")
+    ap.add_argument("--steps", type=int, default=None, help="decode tokens timed (8b: 256, 70b: 128)")
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--ctx", type=int, default=CTX)
+    ap.add_argument("--ctx", type=int, default=None, help="context tokens before the timed decode (8b: 2048, 70b: 8192)")
     ap.add_argument("--model-dir", default=os.environ.get("IFX_BENCH_DIR", os.path.join(tempfile.gettempdir(), "inferox_bench")))
-    ap.add_argument("--cpu-steps", type=int, default=1, help="oracle decode steps for cpu_baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=None,
+                    help="oracle decode steps for cpu_baseline (0: skip; default 1 for 8b, 0 for 70b)")
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="direct launches instead of the step graph")
@@ -62,7 +66,12 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
     ap.add_argument("--prefill-reps", type=int, default=3)
-    return ap.parse_args()
+    args = ap.parse_args()
+    big = args.model == "70b"
+    args.steps = args.steps if args.steps is not None else (128 if big else 256)
+    args.ctx = args.ctx if args.ctx is not None else (8192 if big else CTX)
+    args.cpu_steps = args.cpu_steps if args.cpu_steps is not None else (0 if big else 1)
+    return args
 
 
 def copy_probe():
@@ -199,7 +208,7 @@ def main():
     from inferox_amd._native import check
     L = _native.lib()
 
-    spec = synth.LLAMA3_8B
+    spec = synth.LLAMA3_70B if args.model == "70b" else synth.LLAMA3_8B
     os.makedirs(args.model_dir, exist_ok=True)
     path = os.path.join(args.model_dir, f"{spec.name}-seed1234.gguf")
     if not os.path.exists(path) or os.path.getsize(path) < spec.gguf_bytes():
@@ -224,9 +233,9 @@ def main():
     if args.prefill_only:
         res = measure_prefill(L, model, spec, [512, 2048], args.prefill_reps)
         L.ifx_model_close(model)
-        print(json.dumps({"metric": "prefill tok/s, 8B Q4_K_M, 1xMI355X", "unit": "tok/s",
+        print(json.dumps({"metric": f"prefill tok/s, {args.model.upper()} Q4_K_M, 1xMI355X", "unit": "tok/s",
                           "value": res["p2048"]["tok_s"], "higher_is_better": True, "dtype": "f16x3 (f32 accumulate)",
-                          "data": "synthetic", "config": {"workload": "llama3-8b-shape Q4_K_M batched prefill of "
+                          "data": "synthetic", "config": {"workload": f"{spec.name}-shape Q4_K_M batched prefill of "
                                                                       "seeded 512- and 2048-id prompts"},
                           "prefill": res}), flush=True)
         return
@@ -299,7 +308,8 @@ def main():
         alg = wbytes[dom] + extra
         achieved = alg / (avg[dom] * 1e-3)
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic_for(KCLASS[dom]),
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                    "traffic": traffic_for(KCLASS[dom]) if args.model == "8b" else None,
                     "kernel": KERNEL_NAMES.get(dom, KCLASS[dom]), "kernel_class": KCLASS[dom],
                     "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2)}
         prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "launches_per_step": int(launches[k]),
@@ -324,10 +334,10 @@ def main():
     L.ifx_model_close(model)
 
     line = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "metric": METRIC if args.model == "8b" else METRIC.replace("8B", "70B"), "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"llama3-8b-shape Q4_K_M greedy decode, bs=1, {args.ctx}-token context from a GPU "
+        "config": {"workload": f"{spec.name}-shape Q4_K_M greedy decode, bs=1, {args.ctx}-token context from a GPU "
                                f"prefill of seeded ids, {K} tokens", "ctx": args.ctx, "decode_tokens": K,
                    "batch": 1},
         "roofline": roofline,

@@ -64,6 +64,8 @@ constexpr uint32_t kPartBytes = 48;   // 3 digit planes x 16 bytes per 16-elemen
 constexpr uint32_t kBlockA = 16 * kPartBytes;  // A bytes of one 256-element block
 constexpr uint32_t kZeroBytes = 512;  // read by the lanes that feed zero A rows
 constexpr uint32_t kM4 = 0x0F0F0F0Fu, kM2 = 0x30303030u;
+// dynamic LDS limit: the CU's 160 KiB less the kernel's static arrays (< 4 KiB)
+constexpr size_t kMaxDynLds = 156 * 1024;
 
 struct MArgs {
   GemvSeg seg[3];      // paired: seg[0] gate, seg[1] up
@@ -520,9 +522,9 @@ int cu_count() {
 template <class Epi, int TA, int TB, int D, bool NORM>
 hipError_t go_one(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
   static bool opted = false;
-  if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns
+  if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns (the 70B down projection: 28672)
     hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
     if (e != hipSuccess) return e;
     opted = true;
   }
@@ -580,7 +582,7 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   a.xs_off = 3 * a.cols;                    // digit planes: 48 bytes per 16 elements
   a.zero_off = a.xs_off + a.cols / 2;       // group sums: 16 bytes per 32 elements
   const size_t lds = a.zero_off + kZeroBytes;
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (lds > kMaxDynLds) return hipErrorInvalidValue;
   bool mixed = false;
   for (int s = 1; s < a.nseg; s++) mixed |= L.seg[s].type != L.seg[0].type;
   const size_t want = mixed ? kMaxBlocksPerCu : 1;

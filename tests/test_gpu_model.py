@@ -199,3 +199,35 @@ def test_8b_shape_two_layers(tmpdir_session):
         tok = orc.argmax(ref)[1]
         assert lg[tok] == lg.max()
     g.close()
+
+
+def test_70b_shape_two_layers(tmpdir_session):
+    """Llama-3-70B widths (dim 8192, ffn 28672, GQA 64/8, vocab 128256), two
+    layers: decode from a seeded KV context (group-8 attention, 28672-column
+    down projection) and a batched prefill chunk, against the oracle."""
+    spec = synth.reduced(synth.LLAMA3_70B, n_layers=2, ctx=512)
+    p = str(tmpdir_session / "l70b_2l.gguf")
+    synth.write_llama(p, spec, seed=70)
+    g, o = GpuModel(p), orc.Model(p)
+    c = o.cfg
+    L = 300
+    kvd = c.n_kv_heads * c.head_dim
+    k = synth.normal_f32(c.n_layers * L * kvd, seed=23)
+    v = synth.normal_f32(c.n_layers * L * kvd, seed=24)
+    s, kv = g.session(512), o.kv(512)
+    assert s.kv_import(k, v, L) == 0 and kv.import_(k, v, L) == 0
+    tok = 4242
+    for step in range(3):
+        rc, lg = s.decode_step(tok)
+        _, ref = o.decode_step(kv, tok)
+        assert rc == 0
+        assert rel_l2(lg, ref) < TOL, step
+        tok = orc.argmax(ref)[1]
+        assert lg[tok] == lg.max()
+    # a batched prefill chunk after the decoded rows (chunk-only attention)
+    ids = synth.token_ids(64, spec.vocab, seed=71)
+    rc, lg = s.prefill(ids)
+    orc_rc, ref = o.prefill(kv, ids)
+    assert rc == 0 and orc_rc == 0
+    assert max(rel_l2(lg[t], ref[t]) for t in range(len(ids))) < TOL
+    g.close()
