@@ -66,6 +66,7 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
     ap.add_argument("--prefill-reps", type=int, default=3)
+    ap.add_argument("--prefill-sizes", default="512,2048", help="prompt lengths of the prefill measurement")
     args = ap.parse_args()
     big = args.model == "70b"
     args.steps = args.steps if args.steps is not None else (128 if big else 256)
@@ -231,10 +232,11 @@ def main():
         f"({gguf_b.value / 1e9:.3f} GB stored)")
 
     if args.prefill_only:
-        res = measure_prefill(L, model, spec, [512, 2048], args.prefill_reps)
+        sizes = [int(x) for x in args.prefill_sizes.split(",")]
+        res = measure_prefill(L, model, spec, sizes, args.prefill_reps)
         L.ifx_model_close(model)
         print(json.dumps({"metric": f"prefill tok/s, {args.model.upper()} Q4_K_M, 1xMI355X", "unit": "tok/s",
-                          "value": res["p2048"]["tok_s"], "higher_is_better": True, "dtype": "f16x3 (f32 accumulate)",
+                          "value": res[f"p{sizes[-1]}"]["tok_s"], "higher_is_better": True, "dtype": "f16x3 (f32 accumulate)",
                           "data": "synthetic", "config": {"workload": f"{spec.name}-shape Q4_K_M batched prefill of "
                                                                       "seeded 512- and 2048-id prompts"},
                           "prefill": res}), flush=True)
@@ -330,7 +332,8 @@ def main():
         log(f"cpu: {med:.2f} s/step; first pick cpu={toks[0]} gpu={int(out[0])}")
 
     L.ifx_session_destroy(sess)
-    prefill = None if args.no_profile else measure_prefill(L, model, spec, [512, 2048], 1)
+    prefill = None if args.no_profile else measure_prefill(
+        L, model, spec, [int(x) for x in args.prefill_sizes.split(",")], 1)
     L.ifx_model_close(model)
 
     line = {
