@@ -74,7 +74,7 @@ struct EpiQkv {
     if (s == 0) {
       e.q_out[r] = v;
     } else {
-      const uint64_t off = (uint64_t)w.len * e.kv_dim + r;
+      const uint64_t off = ((uint64_t)(r / e.head_dim) * e.max_seq + w.len) * e.head_dim + r % e.head_dim;
       if (s == 1) e.k_cache[off] = v;
       else e.v_cache[off] = v;
     }

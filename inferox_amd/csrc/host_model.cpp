@@ -228,13 +228,15 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       g.x = s->hidden;
       g.norm_w = L.attn_norm;
       g.eps = c.norm_eps;
-      QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd};
+      QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd,
+               (uint32_t)s->max_seq};
       IFX_HIP(gemv_qkv(g, e, st));
       return IFX_OK;
     }
     case 2: {
       AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
-                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
+                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
+                 (uint32_t)s->max_seq};
       IFX_HIP(launch_attn_decode(a, st));
       return IFX_OK;
     }
@@ -381,10 +383,12 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     float* vc = s->vc + l * s->max_seq * kvd;
     IFX_HIP(launch_rmsnorm_rows_to(w.x, L.attn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
     const GemmIn in{w.a, w.rmax, N, D, w.part, kSplitPartBytes};
-    IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, 0, pos0, hd, rd, s->rope_cs, st));
-    IFX_HIP(gemm_rope(in, gw(L.k), kc, kvd, row0, pos0, hd, rd, s->rope_cs, st));
-    IFX_HIP(gemm_rows(in, gw(L.v), vc, kvd, row0, st));
-    const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd, causal};
+    const uint64_t kv_hs = s->max_seq * hd;  // head stride of the head-major cache
+    IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, hd, 0, pos0, hd, rd, s->rope_cs, st));
+    IFX_HIP(gemm_rope(in, gw(L.k), kc, hd, kv_hs, row0, pos0, hd, rd, s->rope_cs, st));
+    IFX_HIP(gemm_rows(in, gw(L.v), vc, hd, kv_hs, row0, hd, st));
+    const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd,
+                             (uint32_t)s->max_seq, causal};
     IFX_HIP(launch_attn_prefill(aa, st));
     IFX_HIP(launch_rowmax(w.att, N, D, D, w.rmax, st));
     IFX_HIP(gemm_residual(GemmIn{w.att, w.rmax, N, D, w.part, kSplitPartBytes}, gw(L.o), w.x, D, st));
@@ -781,11 +785,14 @@ int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len) 
   if (!s || (len && (!k || !v))) return set_error(IFX_E_INVALID_ARG, "null argument");
   if (len > s->max_seq) return set_error(IFX_E_KV_FULL, "import of %llu rows", (unsigned long long)len);
   const ifx_config& c = s->m->cfg;
-  const uint64_t kvd = c.n_kv_heads * c.head_dim;
-  for (uint64_t l = 0; l < c.n_layers; l++) {
-    IFX_HIP(hipMemcpyAsync(s->kc + l * s->max_seq * kvd, k + l * len * kvd, len * kvd * 4, hipMemcpyHostToDevice, s->stream));
-    IFX_HIP(hipMemcpyAsync(s->vc + l * s->max_seq * kvd, v + l * len * kvd, len * kvd * 4, hipMemcpyHostToDevice, s->stream));
-  }
+  const uint64_t kvd = c.n_kv_heads * c.head_dim, hd = c.head_dim;
+  // reference rows [t][kv_dim] -> the head-major device cache, one strided copy per (layer, head)
+  for (uint64_t l = 0; l < c.n_layers && len; l++)
+    for (uint64_t h = 0; h < c.n_kv_heads; h++) {
+      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd, host = l * len * kvd + h * hd;
+      IFX_HIP(hipMemcpy2DAsync(s->kc + dev, hd * 4, k + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
+      IFX_HIP(hipMemcpy2DAsync(s->vc + dev, hd * 4, v + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
+    }
   IFX_TRY(state_op(s, STATE_RESET, 0, (uint32_t)len));
   IFX_HIP(hipStreamSynchronize(s->stream));
   s->len = len;
@@ -798,11 +805,14 @@ int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len) {
   if (len > s->len) return set_error(IFX_E_INVALID_ARG, "export of %llu rows, %llu cached", (unsigned long long)len, (unsigned long long)s->len);
   const ifx_config& c = s->m->cfg;
   const uint64_t kvd = c.n_kv_heads * c.head_dim;
+  const uint64_t hd = c.head_dim;
   IFX_HIP(hipStreamSynchronize(s->stream));
-  for (uint64_t l = 0; l < c.n_layers; l++) {
-    IFX_HIP(hipMemcpy(k + l * len * kvd, s->kc + l * s->max_seq * kvd, len * kvd * 4, hipMemcpyDeviceToHost));
-    IFX_HIP(hipMemcpy(v + l * len * kvd, s->vc + l * s->max_seq * kvd, len * kvd * 4, hipMemcpyDeviceToHost));
-  }
+  for (uint64_t l = 0; l < c.n_layers && len; l++)
+    for (uint64_t h = 0; h < c.n_kv_heads; h++) {
+      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd, host = l * len * kvd + h * hd;
+      IFX_HIP(hipMemcpy2D(k + host, kvd * 4, s->kc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
+      IFX_HIP(hipMemcpy2D(v + host, kvd * 4, s->vc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
+    }
   return IFX_OK;
 }
 
@@ -923,13 +933,15 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
       GemvLaunch g;
       g.seg[0] = seg_of(L.q); g.seg[1] = seg_of(L.k); g.seg[2] = seg_of(L.v);
       g.nseg = 3; g.cols = (uint32_t)D; g.x = X + t * D; g.norm_w = L.attn_norm; g.eps = c.norm_eps;
-      QkvEpi e{Q + t * D, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, (uint32_t)kvd};
+      QkvEpi e{Q + t * D, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, (uint32_t)kvd,
+               (uint32_t)s->max_seq};
       hip(gemv_qkv(g, e, st));
     }
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
       hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
       AttnArgs a{Q + t * D, kc, vc, A + t * D, s->partial, s->state, (uint32_t)c.n_heads,
-                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk};
+                 (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
+                 (uint32_t)s->max_seq};
       hip(launch_attn_decode(a, st));
     }
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {

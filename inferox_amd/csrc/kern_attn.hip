@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
 
   const uint32_t c = blockIdx.x, hk = blockIdx.y;
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
-  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4, kvd = a.n_kv_heads * HD;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
   const uint32_t lo = a.state->attn_lo;
   const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
   const uint32_t nrows = hi > lo ? hi - lo : 0;
@@ -111,7 +111,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t r0 = wave * kRowsPerWave;  // first chunk row of this wave
   // rows past the chunk's end read the last real row (weight 0)
-  auto cache_row = [&](uint32_t r) -> uint64_t { return (uint64_t)(t0 + min(r, n - 1)) * kvd + hk * HD; };
+  auto cache_row = [&](uint32_t r) -> uint64_t { return ((uint64_t)hk * a.max_seq + t0 + min(r, n - 1)) * HD; };
 
   // ---- K, V and q loads, all in flight together ----
   const uint32_t kr_row = r0 + lane / 4, kq = lane & 3;

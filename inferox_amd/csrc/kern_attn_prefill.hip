@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_prefill(AttnPrefillArgs a) {
   const uint32_t nqb = (a.n + kQ - 1) / kQ;
   const uint32_t qb = nqb - 1 - blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads;
   const uint32_t q0 = qb * kQ, group = a.n_heads / a.n_kv_heads, hk = h / group;
-  const uint32_t qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+  const uint32_t qd = a.n_heads * HD;
   const float sqrt_hd = sqrtf((float)HD);
 
   // ---- Q block: four threads per row, row scale by shuffles ----
@@ -157,7 +157,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_prefill(AttnPrefillArgs a) {
         const int col = 8 * (khalf * KCH + i);
         const uint32_t key = k0 + (uint32_t)kr;
         if (i < KCH && key < kend && col < HD) {
-          const float* src = a.k_cache + (uint64_t)(a.row0 + key) * kvd + hk * HD + col;
+          const float* src = a.k_cache + ((uint64_t)hk * a.max_seq + a.row0 + key) * HD + col;
           x0 = *(const float4*)src;
           x1 = *(const float4*)(src + 4);
         }
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_prefill(AttnPrefillArgs a) {
         const int col = 8 * vdc;
         const uint32_t key = k0 + (uint32_t)(8 * vkc + i);
         if (vtile && key < kend && col < HD) {
-          const float* src = a.v_cache + (uint64_t)(a.row0 + key) * kvd + hk * HD + col;
+          const float* src = a.v_cache + ((uint64_t)hk * a.max_seq + a.row0 + key) * HD + col;
           x0 = *(const float4*)src;
           x1 = *(const float4*)(src + 4);
         }

@@ -211,10 +211,19 @@ struct EpResid {  // x[t * ld + n] += v (src/ops.rs:212-217)
   }
 };
 
+// Output (t, n) of a q/k/v projection at y[(row0 + t) ld + (n / head_dim)
+// hstride + n % head_dim]: a row-major [t][heads * head_dim] buffer, or the
+// head-major KV cache.
+__device__ __forceinline__ uint64_t head_addr(uint32_t t, uint32_t n, uint32_t row0, uint32_t ld, uint64_t hstride,
+                                              uint32_t head_dim) {
+  return (uint64_t)(row0 + t) * ld + (uint64_t)(n / head_dim) * hstride + n % head_dim;
+}
+
 // RoPE on adjacent pairs (src/ops.rs:273-284) at position pos0 + t; `partner`
-// is column n ^ 1 of the same token.  Rows are written to y + (row0 + t) * ld.
+// is column n ^ 1 of the same token.
 struct EpRope {
   float* y;
+  uint64_t hstride;
   uint32_t ld, row0, pos0, head_dim, rope_dim, half;
   const float2* cs;  // [pos][rope_dim / 2]
   __device__ void operator()(uint32_t t, uint32_t n, float v, float partner) const {
@@ -224,15 +233,16 @@ struct EpRope {
       const float2 r = cs[(uint64_t)(pos0 + t) * half + (c >> 1)];
       out = (c & 1u) ? (partner * r.y) + (v * r.x) : (v * r.x) - (partner * r.y);
     }
-    y[(uint64_t)(row0 + t) * ld + n] = out;
+    y[head_addr(t, n, row0, ld, hstride, head_dim)] = out;
   }
 };
 
-struct EpRows {  // y[(row0 + t) * ld + n] = v (the V cache append)
+struct EpRows {  // the V cache append
   float* y;
-  uint32_t ld, row0;
+  uint64_t hstride;
+  uint32_t ld, row0, head_dim;
   __device__ void operator()(uint32_t t, uint32_t n, float v, float) const {
-    y[(uint64_t)(row0 + t) * ld + n] = v;
+    y[head_addr(t, n, row0, ld, hstride, head_dim)] = v;
   }
 };
 
@@ -534,14 +544,17 @@ hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ld
   return dispatch(args_of(in, w, false), EpResid{x, ldx}, st);
 }
 
-hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, uint32_t pos0,
-                     uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st) {
+hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st) {
   if (head_dim == 0 || head_dim % 2 || rope_dim % 2 || rope_dim > head_dim) return hipErrorInvalidValue;
-  return dispatch(args_of(in, w, false), EpRope{y, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs}, st);
+  return dispatch(args_of(in, w, false), EpRope{y, hstride, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs},
+                  st);
 }
 
-hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, hipStream_t st) {
-  return dispatch(args_of(in, w, false), EpRows{y, ldy, row0}, st);
+hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t head_dim, hipStream_t st) {
+  if (head_dim == 0) return hipErrorInvalidValue;
+  return dispatch(args_of(in, w, false), EpRows{y, hstride, ldy, row0, head_dim}, st);
 }
 
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,

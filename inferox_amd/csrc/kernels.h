@@ -57,13 +57,16 @@ struct GemvLaunch {
   bool paired = false;            // seg[0]/seg[1] rows interleaved per tile (gate/up)
 };
 
+// The device KV cache is head-major: per layer [n_kv_heads][max_seq][head_dim]
+// f32, so a kv head's rows are contiguous for the attention kernels (the
+// reference's [t][kv_dim] row order is what ifx_kv_import/export exchange).
 struct QkvEpi {
   float* q_out;          // [q rows]
-  float* k_cache;        // layer base, row-major [max_seq][kv_dim]
+  float* k_cache;        // layer base, [n_kv_heads][max_seq][head_dim]
   float* v_cache;
   const float2* rope_cs; // [max_pos][rope_dim/2] (cos, sin)
   const DevState* state;
-  uint32_t head_dim, rope_dim, kv_dim;
+  uint32_t head_dim, rope_dim, kv_dim, max_seq;
 };
 
 hipError_t gemv_store(const GemvLaunch& L, float* y, hipStream_t st);
@@ -96,11 +99,15 @@ bool gemm_type(uint32_t type);
 hipError_t gemm_store(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, hipStream_t st);
 // x[t * ldx + n] += (A W^T)[t][n]
 hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ldx, hipStream_t st);
-// RoPE at position pos0 + t, rows written to y + (row0 + t) * ldy
-hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, uint32_t pos0,
-                     uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st);
-// rows written to y + (row0 + t) * ldy (the V cache append)
-hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint32_t row0, hipStream_t st);
+// Output (t, n) of the q/k/v GEMMs goes to y[(row0 + t) ldy + (n / head_dim) hstride + n % head_dim]:
+// row-major [t][heads * head_dim] with ldy = heads * head_dim, hstride = head_dim;
+// the head-major KV cache with ldy = head_dim, hstride = max_seq * head_dim.
+// RoPE at position pos0 + t
+hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st);
+// the V cache append
+hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t head_dim, hipStream_t st);
 // mid[t * ld + n] = swiglu(gate row n . A[t], up row n . A[t])
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,
                        hipStream_t st);
@@ -115,10 +122,10 @@ hipError_t launch_rmsnorm_rows_to(const float* x, const float* w, uint32_t rows,
 // (causal) or row0 .. row0 + n - 1; out[t] f32, the row's max |out| in rowmax.
 struct AttnPrefillArgs {
   const float* q;        // [n][n_heads * head_dim]
-  const float* k_cache;  // layer base [max_seq][kv_dim]
+  const float* k_cache;  // layer base [n_kv_heads][max_seq][head_dim]
   const float* v_cache;
   float* out;            // [n][n_heads * head_dim]
-  uint32_t n, row0, n_heads, n_kv_heads, head_dim;
+  uint32_t n, row0, n_heads, n_kv_heads, head_dim, max_seq;
   bool causal;
 };
 bool attn_prefill_head_dim(uint32_t head_dim);
@@ -148,12 +155,12 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t st);
 // ---- attention (kern_attn.hip) ----
 struct AttnArgs {
   const float* q;        // [n_heads * head_dim]
-  const float* k_cache;  // layer base [max_seq][kv_dim]
+  const float* k_cache;  // layer base [n_kv_heads][max_seq][head_dim]
   const float* v_cache;
   float* out;            // [n_heads * head_dim]
   float* partial;        // [n_kv][max_chunks][attn_partial_floats(group, head_dim)]
   const DevState* state;
-  uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk;
+  uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk, max_seq;
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
 // floats of one partial record (per kv head and chunk): o[group][head_dim],
