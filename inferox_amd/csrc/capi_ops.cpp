@@ -128,6 +128,15 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
       bound = (v > bound || v != v) ? v : bound;
     });
     t->L.abs_bound = bound;
+    if (type == T_Q4K) {
+      float dm = 0.f;
+      parallel_ranges(t->L.n_blocks, 65536, [&](uint64_t b0, uint64_t b1) {
+        const float v = block_dmin_max(src, b0, b1);
+        std::lock_guard<std::mutex> g(mu);
+        dm = (v > dm || v != v) ? v : dm;
+      });
+      t->L.dmin_max = dm;
+    }
   }
   if (type == T_F32 || type == T_F16) t->L.abs_bound = INFINITY;
   if (e != hipSuccess) {
@@ -275,26 +284,28 @@ int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream) {
 int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream) {
   IFX_TRY(device_init());
   if (!w || (m && (!a || !c))) return set_error(IFX_E_INVALID_ARG, "null argument");
-  // two rows or more: the prefill GEMM (fp16 matrix cores, hi/lo operand pairs)
-  // for the types and magnitudes it takes; the GEMV row by row otherwise
-  if (m >= 2 && m <= 0xffffffffull && gemm_type(w->L.type) && w->L.abs_bound <= 32768.f && w->L.cols % 32 == 0) {
+  // two rows or more: the prefill GEMM (fp16 matrix cores, hi/lo activation
+  // pairs) for the matrices it takes; the GEMV row by row otherwise
+  if (m >= 2 && m <= 0xffffffffull && w->L.cols <= 0xffffffffull && gemm_type(w->L.type) && gemm_layout_ok(w->L)) {
     hipStream_t st = stream_of(stream);
-    uint32_t* rmax = nullptr;
-    float* part = nullptr;
+    const uint64_t k = w->L.cols;
     const uint64_t part_bytes = 64ull << 20;  // split-K partial tiles of short inputs
-    IFX_HIP(hipMallocAsync((void**)&rmax, m * 4, st));
-    hipError_t e = hipMallocAsync((void**)&part, part_bytes, st);
-    if (e == hipSuccess) e = launch_rowmax(a, (uint32_t)m, (uint32_t)w->L.cols, (uint32_t)w->L.cols, rmax, st);
+    // one allocation: hi, lo planes, group sums, row exponents, partial tiles
+    const uint64_t bh = (m * k * 2 + 255) & ~255ull, bg = (m * (k / 256 + 1) * 32 + 255) & ~255ull,
+                   br = (m * 4 + 255) & ~255ull;
+    uint8_t* buf = nullptr;
+    IFX_HIP(hipMallocAsync((void**)&buf, 2 * bh + bg + br + part_bytes, st));
+    const GemmIn in{(const uint16_t*)buf, (const uint16_t*)(buf + bh), (const uint16_t*)(buf + 2 * bh),
+                    (const int*)(buf + 2 * bh + bg), (uint32_t)m, (uint32_t)k, (float*)(buf + 2 * bh + bg + br),
+                    part_bytes};
+    hipError_t e = launch_prep_rows(a, (uint32_t)m, (uint32_t)k, (uint32_t)k, nullptr, 0.f, in, st);
     if (e == hipSuccess) {
-      const GemmIn in{a, rmax, (uint32_t)m, (uint32_t)w->L.cols, part, part_bytes};
       const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols};
       e = gemm_store(in, gw, c, (uint32_t)w->L.rows, st);
     }
-    const hipError_t ef = hipFreeAsync(rmax, st);
-    const hipError_t ep = part ? hipFreeAsync(part, st) : hipSuccess;
+    const hipError_t ef = hipFreeAsync(buf, st);
     IFX_HIP(e);
     IFX_HIP(ef);
-    IFX_HIP(ep);
     return IFX_OK;
   }
   for (uint64_t i = 0; i < m; i++) {

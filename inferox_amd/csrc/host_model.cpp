@@ -72,9 +72,11 @@ struct ifx_session {
     uint64_t cap = 0, logit_rows = 0;
     void* alloc = nullptr;
     void* logits = nullptr;
-    float *x = nullptr, *q = nullptr, *att = nullptr, *a = nullptr, *mid = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *mid = nullptr;
     float* part = nullptr;  // split-K partial tiles of the GEMMs
-    uint32_t* rmax = nullptr;
+    // the GEMM activation operand (launch_prep_rows), sized for the widest input
+    uint16_t *ahi = nullptr, *alo = nullptr, *gsum = nullptr;
+    int* rexp = nullptr;
   } ws;
 };
 
@@ -158,13 +160,10 @@ GemvSeg seg_of(const ifx_tensor* t) {
   return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows};
 }
 
-// The batched prefill GEMM takes the quantized types whose elements stay in
-// the fp16 range (their hi/lo split, kern_gemm.hip), 32-column blocks, and a
-// head dim the prefill attention kernel is built for.
-constexpr float kGemmAbsMax = 32768.f;
-bool gemm_tensor_ok(const ifx_tensor* t) {
-  return t && gemm_type(t->L.type) && t->L.abs_bound <= kGemmAbsMax && t->L.cols % 32 == 0;
-}
+// The batched prefill GEMM takes the quantized matrices whose operands it can
+// carry exactly (gemm_layout_ok) and a head dim the prefill attention kernel
+// is built for.
+bool gemm_tensor_ok(const ifx_tensor* t) { return t && gemm_type(t->L.type) && gemm_layout_ok(t->L); }
 bool gemm_eligible(const ifx_model* m) {
   const ifx_config& c = m->cfg;
   if (!attn_prefill_head_dim((uint32_t)c.head_dim) || c.hidden_size != c.n_heads * c.head_dim ||
@@ -334,7 +333,9 @@ int ensure_ws(ifx_session* s, uint64_t n) {
   const ifx_config& c = s->m->cfg;
   const uint64_t D = c.hidden_size, F = c.intermediate_size;
   auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
-  const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), br = al(n * 4), bp = kSplitPartBytes;
+  const uint64_t W = std::max(D, F);  // widest GEMM input
+  const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), bh = al(n * W * 2), bg = al(n * (W / 256 + 1) * 32),
+                 br = al(n * 4), bp = kSplitPartBytes;
   if (s->ws.alloc) {
     IFX_HIP(hipStreamSynchronize(s->stream));
     IFX_HIP(hipFree(s->ws.alloc));
@@ -342,16 +343,19 @@ int ensure_ws(ifx_session* s, uint64_t n) {
     s->ws.cap = 0;
   }
   void* p = nullptr;
-  if (hipMalloc(&p, 4 * bx + bm + br + bp) != hipSuccess)
+  if (hipMalloc(&p, 3 * bx + bm + 2 * bh + bg + br + bp) != hipSuccess)
     return set_error(IFX_E_OOM, "prefill workspace of %llu rows", (unsigned long long)n);
   uint8_t* b = (uint8_t*)p;
   s->ws.x = (float*)b;
   s->ws.q = (float*)(b + bx);
   s->ws.att = (float*)(b + 2 * bx);
-  s->ws.a = (float*)(b + 3 * bx);
-  s->ws.mid = (float*)(b + 4 * bx);
-  s->ws.rmax = (uint32_t*)(b + 4 * bx + bm);
-  s->ws.part = (float*)(b + 4 * bx + bm + br);
+  b += 3 * bx;
+  s->ws.mid = (float*)b;
+  s->ws.ahi = (uint16_t*)(b + bm);
+  s->ws.alo = (uint16_t*)(b + bm + bh);
+  s->ws.gsum = (uint16_t*)(b + bm + 2 * bh);
+  s->ws.rexp = (int*)(b + bm + 2 * bh + bg);
+  s->ws.part = (float*)(b + bm + 2 * bh + bg + br);
   s->ws.alloc = p;
   s->ws.cap = n;
   return IFX_OK;
@@ -376,13 +380,15 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
   const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim), row0 = (uint32_t)start;
   const uint32_t pos0 = s->rope_mode == IFX_ROPE_ABSOLUTE ? row0 : 0u;
   auto& w = s->ws;
+  // the GEMM operand of rows of k columns (prep writes it, the GEMMs read it)
+  auto op = [&](uint32_t rows, uint32_t k) { return GemmIn{w.ahi, w.alo, w.gsum, w.rexp, rows, k, w.part, kSplitPartBytes}; };
   IFX_HIP(launch_embed_rows(devw(m->embd), s->feed_ids, n, w.x, st));
   for (size_t l = 0; l < m->layers.size(); l++) {
     const LayerDev& L = m->layers[l];
     float* kc = s->kc + l * s->max_seq * kvd;
     float* vc = s->vc + l * s->max_seq * kvd;
-    IFX_HIP(launch_rmsnorm_rows_to(w.x, L.attn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
-    const GemmIn in{w.a, w.rmax, N, D, w.part, kSplitPartBytes};
+    const GemmIn in = op(N, D);
+    IFX_HIP(launch_prep_rows(w.x, N, D, D, L.attn_norm, c.norm_eps, in, st));
     const uint64_t kv_hs = s->max_seq * hd;  // head stride of the head-major cache
     IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, hd, 0, pos0, hd, rd, s->rope_cs, st));
     IFX_HIP(gemm_rope(in, gw(L.k), kc, hd, kv_hs, row0, pos0, hd, rd, s->rope_cs, st));
@@ -390,12 +396,13 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd,
                              (uint32_t)s->max_seq, causal};
     IFX_HIP(launch_attn_prefill(aa, st));
-    IFX_HIP(launch_rowmax(w.att, N, D, D, w.rmax, st));
-    IFX_HIP(gemm_residual(GemmIn{w.att, w.rmax, N, D, w.part, kSplitPartBytes}, gw(L.o), w.x, D, st));
-    IFX_HIP(launch_rmsnorm_rows_to(w.x, L.ffn_norm, N, D, c.norm_eps, w.a, w.rmax, st));
-    IFX_HIP(gemm_swiglu(GemmIn{w.a, w.rmax, N, D, w.part, kSplitPartBytes}, gw(L.gate), gw(L.up), w.mid, F, st));
-    IFX_HIP(launch_rowmax(w.mid, N, F, F, w.rmax, st));
-    IFX_HIP(gemm_residual(GemmIn{w.mid, w.rmax, N, F, w.part, kSplitPartBytes}, gw(L.down), w.x, D, st));
+    IFX_HIP(launch_prep_rows(w.att, N, D, D, nullptr, 0.f, in, st));
+    IFX_HIP(gemm_residual(in, gw(L.o), w.x, D, st));
+    IFX_HIP(launch_prep_rows(w.x, N, D, D, L.ffn_norm, c.norm_eps, in, st));
+    IFX_HIP(gemm_swiglu(in, gw(L.gate), gw(L.up), w.mid, F, st));
+    const GemmIn inf = op(N, F);
+    IFX_HIP(launch_prep_rows(w.mid, N, F, F, nullptr, 0.f, inf, st));
+    IFX_HIP(gemm_residual(inf, gw(L.down), w.x, D, st));
   }
   // the last row's greedy pick, recorded as a step records it (k_finalize)
   IFX_TRY(state_op(s, STATE_BATCH, 0, N));
@@ -423,9 +430,9 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     }
     for (uint64_t r0 = 0; r0 < n; r0 += rows) {
       const uint32_t nr = (uint32_t)std::min<uint64_t>(rows, n - r0);
-      IFX_HIP(launch_rmsnorm_rows_to(w.x + r0 * D, m->out_norm, nr, D, c.norm_eps, w.a, w.rmax, st));
-      IFX_HIP(gemm_store(GemmIn{w.a, w.rmax, nr, D, w.part, kSplitPartBytes}, gw(m->output), (float*)w.logits,
-                         (uint32_t)V, st));
+      const GemmIn in = op(nr, D);
+      IFX_HIP(launch_prep_rows(w.x + r0 * D, nr, D, D, m->out_norm, c.norm_eps, in, st));
+      IFX_HIP(gemm_store(in, gw(m->output), (float*)w.logits, (uint32_t)V, st));
       IFX_HIP(hipMemcpyAsync(logits_out + r0 * V, w.logits, (size_t)nr * V * 4, hipMemcpyDeviceToHost, st));
     }
   }

@@ -177,6 +177,27 @@ static float host_f16(const uint8_t* p) {
   return (h & 0x8000u) ? -v : v;
 }
 
+float block_dmin_max(const uint8_t* src, uint64_t b0, uint64_t b1) {
+  float m = 0.f;
+  for (uint64_t b = b0; b < b1; b++) {
+    const float v = fabsf(host_f16(src + 144 * b + 2));
+    if (v != v) return v;
+    m = v > m ? v : m;
+  }
+  return m;
+}
+
+bool gemm_layout_ok(const DevLayout& L) {
+  if (!(L.abs_bound <= 3.0e38f)) return false;  // a non-finite block scale
+  switch (L.type) {
+    case T_Q4K: return L.cols % 256 == 0 && L.dmin_max * 2016.f <= 65504.f;  // 63 * 32 * dmin
+    case T_Q6K: return L.cols % 256 == 0;
+    case T_Q8_0:
+    case T_Q4_0: return L.cols % 32 == 0;
+    default: return false;
+  }
+}
+
 float block_abs_bound(uint32_t type, const uint8_t* src, uint64_t b0, uint64_t b1) {
   float m = 0.f;
   for (uint64_t b = b0; b < b1; b++) {

@@ -82,6 +82,7 @@ struct DevLayout {
   uint64_t body_bytes = 0, scal_bytes = 0;
   uint64_t gguf_bytes = 0;    // stored GGUF bytes of the same matrix
   float abs_bound = 0.f;      // bound on |element| from the block scales (inf: unbounded or non-finite)
+  float dmin_max = 0.f;       // Q4_K: largest |dmin| (NaN if any is NaN)
 };
 
 // Host-side repack of one matrix from GGUF block bytes into the device layout
@@ -97,6 +98,11 @@ void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t col
 // block scales alone (Q4_K: |d| 63 15 + |dmin| 63; Q6_K: |d| 255 32; Q8_0:
 // |d| 128; Q4_0: |d| 8); +inf for F32/F16/Q8_K or a non-finite scale.
 float block_abs_bound(uint32_t type, const uint8_t* src, uint64_t b0, uint64_t b1);
+// Largest |dmin| over Q4_K blocks [b0, b1) (NaN if one is NaN).
+float block_dmin_max(const uint8_t* src, uint64_t b0, uint64_t b1);
+// The batched prefill GEMM carries this matrix exactly: finite block scales,
+// whole blocks per row, and (Q4_K) -32 dmin mn inside the fp16 range.
+bool gemm_layout_ok(const DevLayout& L);
 
 }  // namespace ifx
 

@@ -4,33 +4,43 @@
 // C[t][n] = sum_k A[t][k] W[n][k], for t < M tokens and the n < rows of a
 // weight matrix in the device layout (ifx_common.h).
 //
-// Arithmetic.  One fp16 rounding of either operand moves the logits of the
-// synthetic models by up to 4% (their activations amplify rounding ~100x, and
-// reach 4e7, past the fp16 range), so both operands are carried as fp16 pairs:
-//   * W: every element is dequantized exactly as the reference does it (the
-//     same f32 operations in the same order), then split w = w_hi + w_lo with
-//     w_hi = fp16(w), w_lo = fp16(w - w_hi).  |w| is bounded by the block
-//     scales (checked at model upload) and stays inside the fp16 range.
-//   * A: row t is scaled by s_t = 2^(14 - e_t), e_t the exponent of the row's
-//     largest magnitude (given as float bits in rowmax[t]), so that
-//     |A s_t| < 2^15, then split the same way.
-//   * Each 16x16x32 step runs three MFMAs, A_hi W_hi + A_hi W_lo + A_lo W_hi,
-//     accumulating in f32; the A_lo W_lo term is below 2^-22 relative.  The
-//     result is multiplied back by 2^(e_t - 14) (exact).
-// Per product that is about 2^-21 relative, the level of the f32 reference's
-// own roundings (float64 model of this scheme: 1e-5 relative L2 on the tiny
-// model's logits, 5e-8 on the 8B shape).
+// Arithmetic (scale-factored).  Each quantized element is w = s * p - c with
+// an integer p and scales shared by a block (src/gguf/dequant.rs):
+//   Q4_K: p = sc q in 0..945, s = d per 256-element super-block, c = dmin mn
+//         per 32-element group (dequant.rs:133-161);
+//   Q6_K: p = sc (q - 32) with the u8 scale, |p| <= 8160, s = d (dequant.rs:165-199);
+//   Q8_0: p = q, s = delta per 32-block (dequant.rs:93-111);
+//   Q4_0: p = q - 8, s = delta (dequant.rs:62-84).
+// p is an exact fp16 integer (Q6_K: an exact pair p = p_hi + p_lo, |p_lo| <= 4),
+// so the MFMAs run on the integers and the block scale is applied in f32 once
+// per block: C = sum_b s[n][b] (sum_{k in b} p[n][k] A[t][k]) - sum_g c[n][g] S[t][g],
+// S[t][g] the group sums of A.  The Q4_K min term is itself a K = 16 MFMA per
+// super-block (8 groups x the hi/lo parts of S against dmin mn, an exact fp16 pair).
+// The activations are carried as fp16 pairs: k_prep_rows scales row t by
+// 2^(14 - e_t) (e_t the exponent of its largest magnitude, |A s| < 2^15) and
+// splits a = a_hi + a_lo; each 16x16x32 step runs a_hi p + a_lo p (Q6_K adds
+// a_hi p_lo), accumulating in f32.  Only the a_lo p_lo term (below 2^-22
+// relative) is dropped: per product about 2^-21 relative, the level of the f32
+// reference's own roundings.  One fp16 rounding of either operand would move
+// the synthetic models' logits by up to 4%: their activations amplify
+// rounding ~100x and reach 4e7, past the fp16 range.
+//
+// Element order: within every 8-element chunk of K both operands hold
+// elements 0 4 1 5 2 6 3 7, the order in which a 32-bit word of nibbles
+// unpacks into fp16 pairs ((w >> 4j) & 0x000F000F holds elements j, j + 4);
+// k_prep_rows writes A in that order.
 //
 // Tiling: a workgroup of 4 waves computes a 128 (tokens) x 128 (weight rows)
-// tile; wave (wm, wn) owns 64 x 64 as 4 x 4 MFMA tiles.  Per 32-wide K step the
-// workgroup converts one 128 x 32 slab of A and dequantizes one 128 x 32 slab
-// of W into LDS (hi and lo planes, double-buffered: one barrier per step; 64 KB,
-// two workgroups per CU), and
-// the raw loads of the next step are in flight while the MFMAs run.  MFMA
-// v_mfma_f32_16x16x32_f16: lane i + 16g holds A[i][8g..8g+7] and
-// B[8g..8g+7][i]; C[4g + r][i] arrives in lane i + 16g, register r.
-// Compiled with -ffp-contract=off: the dequant keeps the reference's roundings.
+// tile; wave (wm, wn) owns 64 x 64 as 4 x 4 MFMA tiles.  Per 32-wide K step
+// the workgroup copies one 128 x 32 slab of A (hi and lo planes) and unpacks
+// one 128 x 32 slab of p into LDS (double-buffered: one barrier per step),
+// and the raw loads of the next step are in flight while the MFMAs run.
+// Block scales and the Q4_K min operands go to a per-block side area.
+// MFMA v_mfma_f32_16x16x32_f16: lane i + 16g holds A[i][8g..8g+7] and
+// B[8g..8g+7][i]; C[4g + r][i] arrives in lane i + 16g, register r
+// (16x16x16: A[i][4g..4g+3], B[4g..4g+3][i], the same C).
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -39,159 +49,218 @@ namespace ifx {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
 constexpr int kLdk = 32;  // halves per LDS row (64 B), 16-byte chunks XOR-swizzled by swz()
 constexpr int kThreads = 256;
 constexpr int kPlane = kBM * kLdk;  // halves in one 128 x 32 plane
+constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024 in both halves: 0x6400 | u is 1024 + u (u < 1024)
 
 struct GemmArgs {
-  const float* a;         // [m x lda] f32
-  const uint32_t* rowmax; // [m] float bits of max |A[t][:]|
-  uint32_t m, lda, k;     // k = cols of the weight matrix, a multiple of 32
-  GemmW w0, w1;           // w1: the second matrix of a paired launch (gate/up)
-  uint32_t n;             // output columns: rows of w0 (paired: of each)
-  uint32_t ksplit;        // K ranges over grid.z; > 1: partial tiles to `part`
-  uint32_t kps;           // 32-wide K steps per range
-  float* part;            // [ksplit][m][ncols], ncols = n (paired: 2n, up after gate)
+  const uint16_t* ahi;   // [m][k] fp16, chunk order 0 4 1 5 2 6 3 7
+  const uint16_t* alo;
+  const uint16_t* gsum;  // [m][k / 256][16]: S_hi[8], S_lo[8] of each super-block (Q4_K)
+  const int* rexp;       // [m] row scale exponents
+  uint32_t m, k;         // k = cols of the weight matrix, a multiple of 32
+  GemmW w0, w1;          // w1: the second matrix of a paired launch (gate/up)
+  uint32_t n;            // output columns: rows of w0 (paired: of each)
+  uint32_t ksplit;       // K ranges over grid.z; > 1: partial tiles to `part`
+  uint32_t kps;          // 32-wide K steps per range (a multiple of the block's steps)
+  float* part;           // [ksplit][m][ncols], ncols = n (paired: 2n, up after gate)
 };
 
-// ---------------------------------------------------------------------------
-// Weight slab loaders: thread (row n of the tile, half h) holds the raw bytes
-// of elements [k0 + 16h, k0 + 16h + 16) of weight row `row`, then writes their
-// dequantized fp16 pairs to LDS.  Element arithmetic as in dev_quant.h.
-// ---------------------------------------------------------------------------
-template <int T>
-struct WRaw;
-
-template <>
-struct WRaw<T_Q4K> {  // tiled Q4_K (src/gguf/dequant.rs:133-161)
-  uint4 hdr;
-  uint2 qs;
-  uint32_t sb;
-  __device__ void load(const GemmW& w, uint32_t row, uint32_t k0, int h, bool ok) {
-    sb = (k0 & 255u) >> 5;
-    if (!ok) { hdr = make_uint4(0, 0, 0, 0); qs = make_uint2(0, 0); return; }
-    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (k0 >> 8)) * kUnitQ4K;
-    const uint32_t nt = row & 15u;
-    hdr = *(const uint4*)(u + 16u * nt);
-    qs = *(const uint2*)(u + 256u + (sb >> 2) * 1024u + (nt + 16u * (sb & 3u)) * 16u + 8u * (uint32_t)h);
-  }
-  __device__ void dequant(float* y) const {
-    // get_scale_min_k4 on the 12 scale bytes held in hdr.y/z/w (bytes 0-3, 4-7, 8-11)
-    const uint32_t g = sb & 3u, y8 = hdr.y >> (8 * g), z8 = hdr.z >> (8 * g), w8 = hdr.w >> (8 * g);
-    const uint32_t sc = sb < 4 ? (y8 & 63u) : ((w8 & 15u) | (((y8 >> 6) & 3u) << 4));
-    const uint32_t mn = sb < 4 ? (z8 & 63u) : (((w8 >> 4) & 15u) | (((z8 >> 6) & 3u) << 4));
-    const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
-    const float dall = d * (float)sc, dm = dmin * (float)mn;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t b = ((i < 4 ? qs.x : qs.y) >> (8 * (i & 3))) & 255u;
-      y[2 * i] = dall * (float)(b & 15u) - dm;
-      y[2 * i + 1] = dall * (float)(b >> 4) - dm;
-    }
-  }
-};
-
-template <>
-struct WRaw<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
-  uint2 ql;
-  uint32_t hw, sc, d;
-  __device__ void load(const GemmW& w, uint32_t row, uint32_t k0, int h, bool ok) {
-    if (!ok) { ql = make_uint2(0, 0); hw = sc = d = 0; return; }
-    const uint32_t sb = (k0 & 255u) >> 5, nt = row & 15u;
-    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (k0 >> 8)) * kUnitQ6K;
-    const uint32_t lane = nt + 16u * (sb & 3u), c = 2u * (sb >> 2) + (uint32_t)h;
-    ql = *(const uint2*)(u + (sb >> 2) * 1024u + lane * 16u + 8u * (uint32_t)h);
-    hw = *(const uint32_t*)(u + 2048u + lane * 16u + 4u * c);
-    sc = u[3072u + 4u * lane + c];
-    d = *(const uint16_t*)(u + 3328u + 2u * nt);
-  }
-  __device__ void dequant(float* y) const {
-    const float ds = h2f(d) * (float)sc;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const uint32_t b = ((k < 8 ? ql.x : ql.y) >> (8 * ((k >> 1) & 3))) & 255u;
-      const uint32_t lo = (k & 1) ? (b >> 4) : (b & 15u);
-      const uint32_t hi = (hw >> (8 * ((k & 7) >> 1) + 2 * (k & 1) + 4 * (k >> 3))) & 3u;
-      y[k] = ds * (float)((int)(lo | (hi << 4)) - 32);
-    }
-  }
-};
-
-template <>
-struct WRaw<T_Q8_0> {  // Q8_0: qs[nb][32] | d[nb] (src/gguf/dequant.rs:101-109)
-  uint4 q;
-  uint32_t d;
-  __device__ void load(const GemmW& w, uint32_t row, uint32_t k0, int h, bool ok) {
-    if (!ok) { q = make_uint4(0, 0, 0, 0); d = 0; return; }
-    const uint64_t b = (uint64_t)row * (w.cols >> 5) + (k0 >> 5);
-    q = *(const uint4*)(w.body + b * 32u + 16u * (uint32_t)h);
-    d = ((const uint16_t*)w.scal)[b];
-  }
-  __device__ void dequant(float* y) const {
-    const float delta = h2f(d);
-    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 16; k++) y[k] = (float)(int8_t)((v[k >> 2] >> (8 * (k & 3))) & 255u) * delta;
-  }
-};
-
-template <>
-struct WRaw<T_Q4_0> {  // Q4_0: qs[nb][16] | d[nb]; low nibbles -> j, high -> j + 16 (dequant.rs:70-82)
-  uint4 q;
-  uint32_t d;
-  int half;
-  __device__ void load(const GemmW& w, uint32_t row, uint32_t k0, int h, bool ok) {
-    half = h;
-    if (!ok) { q = make_uint4(0, 0, 0, 0); d = 0; return; }
-    const uint64_t b = (uint64_t)row * (w.cols >> 5) + (k0 >> 5);
-    q = *(const uint4*)(w.body + b * 16u);
-    d = ((const uint16_t*)w.scal)[b];
-  }
-  __device__ void dequant(float* y) const {
-    const float delta = h2f(d);
-    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const uint32_t b = (v[k >> 2] >> (8 * (k & 3))) & 255u;
-      y[k] = (float)((int)(half ? (b >> 4) : (b & 15u)) - 8) * delta;
-    }
-  }
-};
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 splat(float v) { return h2{(_Float16)v, (_Float16)v}; }
 
 // Physical 16-byte chunk of logical chunk c (0..3) in LDS row r: rows 4a + b
 // keep chunk c at c ^ a, so the 16 rows of a fragment read land on 16
 // distinct 4-bank groups (64-byte rows: rows b, b + 4, ... share banks).
 __device__ __forceinline__ int swz(int r, int c) { return r * kLdk + 8 * (c ^ ((r >> 2) & 3)); }
 
-// y[0..16) -> hi/lo halves of logical chunks 2h, 2h + 1 of LDS row r
-__device__ __forceinline__ void split_store(const float* y, _Float16* hi_plane, _Float16* lo_plane, int r, int h) {
-  _Float16* hi0 = hi_plane + swz(r, 2 * h);
-  _Float16* hi1 = hi_plane + swz(r, 2 * h + 1);
-  _Float16* lo0 = lo_plane + swz(r, 2 * h);
-  _Float16* lo1 = lo_plane + swz(r, 2 * h + 1);
-  h8 a0, a1, b0, b1;
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const _Float16 x0 = (_Float16)y[k], x1 = (_Float16)y[k + 8];
-    a0[k] = x0;
-    a1[k] = x1;
-    b0[k] = (_Float16)(y[k] - (float)x0);
-    b1[k] = (_Float16)(y[k + 8] - (float)x1);
+// Per-block side data: block scale of each weight row (f32) and, for Q4_K,
+// the min-term operands: bm[n] = {hi[8], lo[8]} of -32 dmin mn per group,
+// sa[t] = {hi[8], lo[8]} of S / 32 per group.
+struct SideD {
+  float d[kBN];
+};
+struct SideMin {
+  float d[kBN];
+  _Float16 bm[kBN][16];
+  _Float16 sa[kBM][16];
+};
+
+// ---------------------------------------------------------------------------
+// Weight staging: thread (row n of the tile, half h) loads the raw bytes of
+// elements [16h, 16h + 16) of the step's 32 for weight row `row`, then writes
+// their integers p as chunks 2h, 2h + 1 of LDS row n.
+// ---------------------------------------------------------------------------
+template <int T>
+struct WQ;
+
+template <>
+struct WQ<T_Q4K> {  // tiled Q4_K (src/gguf/dequant.rs:133-161)
+  static constexpr int kSb = 8;  // steps per super-block
+  static constexpr bool kMins = true, kPLo = false;
+  typedef SideMin Side;
+  uint4 hdr;  // d, dmin, 12 scale bytes: kept through the super-block
+  uint2 qs;
+  // g: the step's group within its super-block (a constant of the unrolled loop)
+  __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t g, int h, bool sb0) {
+    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (ks >> 3)) * kUnitQ4K;
+    const uint32_t nt = row & 15u;
+    if (sb0) hdr = *(const uint4*)(u + 16u * nt);
+    qs = *(const uint2*)(u + 256u + (g >> 2) * 1024u + (nt + 16u * (g & 3u)) * 16u + 8u * (uint32_t)h);
   }
-  *(h8*)hi0 = a0;
-  *(h8*)hi1 = a1;
-  *(h8*)lo0 = b0;
-  *(h8*)lo1 = b1;
+  // get_scale_min_k4 (dequant.rs:141-149) on the scale bytes in hdr.y/z/w
+  __device__ void scale_min(uint32_t grp, uint32_t& sc, uint32_t& mn) const {
+    const uint32_t s8 = 8 * (grp & 3u), y8 = hdr.y >> s8, z8 = hdr.z >> s8, w8 = hdr.w >> s8;
+    sc = grp < 4 ? (y8 & 63u) : ((w8 & 15u) | (((y8 >> 6) & 3u) << 4));
+    mn = grp < 4 ? (z8 & 63u) : (((w8 >> 4) & 15u) | (((z8 >> 6) & 3u) << 4));
+  }
+  __device__ void stage(_Float16* bp, _Float16*, Side& sd, uint32_t g, int wr, int h, bool sb0) const {
+    uint32_t sc, mn;
+    scale_min(g, sc, mn);
+    // (1024 + q) sc - 1024 sc = q sc, one rounding of an exact integer <= 945
+    const h2 s2 = splat((float)sc), o2 = splat(-1024.f * (float)sc);
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[j] = as_u32(__builtin_elementwise_fma(as_h2(((qs.x >> (4 * j)) & 0x000F000Fu) | kMagic), s2, o2));
+      v[4 + j] = as_u32(__builtin_elementwise_fma(as_h2(((qs.y >> (4 * j)) & 0x000F000Fu) | kMagic), s2, o2));
+    }
+    *(uint4*)(bp + swz(wr, 2 * h)) = make_uint4(v[0], v[1], v[2], v[3]);
+    *(uint4*)(bp + swz(wr, 2 * h + 1)) = make_uint4(v[4], v[5], v[6], v[7]);
+    if (sb0) {
+      const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+      sd.d[wr] = d;  // both halves store the same value
+      h4 bh, bl;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        uint32_t s_, m_;
+        scale_min(4u * (uint32_t)h + (uint32_t)i, s_, m_);
+        const float c = -(dmin * (float)m_) * 32.f;  // exact in f32; |c| < 2^16 (checked at upload)
+        bh[i] = (_Float16)c;
+        bl[i] = (_Float16)(c - (float)bh[i]);
+      }
+      *(h4*)&sd.bm[wr][4 * h] = bh;
+      *(h4*)&sd.bm[wr][8 + 4 * h] = bl;
+    }
+  }
+};
+
+template <>
+struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
+  static constexpr int kSb = 8;
+  static constexpr bool kMins = false, kPLo = true;
+  typedef SideD Side;
+  uint2 ql;
+  uint32_t hw, sc, d;
+  __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t g, int h, bool sb0) {
+    const uint32_t nt = row & 15u;
+    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (ks >> 3)) * kUnitQ6K;
+    const uint32_t lane = nt + 16u * (g & 3u), c = 2u * (g >> 2) + (uint32_t)h;
+    ql = *(const uint2*)(u + (g >> 2) * 1024u + lane * 16u + 8u * (uint32_t)h);
+    hw = *(const uint32_t*)(u + 2048u + lane * 16u + 4u * c);
+    sc = u[3072u + 4u * lane + c];
+    if (sb0) d = *(const uint16_t*)(u + 3328u + 2u * nt);
+  }
+  // q of elements (j, j + 4) of chunk cc: low nibbles from ql, high parts at
+  // bits 8 (j / 2) + 2 (j & 1) + 4 cc of hw (16 bits apart), as 1024 + q
+  template <int CC, int J>
+  __device__ __forceinline__ uint32_t q_pair() const {
+    constexpr int s = 8 * (J >> 1) + 2 * (J & 1) + 4 * CC;
+    const uint32_t lo = ((CC ? ql.y : ql.x) >> (4 * J)) & 0x000F000Fu;
+    const uint32_t hi = (s >= 4 ? (hw >> (s - 4)) : (hw << (4 - s))) & 0x00300030u;
+    return lo | hi | kMagic;
+  }
+  __device__ void stage(_Float16* bp, _Float16* bpl, Side& sd, uint32_t, int wr, int h, bool sb0) const {
+    const h2 s2 = splat((float)sc), m2 = splat(-1056.f);
+    uint32_t vh[8], vl[8];
+    auto pair = [&](uint32_t qv, int o) {
+      const h2 t = as_h2(qv) + m2;                              // q - 32, exact
+      const h2 ph = t * s2;                                     // p_hi: p rounded once
+      const h2 pl = __builtin_elementwise_fma(t, s2, -ph);      // p - p_hi, exact (|.| <= 4)
+      vh[o] = as_u32(ph);
+      vl[o] = as_u32(pl);
+    };
+    pair(q_pair<0, 0>(), 0);
+    pair(q_pair<0, 1>(), 1);
+    pair(q_pair<0, 2>(), 2);
+    pair(q_pair<0, 3>(), 3);
+    pair(q_pair<1, 0>(), 4);
+    pair(q_pair<1, 1>(), 5);
+    pair(q_pair<1, 2>(), 6);
+    pair(q_pair<1, 3>(), 7);
+    *(uint4*)(bp + swz(wr, 2 * h)) = make_uint4(vh[0], vh[1], vh[2], vh[3]);
+    *(uint4*)(bp + swz(wr, 2 * h + 1)) = make_uint4(vh[4], vh[5], vh[6], vh[7]);
+    *(uint4*)(bpl + swz(wr, 2 * h)) = make_uint4(vl[0], vl[1], vl[2], vl[3]);
+    *(uint4*)(bpl + swz(wr, 2 * h + 1)) = make_uint4(vl[4], vl[5], vl[6], vl[7]);
+    if (sb0) sd.d[wr] = h2f(d);
+  }
+};
+
+// bytes j of x and y as the fp16-pair word (x_j, 0, y_j, 0)
+__device__ __forceinline__ uint32_t byte_pair(uint32_t x, uint32_t y, int j) {
+  return __builtin_amdgcn_perm(y, x, (uint32_t)j | (0x0cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0cu << 24));
 }
 
-// row t's scale exponent: |A[t][:] * 2^(14 - e)| < 2^15
-__device__ __forceinline__ int row_exp(uint32_t bits) {
-  const int e = (int)((bits >> 23) & 255u) - 127;
-  return e < -100 ? -100 : e;
-}
+template <>
+struct WQ<T_Q8_0> {  // Q8_0: qs[nb][32] | d[nb] (src/gguf/dequant.rs:101-109)
+  static constexpr int kSb = 1;
+  static constexpr bool kMins = false, kPLo = false;
+  typedef SideD Side;
+  uint4 q;
+  uint32_t d;
+  __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t, int h, bool) {
+    const uint64_t b = (uint64_t)row * (w.cols >> 5) + ks;
+    q = *(const uint4*)(w.body + b * 32u + 16u * (uint32_t)h);
+    d = ((const uint16_t*)w.scal)[b];
+  }
+  __device__ void stage(_Float16* bp, _Float16*, Side& sd, uint32_t, int wr, int h, bool) const {
+    // int8 -> 1024 + (q + 128) by flipping the sign bit under the fp16 1024 pattern
+    const h2 m2 = splat(-1152.f);
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[j] = as_u32(as_h2(byte_pair(q.x, q.y, j) ^ 0x64806480u) + m2);
+      v[4 + j] = as_u32(as_h2(byte_pair(q.z, q.w, j) ^ 0x64806480u) + m2);
+    }
+    *(uint4*)(bp + swz(wr, 2 * h)) = make_uint4(v[0], v[1], v[2], v[3]);
+    *(uint4*)(bp + swz(wr, 2 * h + 1)) = make_uint4(v[4], v[5], v[6], v[7]);
+    sd.d[wr] = h2f(d);
+  }
+};
+
+template <>
+struct WQ<T_Q4_0> {  // Q4_0: qs[nb][16] | d[nb]; low nibbles -> j, high -> j + 16 (dequant.rs:70-82)
+  static constexpr int kSb = 1;
+  static constexpr bool kMins = false, kPLo = false;
+  typedef SideD Side;
+  uint4 q;
+  uint32_t d;
+  __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t, int, bool) {
+    const uint64_t b = (uint64_t)row * (w.cols >> 5) + ks;
+    q = *(const uint4*)(w.body + b * 16u);
+    d = ((const uint16_t*)w.scal)[b];
+  }
+  __device__ void stage(_Float16* bp, _Float16*, Side& sd, uint32_t, int wr, int h, bool) const {
+    const h2 m2 = splat(-1032.f);  // 1024 + q - 1032 = q - 8
+    const int sh = 4 * h;          // half h: the high nibbles (elements 16..31)
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[j] = as_u32(as_h2(((byte_pair(q.x, q.y, j) >> sh) & 0x000F000Fu) | kMagic) + m2);
+      v[4 + j] = as_u32(as_h2(((byte_pair(q.z, q.w, j) >> sh) & 0x000F000Fu) | kMagic) + m2);
+    }
+    *(uint4*)(bp + swz(wr, 2 * h)) = make_uint4(v[0], v[1], v[2], v[3]);
+    *(uint4*)(bp + swz(wr, 2 * h + 1)) = make_uint4(v[4], v[5], v[6], v[7]);
+    sd.d[wr] = h2f(d);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Epilogues: v(t, n) for token t < m and output column n < a.n.
@@ -269,17 +338,14 @@ struct EpTraits<EpRope> {
   static constexpr bool kPaired = false, kNeighbor = true;
 };
 
-__device__ __forceinline__ f4 mfma3(h8 ah, h8 al, h8 bh, h8 bl, f4 c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
-}
-
 template <int T, class Ep>
 __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
+  using Q = WQ<T>;
   constexpr bool kPaired = EpTraits<Ep>::kPaired;
-  // [buffer][A hi, A lo, W hi, W lo][128][kLdk]
-  __shared__ __attribute__((aligned(16))) _Float16 lds[2][4][kPlane];
+  constexpr int kNp = Q::kPLo ? 4 : 3;  // planes: A hi, A lo, p (hi), [p lo]
+  constexpr bool kOverlap = !Q::kPLo;   // unpack step ks + 1 among the MFMAs of step ks
+  __shared__ __attribute__((aligned(16))) _Float16 lds[2][kNp][kPlane];
+  __shared__ __attribute__((aligned(16))) typename Q::Side side[2];
   __shared__ int rexp[kBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -287,45 +353,53 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
   // output columns of the tile (paired: gate rows n0.. in W rows 0..63, up in 64..127)
   const uint32_t n0 = blockIdx.x * (kPaired ? kBN / 2 : kBN);
 
-  // staging roles: A row ar, W row wr, 16-element half h
-  const int h = tid & 1, ar = tid >> 1, wr = tid >> 1;
-  const uint32_t at = m0 + (uint32_t)ar;
-  const bool a_ok = at < a.m;
+  // staging roles: A row ar (chunks ac, ac + 1 of both planes), W row wr half h.
+  // Rows past the operands read a clamped row: their outputs are never stored.
+  const int h = tid & 1, ar = tid >> 1, wr = tid >> 1, ac = 2 * h;
+  const uint32_t at = min(m0 + (uint32_t)ar, a.m - 1);
   const GemmW& ws = (kPaired && wr >= 64) ? a.w1 : a.w0;
-  const uint32_t wrow = kPaired ? n0 + (uint32_t)(wr & 63) : n0 + (uint32_t)wr;
   const uint32_t w_rows_avail = (T == T_Q4K || T == T_Q6K) ? (ws.rows + 15u) & ~15u : ws.rows;
-  const bool w_ok = wrow < w_rows_avail && (!kPaired || n0 + (uint32_t)(wr & 63) < a.n);
-  if (tid < kBM) rexp[tid] = m0 + (uint32_t)tid < a.m ? row_exp(a.rowmax[m0 + tid]) : 0;
-  __syncthreads();
-  const float ascale = ldexpf(1.0f, 14 - rexp[ar]);
+  const uint32_t wrow = min(kPaired ? n0 + (uint32_t)(wr & 63) : n0 + (uint32_t)wr, w_rows_avail - 1);
+  if (tid < kBM) rexp[tid] = m0 + (uint32_t)tid < a.m ? a.rexp[m0 + tid] : 0;
 
-  const float* arow = a.a + (uint64_t)(a_ok ? at : 0u) * a.lda + 16 * h;
-  float4 ra[4];
-  WRaw<T> rw;
-  auto load_step = [&](uint32_t k0) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) ra[i] = a_ok ? *(const float4*)(arow + k0 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    rw.load(ws, wrow, k0, h, w_ok);
+  const uint64_t arow = (uint64_t)at * a.k + 8u * (uint32_t)ac;
+  const uint16_t* ahi = a.ahi + arow;
+  const uint16_t* alo = a.alo + arow;
+  const uint16_t* gs = Q::kMins ? a.gsum + (uint64_t)at * (a.k >> 8) * 16u + 8u * (uint32_t)h : nullptr;
+  uint4 ra0, ra1, ra2, ra3;  // hi chunks ac, ac + 1; lo chunks ac, ac + 1
+  uint4 rs = make_uint4(0, 0, 0, 0);  // S_hi or S_lo of the row's super-block (Q4_K)
+  Q rw;
+  // raw loads of step ks, group g of its block (sb0: g == 0)
+  auto load_step = [&](uint32_t ks, uint32_t g, bool sb0) __attribute__((always_inline)) {
+    const uint32_t k0 = ks * kBK;
+    ra0 = *(const uint4*)(ahi + k0);
+    ra1 = *(const uint4*)(ahi + k0 + 8);
+    ra2 = *(const uint4*)(alo + k0);
+    ra3 = *(const uint4*)(alo + k0 + 8);
+    if (Q::kMins && sb0) rs = *(const uint4*)(gs + (ks >> 3) * 16u);
+    rw.load(ws, wrow, ks, g, h, sb0);
   };
-  auto stage = [&](int buf) {
-    float y[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      y[4 * i] = ra[i].x * ascale;
-      y[4 * i + 1] = ra[i].y * ascale;
-      y[4 * i + 2] = ra[i].z * ascale;
-      y[4 * i + 3] = ra[i].w * ascale;
+  auto stage = [&](int buf, int sbi, uint32_t g, bool sb0) __attribute__((always_inline)) {
+    _Float16* ph = lds[buf][0];
+    _Float16* pl = lds[buf][1];
+    *(uint4*)(ph + swz(ar, ac)) = ra0;
+    *(uint4*)(ph + swz(ar, ac + 1)) = ra1;
+    *(uint4*)(pl + swz(ar, ac)) = ra2;
+    *(uint4*)(pl + swz(ar, ac + 1)) = ra3;
+    if constexpr (Q::kMins) {
+      if (sb0) *(uint4*)&side[sbi].sa[ar][8 * h] = rs;
     }
-    split_store(y, lds[buf][0], lds[buf][1], ar, h);
-    rw.dequant(y);
-    split_store(y, lds[buf][2], lds[buf][3], wr, h);
+    rw.stage(lds[buf][2], Q::kPLo ? lds[buf][kNp - 1] : nullptr, side[sbi], g, wr, h, sb0);
   };
 
-  f4 acc[4][4];
+  f4 acc[4][4], cs[4][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; j++) {
+      acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+      cs[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    }
 
   const int fi = lane & 15, fg = lane >> 4;
   // W rows of this wave's four 16-column fragments
@@ -334,19 +408,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
   for (int j = 0; j < 4; j++)
     wcol[j] = kPaired ? (j < 2 ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
 
-  // this workgroup's K steps [ks0, ks1)
-  const uint32_t ks0 = blockIdx.z * a.kps, ks1 = min(a.k / kBK, ks0 + a.kps);
-  load_step(ks0 * kBK);
-  for (uint32_t ks = ks0; ks < ks1; ks++) {
-    const int buf = ks & 1;
-    stage(buf);
-    __syncthreads();
-    if (ks + 1 < ks1) load_step((ks + 1) * kBK);
+  // the block's integer dot products: cs = (first step of a block ? 0 : cs) + a p
+  auto mma = [&](int buf, auto first) __attribute__((always_inline)) {
+    constexpr bool kFirst = decltype(first)::value;
     h8 bh[4], bl[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       bh[j] = *(const h8*)&lds[buf][2][swz(wcol[j] + fi, fg)];
-      bl[j] = *(const h8*)&lds[buf][3][swz(wcol[j] + fi, fg)];
+      if (Q::kPLo) bl[j] = *(const h8*)&lds[buf][kNp - 1][swz(wcol[j] + fi, fg)];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -354,7 +423,89 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
       const h8 ah = *(const h8*)&lds[buf][0][swz(r, fg)];
       const h8 al = *(const h8*)&lds[buf][1][swz(r, fg)];
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[i][j] = mfma3(ah, al, bh[j], bl[j], acc[i][j]);
+      for (int j = 0; j < 4; j++) {
+        f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], kFirst ? f4{0.f, 0.f, 0.f, 0.f} : cs[i][j], 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], c, 0, 0, 0);
+        if (Q::kPLo) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j], c, 0, 0, 0);
+        cs[i][j] = c;
+      }
+    }
+  };
+  // end of a block: acc += s cs (and the Q4_K min term)
+  auto flush = [&](int sbi) __attribute__((always_inline)) {
+    const typename Q::Side& sd = side[sbi];
+    float dj[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) dj[j] = sd.d[wcol[j] + fi];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(dj[j], cs[i][j][r], acc[i][j][r]);
+    if constexpr (Q::kMins) {
+      // K = 16: lanes of group g take S_hi (g < 2) or S_lo (g >= 2) of
+      // groups 4 (g & 1) .. + 3 against the hi parts; the second MFMA adds
+      // S_hi against the lo parts
+      const h4 z = {0, 0, 0, 0};
+      h4 a1[4], a2[4], b1[4], b2[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        a1[i] = *(const h4*)&sd.sa[wm * 64 + 16 * i + fi][4 * fg];
+        a2[i] = fg < 2 ? a1[i] : z;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        b1[j] = *(const h4*)&sd.bm[wcol[j] + fi][4 * (fg & 1)];
+        const h4 lo = *(const h4*)&sd.bm[wcol[j] + fi][8 + 4 * (fg & 1)];
+        b2[j] = fg < 2 ? lo : z;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2[i], b2[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  };
+
+  // this workgroup's K steps [ks0, ks1): whole blocks.  Step ks runs the
+  // MFMAs of buffer ks & 1 while unpacking step ks + 1 into the other buffer
+  // (its last readers finished before the previous barrier), then issues the
+  // raw loads of step ks + 2: one barrier per step, and a whole block of
+  // steps unrolled so that the MFMAs and the unpacking interleave.
+  const uint32_t ks0 = blockIdx.z * a.kps, ks1 = min(a.k / kBK, ks0 + a.kps);
+  const uint32_t klast = ks1 - 1;  // loads past the range re-read its last step (unused)
+  __syncthreads();  // rexp
+  load_step(ks0, 0, true);
+  stage(ks0 & 1, (ks0 / Q::kSb) & 1, 0, true);
+  load_step(min(ks0 + 1, klast), 1 % Q::kSb, Q::kSb == 1);
+  __syncthreads();
+  auto step = [&](uint32_t kb, int i) __attribute__((always_inline)) {
+    const int sbi = (kb / Q::kSb) & 1;
+    const uint32_t ks = kb + (uint32_t)i;
+    const int buf = Q::kSb % 2 == 0 ? (i & 1) ^ (int)(kb & 1) : (int)(ks & 1);
+    if (i == 0) mma(buf, std::true_type{});
+    else mma(buf, std::false_type{});
+    // Q6_K's second weight plane leaves no registers to overlap the two
+    if (!kOverlap) __builtin_amdgcn_sched_barrier(0);
+    // step ks + 1 starts a block when i is the block's last step
+    stage(buf ^ 1, i == Q::kSb - 1 ? sbi ^ 1 : sbi, (uint32_t)((i + 1) % Q::kSb), i == Q::kSb - 1);
+    if (i == Q::kSb - 1) flush(sbi);
+    // the next raw loads reuse the registers just unpacked: no second set
+    __builtin_amdgcn_sched_barrier(0);
+    // group and block start by position (a clamped load past the range is unused)
+    load_step(min(ks + 2, klast), (uint32_t)((i + 2) % Q::kSb), (i + 2) % Q::kSb == 0);
+    __syncthreads();
+  };
+  for (uint32_t kb = ks0; kb < ks1; kb += Q::kSb) {
+    if constexpr (kOverlap) {
+#pragma unroll
+      for (int i = 0; i < Q::kSb; i++) step(kb, i);
+    } else {
+#pragma unroll 1
+      for (int i = 0; i < Q::kSb; i++) step(kb, i);
     }
   }
 
@@ -436,14 +587,18 @@ hipError_t go(const GemmArgs& a, const Ep& ep, hipStream_t st) {
 template <class Ep>
 hipError_t dispatch(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   if (a.m == 0 || a.n == 0) return hipSuccess;
-  if (a.k == 0 || a.k % kBK || a.lda < a.k || a.lda % 4) return hipErrorInvalidValue;
+  if (a.k == 0 || a.k % kBK || !a.ahi || !a.alo || !a.rexp) return hipErrorInvalidValue;
   if (EpTraits<Ep>::kPaired && (a.w1.type != a.w0.type || a.w1.rows != a.w0.rows || a.w1.cols != a.w0.cols))
     return hipErrorInvalidValue;
   if (a.w0.cols != a.k) return hipErrorInvalidValue;
   if (a.ksplit == 0 || a.kps == 0) return hipErrorInvalidValue;
   switch (a.w0.type) {
-    case T_Q4K: return go<T_Q4K, Ep>(a, ep, st);
-    case T_Q6K: return go<T_Q6K, Ep>(a, ep, st);
+    case T_Q4K:
+      if (a.k % 256 || !a.gsum || a.kps % WQ<T_Q4K>::kSb) return hipErrorInvalidValue;
+      return go<T_Q4K, Ep>(a, ep, st);
+    case T_Q6K:
+      if (a.k % 256 || a.kps % WQ<T_Q6K>::kSb) return hipErrorInvalidValue;
+      return go<T_Q6K, Ep>(a, ep, st);
     case T_Q8_0: return go<T_Q8_0, Ep>(a, ep, st);
     case T_Q4_0: return go<T_Q4_0, Ep>(a, ep, st);
     default: return hipErrorInvalidValue;
@@ -456,15 +611,17 @@ constexpr uint32_t kTargetWgs = 512, kMinStepsPerSplit = 8;
 
 GemmArgs args_of(const GemmIn& in, const GemmW& w, bool paired) {
   GemmArgs a{};
-  a.a = in.a;
-  a.rowmax = in.rowmax;
+  a.ahi = in.hi;
+  a.alo = in.lo;
+  a.gsum = in.gsum;
+  a.rexp = in.rexp;
   a.m = in.m;
-  a.lda = in.lda;
   a.k = (uint32_t)w.cols;
   a.w0 = w;
   a.w1 = w;
   a.n = w.rows;
   const uint32_t nk = a.k / kBK, bn = paired ? kBN / 2 : kBN;
+  const uint32_t sb = (w.type == T_Q4K || w.type == T_Q6K) ? 8u : 1u;  // steps per scale block
   const uint64_t tiles = (uint64_t)((a.n + bn - 1) / bn) * ((a.m + kBM - 1) / kBM);
   uint32_t split = 1;
   if (in.part && tiles < kTargetWgs) {
@@ -473,62 +630,107 @@ GemmArgs args_of(const GemmIn& in, const GemmW& w, bool paired) {
     split = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>({split, in.part_bytes / per, 64}));
   }
   a.kps = (nk + split - 1) / split;
+  a.kps = (a.kps + sb - 1) / sb * sb;  // ranges of whole scale blocks
   a.ksplit = (nk + a.kps - 1) / a.kps;
   a.part = a.ksplit > 1 ? in.part : nullptr;
   return a;
 }
 
-// ---- row statistics and RMSNorm for the A operands ----
+// ---- the A operand: fp16 pairs, group sums and row exponents ----
 
-// rowmax[t] = float bits of max_k |x[t][k]| (positive floats order as integers)
-__global__ void k_rowmax(const float* x, uint32_t ld, uint32_t cols, uint32_t* out) {
-  const float* r = x + (uint64_t)blockIdx.x * ld;
+// Row t of x (optionally rms_norm'ed, src/ops.rs:155-168: y = (x * scale) * w,
+// scale = 1 / sqrt(sum(x^2) / n + eps)), scaled by 2^(14 - e) with e the
+// exponent of its largest magnitude, split into fp16 hi + lo in the chunk
+// order 0 4 1 5 2 6 3 7; the 32-element group sums of the scaled row / 32 as
+// fp16 pairs when cols % 256 == 0.  One workgroup per row; thread i takes the
+// 8-element chunks i, i + 256, ... (a group is four consecutive threads).
+__global__ void __launch_bounds__(256) k_prep_rows(const float* x, uint32_t ld, uint32_t cols, const float* nw,
+                                                   float eps, uint16_t* hi, uint16_t* lo, uint16_t* gsum,
+                                                   int* rexp) {
+  const uint32_t t = blockIdx.x, nch = cols / 8;
+  const float4* r4 = (const float4*)(x + (uint64_t)t * ld);
+  const float4* w4 = (const float4*)nw;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float red[4];
+  __shared__ float bcast;
+  auto row8 = [&](uint32_t c, float* v, float scale) {
+    const float4 u0 = r4[2 * c], u1 = r4[2 * c + 1];
+    v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+    v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    if (nw) {
+      const float4 g0 = w4[2 * c], g1 = w4[2 * c + 1];
+      const float w[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = (v[k] * scale) * w[k];
+    }
+  };
+  float scale = 1.f;
+  if (nw) {
+    float ss = 0.f;
+    for (uint32_t c = tid; c < nch; c += 256) {
+      const float4 u0 = r4[2 * c], u1 = r4[2 * c + 1];
+      ss = fmaf(u0.x, u0.x, ss); ss = fmaf(u0.y, u0.y, ss); ss = fmaf(u0.z, u0.z, ss); ss = fmaf(u0.w, u0.w, ss);
+      ss = fmaf(u1.x, u1.x, ss); ss = fmaf(u1.y, u1.y, ss); ss = fmaf(u1.z, u1.z, ss); ss = fmaf(u1.w, u1.w, ss);
+    }
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (tid == 0) bcast = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
+    __syncthreads();
+    scale = bcast;
+  }
   float m = 0.f;
-  for (uint32_t k = threadIdx.x; k < cols; k += blockDim.x) m = fmaxf(m, fabsf(r[k]));
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  __shared__ float red[16];
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (unsigned w = 1; w < blockDim.x / 64; w++) m = fmaxf(m, red[w]);
-    m = fmaxf(m, red[0]);
-    out[blockIdx.x] = __float_as_uint(m);
-  }
-}
-
-// rms_norm (src/ops.rs:155-168) of each row into y, with the row's max |y|:
-// scale = 1 / sqrt(sum(x^2) / n + eps), y = (x * scale) * w.
-__global__ void k_rmsnorm_rows(const float* x, const float* w, uint32_t n, float eps, float* y, uint32_t* rowmax) {
-  const float* r = x + (uint64_t)blockIdx.x * n;
-  float* o = y + (uint64_t)blockIdx.x * n;
-  float ss = 0.f;
-  for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) ss = fmaf(r[k], r[k], ss);
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  __shared__ float red[16];
-  __shared__ float scale_s;
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.f;
-    for (unsigned v = 0; v < blockDim.x / 64; v++) t += red[v];
-    scale_s = 1.0f / sqrtf(t / (float)n + eps);
-  }
-  __syncthreads();
-  const float scale = scale_s;
-  float m = 0.f;
-  for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-    const float v = (r[k] * scale) * w[k];
-    o[k] = v;
-    m = fmaxf(m, fabsf(v));
+  for (uint32_t c = tid; c < nch; c += 256) {
+    float v[8];
+    row8(c, v, scale);
+#pragma unroll
+    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
   }
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  if (lane == 0) red[wave] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (unsigned v = 1; v < blockDim.x / 64; v++) m = fmaxf(m, red[v]);
-    m = fmaxf(m, red[0]);
-    rowmax[blockIdx.x] = __float_as_uint(m);
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = (int)((__float_as_uint(m) >> 23) & 255u) - 127;
+  e = e < -100 ? -100 : e;
+  if (tid == 0) rexp[t] = e;
+  const float s = ldexpf(1.0f, 14 - e);
+  const bool sums = gsum && cols % 256 == 0;
+  uint16_t* ho = hi + (uint64_t)t * cols;
+  uint16_t* lw = lo + (uint64_t)t * cols;
+  for (uint32_t c0 = 0; c0 < nch; c0 += 256) {
+    const uint32_t c = c0 + tid;
+    const bool ok = c < nch;  // nch is a multiple of 4: a group's threads agree
+    float v[8];
+    if (ok) row8(c, v, scale);
+    else
+      for (int k = 0; k < 8; k++) v[k] = 0.f;
+    h8 vh, vl;
+    float s8 = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const float y = v[(p >> 1) + 4 * (p & 1)] * s;
+      vh[p] = (_Float16)y;
+      vl[p] = (_Float16)(y - (float)vh[p]);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) s8 += v[k] * s;
+    if (ok) {
+      *(h8*)(ho + 8u * c) = vh;
+      *(h8*)(lw + 8u * c) = vl;
+    }
+    if (sums) {
+      s8 += __shfl_xor(s8, 1, 64);
+      s8 += __shfl_xor(s8, 2, 64);
+      if (ok && (c & 3u) == 0) {
+        const uint32_t g = c >> 2;
+        const float sg = s8 * 0.03125f;
+        const _Float16 sh = (_Float16)sg, sl = (_Float16)(sg - (float)sh);
+        _Float16* dst = (_Float16*)gsum + ((uint64_t)t * (cols >> 8) + (g >> 3)) * 16u + (g & 7u);
+        dst[0] = sh;
+        dst[8] = sl;
+      }
+    }
   }
 }
 
@@ -564,16 +766,14 @@ hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, flo
   return dispatch(a, EpSwiglu{mid, ld}, st);
 }
 
-hipError_t launch_rowmax(const float* x, uint32_t rows, uint32_t ld, uint32_t cols, uint32_t* out, hipStream_t st) {
+hipError_t launch_prep_rows(const float* x, uint32_t rows, uint32_t ld, uint32_t cols, const float* norm_w,
+                            float eps, const GemmIn& out, hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rowmax, dim3(rows), dim3(256), 0, st, x, ld, cols, out);
-  return hipGetLastError();
-}
-
-hipError_t launch_rmsnorm_rows_to(const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* y,
-                                  uint32_t* rowmax, hipStream_t st) {
-  if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(256), 0, st, x, w, n, eps, y, rowmax);
+  if (cols == 0 || cols % 32 || ld % 4 || ld < cols || !out.hi || !out.lo || !out.rexp || out.k != cols ||
+      rows > out.m)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_prep_rows, dim3(rows), dim3(256), 0, st, x, ld, cols, norm_w, eps, (uint16_t*)out.hi,
+                     (uint16_t*)out.lo, (uint16_t*)out.gsum, (int*)out.rexp);
   return hipGetLastError();
 }
 

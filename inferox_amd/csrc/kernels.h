@@ -85,12 +85,15 @@ struct GemmW {
   uint32_t rows;
   uint64_t cols;
 };
-// The f32 activation operand: m rows of stride lda, and per row the float bits
-// of its largest magnitude (the GEMM scales each row into the fp16 range).
+// The activation operand as k_prep_rows leaves it (launch_prep_rows): m rows
+// of k columns scaled per row into the fp16 range and split into hi + lo fp16
+// planes, the 32-element group sums, and each row's scale exponent.
 struct GemmIn {
-  const float* a;
-  const uint32_t* rowmax;
-  uint32_t m, lda;
+  const uint16_t* hi;    // [m][k] fp16 bits
+  const uint16_t* lo;    // [m][k]
+  const uint16_t* gsum;  // [m][k / 256][16] (needed by Q4_K weights; k % 256 == 0)
+  const int* rexp;       // [m]
+  uint32_t m, k;
   float* part = nullptr;     // optional workspace for split-K partial tiles
   uint64_t part_bytes = 0;
 };
@@ -111,10 +114,10 @@ hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, u
 // mid[t * ld + n] = swiglu(gate row n . A[t], up row n . A[t])
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,
                        hipStream_t st);
-hipError_t launch_rowmax(const float* x, uint32_t rows, uint32_t ld, uint32_t cols, uint32_t* out, hipStream_t st);
-// y = rms_norm(x) row by row (src/ops.rs:155-180), rowmax[t] = bits of max |y[t][:]|
-hipError_t launch_rmsnorm_rows_to(const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* y,
-                                  uint32_t* rowmax, hipStream_t st);
+// rows x cols of x (row stride ld), rms_norm'ed with norm_w when non-null
+// (src/ops.rs:155-180), into the GEMM operand `out` (out.k == cols, rows <= out.m)
+hipError_t launch_prep_rows(const float* x, uint32_t rows, uint32_t ld, uint32_t cols, const float* norm_w,
+                            float eps, const GemmIn& out, hipStream_t st);
 
 // ---- batched prefill attention (kern_attn_prefill.hip) ----
 // Attention of n query rows over the chunk's keys (src/model/forward.rs:

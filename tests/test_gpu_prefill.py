@@ -1,6 +1,8 @@
-"""Batched prefill on the GPU: the dequant-to-LDS fp16-MFMA GEMM (operands as
-fp16 hi/lo pairs, three MFMAs per step) and the batched causal attention,
-against the oracle.
+"""Batched prefill on the GPU: the dequant-to-LDS fp16-MFMA GEMM (the weights'
+integer parts as exact fp16 values with the block scales applied in f32, the
+activations as fp16 hi/lo pairs) and the batched causal attention, against the
+oracle.  The Q6_K cases carry u8 scales up to 255, so they run the split
+weight plane; the Q4_K cases run the min-term MFMA.
 
 Bars: the GEMM within 1e-5 relative L2 of a float64 product of the oracle's
 dequantized weights, and every element within 1e-5 * sum_k |a||w| of it; model
