@@ -191,7 +191,7 @@ bool gemm_layout_ok(const DevLayout& L) {
   if (!(L.abs_bound <= 3.0e38f)) return false;  // a non-finite block scale
   switch (L.type) {
     case T_Q4K: return L.cols % 256 == 0 && L.dmin_max * 2016.f <= 65504.f;  // 63 * 32 * dmin
-    case T_Q6K: return L.cols % 256 == 0;
+    case T_Q6K: return L.cols % 256 == 0 && L.abs_bound <= 32768.f;  // w = (d sc)(q - 32) as fp16 hi + lo
     case T_Q8_0:
     case T_Q4_0: return L.cols % 32 == 0;
     default: return false;

@@ -101,7 +101,8 @@ float block_abs_bound(uint32_t type, const uint8_t* src, uint64_t b0, uint64_t b
 // Largest |dmin| over Q4_K blocks [b0, b1) (NaN if one is NaN).
 float block_dmin_max(const uint8_t* src, uint64_t b0, uint64_t b1);
 // The batched prefill GEMM carries this matrix exactly: finite block scales,
-// whole blocks per row, and (Q4_K) -32 dmin mn inside the fp16 range.
+// whole blocks per row, and (Q4_K) -32 dmin mn or (Q6_K) the weights inside
+// the fp16 range.
 bool gemm_layout_ok(const DevLayout& L);
 
 }  // namespace ifx

@@ -8,19 +8,20 @@
 // an integer p and scales shared by a block (src/gguf/dequant.rs):
 //   Q4_K: p = sc q in 0..945, s = d per 256-element super-block, c = dmin mn
 //         per 32-element group (dequant.rs:133-161);
-//   Q6_K: p = sc (q - 32) with the u8 scale, |p| <= 8160, s = d (dequant.rs:165-199);
+//   Q6_K: p = sc (q - 32) with the u8 scale reaches 8160, past fp16's
+//         integers: the weight (d sc)(q - 32) itself is carried instead, as
+//         an fp16 pair w_hi + w_lo (dequant.rs:165-199);
 //   Q8_0: p = q, s = delta per 32-block (dequant.rs:93-111);
 //   Q4_0: p = q - 8, s = delta (dequant.rs:62-84).
-// p is an exact fp16 integer (Q6_K: an exact pair p = p_hi + p_lo, |p_lo| <= 4),
-// so the MFMAs run on the integers and the block scale is applied in f32 once
-// per block: C = sum_b s[n][b] (sum_{k in b} p[n][k] A[t][k]) - sum_g c[n][g] S[t][g],
+// p is an exact fp16 integer, so the MFMAs run on the integers and the block
+// scale is applied in f32 once per block: C = sum_b s[n][b] (sum_{k in b} p[n][k] A[t][k]) - sum_g c[n][g] S[t][g],
 // S[t][g] the group sums of A.  The Q4_K min term is itself a K = 16 MFMA per
 // super-block (8 groups x the hi/lo parts of S against dmin mn, an exact fp16 pair).
 // The activations are carried as fp16 pairs: k_prep_rows scales row t by
 // 2^(14 - e_t) (e_t the exponent of its largest magnitude, |A s| < 2^15) and
-// splits a = a_hi + a_lo; each 16x16x32 step runs a_hi p + a_lo p (Q6_K adds
-// a_hi p_lo), accumulating in f32.  Only the a_lo p_lo term (below 2^-22
-// relative) is dropped: per product about 2^-21 relative, the level of the f32
+// splits a = a_hi + a_lo; each 16x16x32 step runs a_hi p + a_lo p (Q6_K:
+// a_hi w_hi + a_lo w_hi + a_hi w_lo), accumulating in f32.  Only the lo x lo
+// term (below 2^-22 relative) is dropped: per product about 2^-21 relative, the level of the f32
 // reference's own roundings.  One fp16 rounding of either operand would move
 // the synthetic models' logits by up to 4%: their activations amplify
 // rounding ~100x and reach 4e7, past the fp16 range.
@@ -30,11 +31,13 @@
 // unpacks into fp16 pairs ((w >> 4j) & 0x000F000F holds elements j, j + 4);
 // k_prep_rows writes A in that order.
 //
-// Tiling: a workgroup of 4 waves computes a 128 (tokens) x 128 (weight rows)
-// tile; wave (wm, wn) owns 64 x 64 as 4 x 4 MFMA tiles.  Per 32-wide K step
-// the workgroup copies one 128 x 32 slab of A (hi and lo planes) and unpacks
-// one 128 x 32 slab of p into LDS (double-buffered: one barrier per step),
-// and the raw loads of the next step are in flight while the MFMAs run.
+// Tiling: a workgroup of 8 waves (one per CU) computes a 128 (tokens) x 256
+// (weight rows) tile; wave (wm, wn) owns 64 x 64 as 4 x 4 MFMA tiles.  The
+// wide tile halves the A bytes (two fp16 planes, 7x the weight bytes) per
+// MFMA against a 128 x 128 one.  Per 32-wide K step the workgroup copies one
+// 128 x 32 slab of A (hi and lo planes) and unpacks one 256 x 32 slab of p
+// into LDS (double-buffered: one barrier per step), and the raw loads of the
+// next step are in flight while the MFMAs run.
 // Block scales and the Q4_K min operands go to a per-block side area.
 // MFMA v_mfma_f32_16x16x32_f16: lane i + 16g holds A[i][8g..8g+7] and
 // B[8g..8g+7][i]; C[4g + r][i] arrives in lane i + 16g, register r
@@ -53,10 +56,10 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kBM = 128, kBN = 256, kBK = 32;
 constexpr int kLdk = 32;  // halves per LDS row (64 B), 16-byte chunks XOR-swizzled by swz()
-constexpr int kThreads = 256;
-constexpr int kPlane = kBM * kLdk;  // halves in one 128 x 32 plane
+constexpr int kThreads = 512;
+constexpr int kAPlane = kBM * kLdk, kWPlane = kBN * kLdk;  // halves in one 128 (256) x 32 plane
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024 in both halves: 0x6400 | u is 1024 + u (u < 1024)
 
 struct GemmArgs {
@@ -76,21 +79,25 @@ __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, 
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 splat(float v) { return h2{(_Float16)v, (_Float16)v}; }
 
-// Physical 16-byte chunk of logical chunk c (0..3) in LDS row r: rows 4a + b
-// keep chunk c at c ^ a, so the 16 rows of a fragment read land on 16
-// distinct 4-bank groups (64-byte rows: rows b, b + 4, ... share banks).
-__device__ __forceinline__ int swz(int r, int c) { return r * kLdk + 8 * (c ^ ((r >> 2) & 3)); }
+// Physical 16-byte chunk of logical chunk c (0..3) in LDS row r (64-byte
+// rows): c ^ ((r >> 1) ^ (r >> 2)) & 3.  A fragment read (16 rows, one chunk)
+// and a staging write (8 rows x 2 chunks per 16 lanes) then touch distinct
+// banks both 8 lanes per cycle over 32 banks and 16 lanes over 64 (an
+// r >> 2 swizzle left 2-way conflicts on every fragment read, measured).
+__device__ __forceinline__ int swz(int r, int c) { return r * kLdk + 8 * (c ^ (((r >> 1) ^ (r >> 2)) & 3)); }
 
 // Per-block side data: block scale of each weight row (f32) and, for Q4_K,
 // the min-term operands: bm[n] = {hi[8], lo[8]} of -32 dmin mn per group,
-// sa[t] = {hi[8], lo[8]} of S / 32 per group.
+// sa[t] = {hi[8], lo[8]} of S / 32 per group; rows padded to 40 bytes so the
+// 8-byte reads of 16 rows fall on distinct banks.
+constexpr int kSideRow = 20;
 struct SideD {
   float d[kBN];
 };
 struct SideMin {
   float d[kBN];
-  _Float16 bm[kBN][16];
-  _Float16 sa[kBM][16];
+  _Float16 bm[kBN][kSideRow];
+  _Float16 sa[kBM][kSideRow];
 };
 
 // ---------------------------------------------------------------------------
@@ -104,7 +111,7 @@ struct WQ;
 template <>
 struct WQ<T_Q4K> {  // tiled Q4_K (src/gguf/dequant.rs:133-161)
   static constexpr int kSb = 8;  // steps per super-block
-  static constexpr bool kMins = true, kPLo = false;
+  static constexpr bool kMins = true, kPLo = false, kScaled = true;
   typedef SideMin Side;
   uint4 hdr;  // d, dmin, 12 scale bytes: kept through the super-block
   uint2 qs;
@@ -154,8 +161,13 @@ struct WQ<T_Q4K> {  // tiled Q4_K (src/gguf/dequant.rs:133-161)
 
 template <>
 struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
+  // The u8 scale makes p = sc (q - 32) up to 8160, past fp16's integers, so the
+  // weight itself is carried: w = (d sc)(q - 32) as the reference rounds it
+  // (d sc is exact, one rounding of the product), split w = w_hi + w_lo (22
+  // bits of its 24).  No block scale is left to apply; |w| <= 8160 |d| stays
+  // inside the fp16 range (checked at upload).
   static constexpr int kSb = 8;
-  static constexpr bool kMins = false, kPLo = true;
+  static constexpr bool kMins = false, kPLo = true, kScaled = false;
   typedef SideD Side;
   uint2 ql;
   uint32_t hw, sc, d;
@@ -177,15 +189,21 @@ struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
     const uint32_t hi = (s >= 4 ? (hw >> (s - 4)) : (hw << (4 - s))) & 0x00300030u;
     return lo | hi | kMagic;
   }
-  __device__ void stage(_Float16* bp, _Float16* bpl, Side& sd, uint32_t, int wr, int h, bool sb0) const {
-    const h2 s2 = splat((float)sc), m2 = splat(-1056.f);
+  __device__ void stage(_Float16* bp, _Float16* bpl, Side&, uint32_t, int wr, int h, bool) const {
+    const float ds = h2f(d) * (float)sc;  // exact: 11 x 8 bits
+    const h2 m2 = splat(-1056.f);
     uint32_t vh[8], vl[8];
     auto pair = [&](uint32_t qv, int o) {
-      const h2 t = as_h2(qv) + m2;                              // q - 32, exact
-      const h2 ph = t * s2;                                     // p_hi: p rounded once
-      const h2 pl = __builtin_elementwise_fma(t, s2, -ph);      // p - p_hi, exact (|.| <= 4)
-      vh[o] = as_u32(ph);
-      vl[o] = as_u32(pl);
+      const h2 t = as_h2(qv) + m2;  // q - 32, exact
+      h2 wh, wl;
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const float w = ds * (float)t[e];  // the reference's rounding
+        wh[e] = (_Float16)w;
+        wl[e] = (_Float16)(w - (float)wh[e]);
+      }
+      vh[o] = as_u32(wh);
+      vl[o] = as_u32(wl);
     };
     pair(q_pair<0, 0>(), 0);
     pair(q_pair<0, 1>(), 1);
@@ -199,7 +217,6 @@ struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
     *(uint4*)(bp + swz(wr, 2 * h + 1)) = make_uint4(vh[4], vh[5], vh[6], vh[7]);
     *(uint4*)(bpl + swz(wr, 2 * h)) = make_uint4(vl[0], vl[1], vl[2], vl[3]);
     *(uint4*)(bpl + swz(wr, 2 * h + 1)) = make_uint4(vl[4], vl[5], vl[6], vl[7]);
-    if (sb0) sd.d[wr] = h2f(d);
   }
 };
 
@@ -211,7 +228,7 @@ __device__ __forceinline__ uint32_t byte_pair(uint32_t x, uint32_t y, int j) {
 template <>
 struct WQ<T_Q8_0> {  // Q8_0: qs[nb][32] | d[nb] (src/gguf/dequant.rs:101-109)
   static constexpr int kSb = 1;
-  static constexpr bool kMins = false, kPLo = false;
+  static constexpr bool kMins = false, kPLo = false, kScaled = true;
   typedef SideD Side;
   uint4 q;
   uint32_t d;
@@ -238,7 +255,7 @@ struct WQ<T_Q8_0> {  // Q8_0: qs[nb][32] | d[nb] (src/gguf/dequant.rs:101-109)
 template <>
 struct WQ<T_Q4_0> {  // Q4_0: qs[nb][16] | d[nb]; low nibbles -> j, high -> j + 16 (dequant.rs:70-82)
   static constexpr int kSb = 1;
-  static constexpr bool kMins = false, kPLo = false;
+  static constexpr bool kMins = false, kPLo = false, kScaled = true;
   typedef SideD Side;
   uint4 q;
   uint32_t d;
@@ -339,57 +356,56 @@ struct EpTraits<EpRope> {
 };
 
 template <int T, class Ep>
-__global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
+__global__ void __launch_bounds__(kThreads, 1) k_gemm(GemmArgs a, Ep ep) {
   using Q = WQ<T>;
   constexpr bool kPaired = EpTraits<Ep>::kPaired;
-  constexpr int kNp = Q::kPLo ? 4 : 3;  // planes: A hi, A lo, p (hi), [p lo]
-  constexpr bool kOverlap = !Q::kPLo;   // unpack step ks + 1 among the MFMAs of step ks
-  __shared__ __attribute__((aligned(16))) _Float16 lds[2][kNp][kPlane];
+  constexpr int kNw = Q::kPLo ? 2 : 1;  // weight planes: p (hi), [p lo]
+  __shared__ __attribute__((aligned(16))) _Float16 la[2][2][kAPlane];    // [buffer][A hi, A lo]
+  __shared__ __attribute__((aligned(16))) _Float16 lw[2][kNw][kWPlane];  // [buffer][p hi, p lo]
   __shared__ __attribute__((aligned(16))) typename Q::Side side[2];
   __shared__ int rexp[kBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const uint32_t m0 = blockIdx.y * kBM;
-  // output columns of the tile (paired: gate rows n0.. in W rows 0..63, up in 64..127)
+  // output columns of the tile (paired: gate rows n0.. in W rows 0..127, up in 128..255)
   const uint32_t n0 = blockIdx.x * (kPaired ? kBN / 2 : kBN);
 
-  // staging roles: A row ar (chunks ac, ac + 1 of both planes), W row wr half h.
+  // staging roles: A row ar chunk ac (both planes), W row wr half h.
   // Rows past the operands read a clamped row: their outputs are never stored.
-  const int h = tid & 1, ar = tid >> 1, wr = tid >> 1, ac = 2 * h;
+  const int h = tid & 1, wr = tid >> 1, ar = tid >> 2, ac = tid & 3;
   const uint32_t at = min(m0 + (uint32_t)ar, a.m - 1);
-  const GemmW& ws = (kPaired && wr >= 64) ? a.w1 : a.w0;
+  const GemmW& ws = (kPaired && wr >= kBN / 2) ? a.w1 : a.w0;
   const uint32_t w_rows_avail = (T == T_Q4K || T == T_Q6K) ? (ws.rows + 15u) & ~15u : ws.rows;
-  const uint32_t wrow = min(kPaired ? n0 + (uint32_t)(wr & 63) : n0 + (uint32_t)wr, w_rows_avail - 1);
+  const uint32_t wrow =
+      min(kPaired ? n0 + (uint32_t)(wr & (kBN / 2 - 1)) : n0 + (uint32_t)wr, w_rows_avail - 1);
   if (tid < kBM) rexp[tid] = m0 + (uint32_t)tid < a.m ? a.rexp[m0 + tid] : 0;
 
   const uint64_t arow = (uint64_t)at * a.k + 8u * (uint32_t)ac;
   const uint16_t* ahi = a.ahi + arow;
   const uint16_t* alo = a.alo + arow;
-  const uint16_t* gs = Q::kMins ? a.gsum + (uint64_t)at * (a.k >> 8) * 16u + 8u * (uint32_t)h : nullptr;
-  uint4 ra0, ra1, ra2, ra3;  // hi chunks ac, ac + 1; lo chunks ac, ac + 1
+  // group sums: thread (row ar, ac < 2) fetches S_hi (ac 0) or S_lo (ac 1)
+  const uint16_t* gs = Q::kMins ? a.gsum + (uint64_t)at * (a.k >> 8) * 16u + 8u * (uint32_t)(ac & 1) : nullptr;
+  uint4 ra0, ra1;  // chunk ac of the hi and lo planes
   uint4 rs = make_uint4(0, 0, 0, 0);  // S_hi or S_lo of the row's super-block (Q4_K)
   Q rw;
   // raw loads of step ks, group g of its block (sb0: g == 0)
   auto load_step = [&](uint32_t ks, uint32_t g, bool sb0) __attribute__((always_inline)) {
     const uint32_t k0 = ks * kBK;
     ra0 = *(const uint4*)(ahi + k0);
-    ra1 = *(const uint4*)(ahi + k0 + 8);
-    ra2 = *(const uint4*)(alo + k0);
-    ra3 = *(const uint4*)(alo + k0 + 8);
-    if (Q::kMins && sb0) rs = *(const uint4*)(gs + (ks >> 3) * 16u);
+    ra1 = *(const uint4*)(alo + k0);
+    if (Q::kMins && sb0) rs = *(const uint4*)(gs + (ks >> 3) * 16u);  // ac >= 2: a duplicate, unused
     rw.load(ws, wrow, ks, g, h, sb0);
   };
   auto stage = [&](int buf, int sbi, uint32_t g, bool sb0) __attribute__((always_inline)) {
-    _Float16* ph = lds[buf][0];
-    _Float16* pl = lds[buf][1];
-    *(uint4*)(ph + swz(ar, ac)) = ra0;
-    *(uint4*)(ph + swz(ar, ac + 1)) = ra1;
-    *(uint4*)(pl + swz(ar, ac)) = ra2;
-    *(uint4*)(pl + swz(ar, ac + 1)) = ra3;
+    *(uint4*)(la[buf][0] + swz(ar, ac)) = ra0;
+    *(uint4*)(la[buf][1] + swz(ar, ac)) = ra1;
     if constexpr (Q::kMins) {
-      if (sb0) *(uint4*)&side[sbi].sa[ar][8 * h] = rs;
+      if (sb0 && ac < 2) {  // 8-byte aligned rows: two 8-byte stores
+        *(uint2*)&side[sbi].sa[ar][8 * ac] = make_uint2(rs.x, rs.y);
+        *(uint2*)&side[sbi].sa[ar][8 * ac + 4] = make_uint2(rs.z, rs.w);
+      }
     }
-    rw.stage(lds[buf][2], Q::kPLo ? lds[buf][kNp - 1] : nullptr, side[sbi], g, wr, h, sb0);
+    rw.stage(lw[buf][0], Q::kPLo ? lw[buf][kNw - 1] : nullptr, side[sbi], g, wr, h, sb0);
   };
 
   f4 acc[4][4], cs[4][4];
@@ -406,7 +422,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
   int wcol[4];
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    wcol[j] = kPaired ? (j < 2 ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
+    wcol[j] = kPaired ? (j < 2 ? wn * 32 + 16 * j : kBN / 2 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
 
   // the block's integer dot products: cs = (first step of a block ? 0 : cs) + a p
   auto mma = [&](int buf, auto first) __attribute__((always_inline)) {
@@ -414,25 +430,30 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
     h8 bh[4], bl[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      bh[j] = *(const h8*)&lds[buf][2][swz(wcol[j] + fi, fg)];
-      if (Q::kPLo) bl[j] = *(const h8*)&lds[buf][kNp - 1][swz(wcol[j] + fi, fg)];
+      bh[j] = *(const h8*)&lw[buf][0][swz(wcol[j] + fi, fg)];
+      if (Q::kPLo) bl[j] = *(const h8*)&lw[buf][kNw - 1][swz(wcol[j] + fi, fg)];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int r = wm * 64 + 16 * i + fi;
-      const h8 ah = *(const h8*)&lds[buf][0][swz(r, fg)];
-      const h8 al = *(const h8*)&lds[buf][1][swz(r, fg)];
+      const h8 ah = *(const h8*)&la[buf][0][swz(r, fg)];
+      const h8 al = *(const h8*)&la[buf][1][swz(r, fg)];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], kFirst ? f4{0.f, 0.f, 0.f, 0.f} : cs[i][j], 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], c, 0, 0, 0);
-        if (Q::kPLo) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j], c, 0, 0, 0);
-        cs[i][j] = c;
+        if constexpr (Q::kScaled) {
+          f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], kFirst ? f4{0.f, 0.f, 0.f, 0.f} : cs[i][j], 0, 0, 0);
+          cs[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], c, 0, 0, 0);
+        } else {  // the weight itself: straight into acc
+          f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[i][j], 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], c, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j], c, 0, 0, 0);
+        }
       }
     }
   };
   // end of a block: acc += s cs (and the Q4_K min term)
   auto flush = [&](int sbi) __attribute__((always_inline)) {
+    if constexpr (!Q::kScaled) return;
     const typename Q::Side& sd = side[sbi];
     float dj[4];
 #pragma unroll
@@ -488,8 +509,6 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
     const int buf = Q::kSb % 2 == 0 ? (i & 1) ^ (int)(kb & 1) : (int)(ks & 1);
     if (i == 0) mma(buf, std::true_type{});
     else mma(buf, std::false_type{});
-    // Q6_K's second weight plane leaves no registers to overlap the two
-    if (!kOverlap) __builtin_amdgcn_sched_barrier(0);
     // step ks + 1 starts a block when i is the block's last step
     stage(buf ^ 1, i == Q::kSb - 1 ? sbi ^ 1 : sbi, (uint32_t)((i + 1) % Q::kSb), i == Q::kSb - 1);
     if (i == Q::kSb - 1) flush(sbi);
@@ -500,13 +519,8 @@ __global__ void __launch_bounds__(kThreads, 2) k_gemm(GemmArgs a, Ep ep) {
     __syncthreads();
   };
   for (uint32_t kb = ks0; kb < ks1; kb += Q::kSb) {
-    if constexpr (kOverlap) {
 #pragma unroll
-      for (int i = 0; i < Q::kSb; i++) step(kb, i);
-    } else {
-#pragma unroll 1
-      for (int i = 0; i < Q::kSb; i++) step(kb, i);
-    }
+    for (int i = 0; i < Q::kSb; i++) step(kb, i);
   }
 
   // epilogue: C[4 fg + r][fi] of fragment (i, j)
@@ -605,9 +619,9 @@ hipError_t dispatch(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   }
 }
 
-// Tiles of fewer than two workgroups per CU split K over grid.z (at least 8
+// Tiles of fewer than one workgroup per CU split K over grid.z (at least 8
 // steps per range), as far as the partial buffer holds them.
-constexpr uint32_t kTargetWgs = 512, kMinStepsPerSplit = 8;
+constexpr uint32_t kTargetWgs = 256, kMinStepsPerSplit = 8;
 
 GemmArgs args_of(const GemmIn& in, const GemmW& w, bool paired) {
   GemmArgs a{};
