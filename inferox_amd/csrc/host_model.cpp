@@ -77,6 +77,7 @@ struct ifx_session {
     // the GEMM activation operand (launch_prep_rows), sized for the widest input
     uint16_t *ahi = nullptr, *alo = nullptr, *gsum = nullptr;
     int* rexp = nullptr;
+    void* kv_split = nullptr;  // the attention's fp16 K/V pairs (attn_prefill_ws_bytes)
   } ws;
 };
 
@@ -336,6 +337,7 @@ int ensure_ws(ifx_session* s, uint64_t n) {
   const uint64_t W = std::max(D, F);  // widest GEMM input
   const uint64_t bx = al(n * D * 4), bm = al(n * F * 4), bh = al(n * W * 2), bg = al(n * (W / 256 + 1) * 32),
                  br = al(n * 4), bp = kSplitPartBytes;
+  const uint64_t ba = al(attn_prefill_ws_bytes((uint32_t)n, (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim));
   if (s->ws.alloc) {
     IFX_HIP(hipStreamSynchronize(s->stream));
     IFX_HIP(hipFree(s->ws.alloc));
@@ -343,7 +345,7 @@ int ensure_ws(ifx_session* s, uint64_t n) {
     s->ws.cap = 0;
   }
   void* p = nullptr;
-  if (hipMalloc(&p, 3 * bx + bm + 2 * bh + bg + br + bp) != hipSuccess)
+  if (hipMalloc(&p, 3 * bx + bm + 2 * bh + bg + br + bp + ba) != hipSuccess)
     return set_error(IFX_E_OOM, "prefill workspace of %llu rows", (unsigned long long)n);
   uint8_t* b = (uint8_t*)p;
   s->ws.x = (float*)b;
@@ -356,6 +358,7 @@ int ensure_ws(ifx_session* s, uint64_t n) {
   s->ws.gsum = (uint16_t*)(b + bm + 2 * bh);
   s->ws.rexp = (int*)(b + bm + 2 * bh + bg);
   s->ws.part = (float*)(b + bm + 2 * bh + bg + br);
+  s->ws.kv_split = b + bm + 2 * bh + bg + br + bp;
   s->ws.alloc = p;
   s->ws.cap = n;
   return IFX_OK;
@@ -394,7 +397,7 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
     IFX_HIP(gemm_rope(in, gw(L.k), kc, hd, kv_hs, row0, pos0, hd, rd, s->rope_cs, st));
     IFX_HIP(gemm_rows(in, gw(L.v), vc, hd, kv_hs, row0, hd, st));
     const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd,
-                             (uint32_t)s->max_seq, causal};
+                             (uint32_t)s->max_seq, causal, w.kv_split};
     IFX_HIP(launch_attn_prefill(aa, st));
     IFX_HIP(launch_prep_rows(w.att, N, D, D, nullptr, 0.f, in, st));
     IFX_HIP(gemm_residual(in, gw(L.o), w.x, D, st));

@@ -5,21 +5,34 @@
 // of kv head h / (n_heads / n_kv_heads): s = (q . k) / sqrt(head_dim), softmax,
 // o = p V (src/model/forward.rs:383-414 per row, src/ops.rs:223-239).
 //
-// Arithmetic as in kern_gemm.hip: both products run on
-// v_mfma_f32_16x16x32_f16 with each operand an fp16 hi/lo pair (three MFMAs
-// per step, f32 accumulation), within the rounding of the f32 reference.  The
-// fp16 range is kept by power-of-2 scales: per query row and per key row for
-// q . k (undone per score: the key scale is per lane, each lane holding one
-// key column of the score tile), and one per 64-row V block (P V of a block
-// lands in a temporary and is added as tmp / s).  Softmax weights lie in
-// [0, 1].
+// Arithmetic as in kern_gemm.hip: both products run on the fp16 matrix cores
+// with each operand an fp16 hi/lo pair (three MFMAs per step, f32
+// accumulation), within the rounding of the f32 reference.  The fp16 range is
+// kept by power-of-2 scales: per query row and per key row for q . k (undone
+// per score), and one per 64-key V block.  The V block scales are folded into
+// the softmax weights against a running reference exponent (the weights of a
+// block with a smaller scale shrink; a block with a larger one rescales the
+// accumulated output as a new running maximum does), so the output
+// accumulates in place.
 //
-// A workgroup of 4 waves owns 64 query rows of one head and walks the key
-// blocks of 64 rows with the running-max softmax; wave w owns queries
-// 16w .. 16w + 15: scores as a 16 x 64 tile (4 MFMA tiles), the weights through
-// the wave's LDS slab into A-operand order, O as head_dim / 16 tiles.  V is
-// staged transposed so that B fragments are contiguous.  The head dim is padded
-// to a multiple of 32 with zeros.
+// Two launches per layer:
+//   * k_kv_prep: one workgroup per (64-key block, kv head) splits the chunk's
+//     K rows (row scale) and its V block, transposed (block scale), into fp16
+//     hi/lo planes in the workspace, once for all the query heads and query
+//     blocks that read them.
+//   * k_attn_prefill: a workgroup of 8 waves owns 128 query rows of one head,
+//     wave w rows 16w .. 16w + 15 with their q scale and fp16 pairs in
+//     registers.  Per 64-key block it copies K and V^T into LDS (the next
+//     block's copies wait in registers meanwhile) and computes the scores
+//     transposed, S^T = K Q^T (16x16x32 MFMAs): lane i + 16g then holds the
+//     scores of query i against keys 16j + 4g + r, which is exactly the
+//     B operand of O^T = V^T P^T on v_mfma_f32_16x16x16_f16 (B[4g + r][i]),
+//     so the softmax weights never leave registers, and the row max and sum
+//     take two shuffles.  64 KB of LDS and one workgroup per CU (two waves
+//     per SIMD): each staged block serves 128 queries.
+// MFMA lane layouts: 16x16x32: lane i + 16g holds A[i][8g..8g+7],
+// B[8g..8g+7][i]; 16x16x16: A[i][4g..4g+3], B[4g..4g+3][i]; both give C[4g + r][i]
+// in lane i + 16g, register r.
 #include "kernels.h"
 
 namespace ifx {
@@ -27,299 +40,373 @@ namespace ifx {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
 
-constexpr int kQ = 64, kKB = 64, kThreads = 256;
-
-__device__ __forceinline__ f4 mfma3(h8 ah, h8 al, h8 bh, h8 bl, f4 c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
-}
+constexpr int kQ = 128, kKB = 64, kThreads = 512, kPrepThreads = 256;
 
 __device__ __forceinline__ int exp_of(uint32_t bits) {
   const int e = (int)((bits >> 23) & 255u) - 127;
   return e < -100 ? -100 : e;
 }
 
-// LDS row of W halves in 16-byte chunks; logical chunk c of row r sits at
-// c ^ x(r), x chosen so that the 16 consecutive rows of a fragment read at one
-// logical chunk land on 16 distinct 4-bank groups: rows of 256 bytes start on
-// the same bank (x = r mod 16), rows of 128 bytes on two (x = r / 2 mod 8),
-// rows of 64 or 192 bytes on four (x = r / 4 mod 4).
+template <int HD>
+struct Dims {
+  static constexpr int HP = (HD + 31) / 32 * 32;  // padded head dim
+  static constexpr int NCH = HP / 8;              // 16-byte chunks per K row
+  static constexpr int NKS = HP / 32;             // 16x16x32 steps over the head dim
+  static constexpr int NT = HP / 16;              // O^T tiles (16 dims each)
+};
+
+// Workspace of a chunk of n keys: K hi/lo [kvh][npad][HP], V^T hi/lo
+// [kvh][nkb][HP][64] (fp16 bits), key exponents [kvh][npad], V block
+// exponents [kvh][nkb].
+struct PrepWs {
+  uint16_t *kh, *kl, *vh, *vl;
+  int *kexp, *vexp;
+};
+
+constexpr uint64_t al256(uint64_t b) { return (b + 255) & ~255ull; }
+
+PrepWs prep_ws(void* base, uint32_t n, uint32_t n_kv, uint32_t hp) {
+  const uint64_t nkb = (n + kKB - 1) / kKB, npad = nkb * kKB, plane = (uint64_t)n_kv * npad * hp;
+  uint8_t* p = (uint8_t*)base;
+  PrepWs w;
+  w.kh = (uint16_t*)p;
+  p += al256(plane * 2);
+  w.kl = (uint16_t*)p;
+  p += al256(plane * 2);
+  w.vh = (uint16_t*)p;
+  p += al256(plane * 2);
+  w.vl = (uint16_t*)p;
+  p += al256(plane * 2);
+  w.kexp = (int*)p;
+  p += al256((uint64_t)n_kv * npad * 4);
+  w.vexp = (int*)p;
+  return w;
+}
+
+uint64_t prep_ws_bytes(uint32_t n, uint32_t n_kv, uint32_t hp) {
+  const uint64_t nkb = (n + kKB - 1) / kKB, npad = nkb * kKB, plane = (uint64_t)n_kv * npad * hp;
+  return 4 * al256(plane * 2) + al256((uint64_t)n_kv * npad * 4) + al256((uint64_t)n_kv * nkb * 4);
+}
+
+// LDS K rows (HP halves): 16-byte chunk c of row r at c ^ (r & 15) for
+// 256-byte rows, c ^ ((r >> 1) & 7) for 128, c ^ ((r >> 2) & 3) for 64 and
+// 192: the 16 rows of a fragment read at one chunk land on distinct banks.
 template <int W>
 __device__ __forceinline__ int swz(int r, int c) {
   constexpr int RB = 2 * W;
   const int x = (RB % 256 == 0) ? (r & 15) : (RB % 128 == 0) ? ((r >> 1) & 7) : ((r >> 2) & 3);
   return r * W + 8 * (c ^ x);
 }
+// LDS V^T rows (64 keys, 128 bytes): chunk c of row r at c ^ ((r ^ r >> 3) & 7),
+// so that the 8-byte reads of 16 consecutive rows at one offset land on
+// distinct banks (16 lanes over 64 banks; 8-lane groups see 8 distinct chunks)
+__device__ __forceinline__ int swzv(int r, int c) { return r * kKB + 8 * (c ^ ((r ^ (r >> 3)) & 7)); }
 
-__device__ __forceinline__ void split8(const float* y, float scale, h8& hi, h8& lo) {
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const float v = y[k] * scale;
-    const _Float16 x = (_Float16)v;
-    hi[k] = x;
-    lo[k] = (_Float16)(v - (float)x);
-  }
-}
-
+// ---------------------------------------------------------------------------
+// K/V preparation: grid (key block, kv head).
+// ---------------------------------------------------------------------------
 template <int HD>
-__global__ void __launch_bounds__(kThreads) k_attn_prefill(AttnPrefillArgs a) {
-  constexpr int HP = (HD + 31) / 32 * 32;  // padded head dim (halves per Q/K row)
-  constexpr int NCH = HP / 8;              // 16-byte chunks per Q/K row
-  constexpr int NT = HD / 16;              // output tiles per wave
-  constexpr int NKS = HP / 32;             // MFMA steps over the head dim
-  constexpr int KCH = NCH / 2;             // K staging: two threads per key row
-  constexpr int QCH = NCH / 4;             // Q staging: four threads per query row
-  extern __shared__ __attribute__((aligned(16))) _Float16 sm[];
-  _Float16* Qh = sm;                  // [kQ][HP]
-  _Float16* Ql = Qh + kQ * HP;
-  _Float16* Kh = Ql + kQ * HP;        // [kKB][HP]
-  _Float16* Kl = Kh + kKB * HP;
-  _Float16* Vh = Kl + kKB * HP;       // [HP][kKB] (transposed)
-  _Float16* Vl = Vh + HP * kKB;
-  _Float16* Pb = Vl + HP * kKB;       // per wave [2][16][kKB]
-  __shared__ int qexp[kQ], kexp[kKB];
-  __shared__ float vwmax[2];
-
+__global__ void __launch_bounds__(kPrepThreads) k_kv_prep(AttnPrefillArgs a, PrepWs w) {
+  using D = Dims<HD>;
+  constexpr int HP = D::HP, CPT = D::NCH / 4;  // K: four threads per key row
+  __shared__ float vblk[kKB][HD + 1];
+  __shared__ float red[kPrepThreads / 64];
+  const uint32_t b = blockIdx.x, hk = blockIdx.y, k0 = b * kKB;
+  const uint32_t nkb = gridDim.x, npad = nkb * kKB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int fi = lane & 15, fg = lane >> 4;
-  // heaviest query blocks of every head first
-  const uint32_t nqb = (a.n + kQ - 1) / kQ;
-  const uint32_t qb = nqb - 1 - blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads;
-  const uint32_t q0 = qb * kQ, group = a.n_heads / a.n_kv_heads, hk = h / group;
-  const uint32_t qd = a.n_heads * HD;
-  const float sqrt_hd = sqrtf((float)HD);
+  const float* kbase = a.k_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
+  const float* vbase = a.v_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
 
-  // ---- Q block: four threads per row, row scale by shuffles ----
+  // K: row kr, chunks qq * CPT .. + CPT - 1; the row scale from the four threads' maxima
   {
-    const int r = tid >> 2, qq = tid & 3;
-    const uint32_t t = q0 + (uint32_t)r;
-    float v[QCH][8];
+    const int kr = tid >> 2, qq = tid & 3;
+    const uint32_t key = k0 + (uint32_t)kr;
+    float v[CPT][8];
     float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < QCH; i++) {
-      const int col = 8 * (qq * QCH + i);
-      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-      if (t < a.n && col < HD) {
-        const float* src = a.q + (uint64_t)t * qd + h * HD + col;
-        x0 = *(const float4*)src;
-        x1 = *(const float4*)(src + 4);
+    for (int i = 0; i < CPT; i++) {
+      const int col = 8 * (qq * CPT + i);
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[i][k] = 0.f;
+      if (key < a.n && col < HD) {
+        const float4 x0 = *(const float4*)(kbase + (uint64_t)key * HD + col);
+        const float4 x1 = *(const float4*)(kbase + (uint64_t)key * HD + col + 4);
+        v[i][0] = x0.x; v[i][1] = x0.y; v[i][2] = x0.z; v[i][3] = x0.w;
+        v[i][4] = x1.x; v[i][5] = x1.y; v[i][6] = x1.z; v[i][7] = x1.w;
       }
-      v[i][0] = x0.x; v[i][1] = x0.y; v[i][2] = x0.z; v[i][3] = x0.w;
-      v[i][4] = x1.x; v[i][5] = x1.y; v[i][6] = x1.z; v[i][7] = x1.w;
 #pragma unroll
       for (int k = 0; k < 8; k++) mx = fmaxf(mx, fabsf(v[i][k]));
     }
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
     const int e = exp_of(__float_as_uint(mx));
-    if (qq == 0) qexp[r] = e;
+    if (qq == 0) w.kexp[(uint64_t)hk * npad + key] = e;
     const float sc = ldexpf(1.f, 14 - e);
+    const uint64_t row = ((uint64_t)hk * npad + key) * HP;
 #pragma unroll
-    for (int i = 0; i < QCH; i++) {
+    for (int i = 0; i < CPT; i++) {
       h8 hi, lo;
-      split8(v[i], sc, hi, lo);
-      *(h8*)&Qh[swz<HP>(r, qq * QCH + i)] = hi;
-      *(h8*)&Ql[swz<HP>(r, qq * QCH + i)] = lo;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float y = v[i][k] * sc;
+        hi[k] = (_Float16)y;
+        lo[k] = (_Float16)(y - (float)hi[k]);
+      }
+      const int ch = qq * CPT + i;
+      *(h8*)(w.kh + row + 8 * ch) = hi;
+      *(h8*)(w.kl + row + 8 * ch) = lo;
     }
   }
 
-  f4 o[NT];
+  // V block: into LDS, block maximum, then transposed rows d (64 keys each)
+  float mx = 0.f;
+  for (int c = tid; c < kKB * (HD / 4); c += kPrepThreads) {
+    const int r = c / (HD / 4), col = 4 * (c % (HD / 4));
+    const uint32_t key = k0 + (uint32_t)r;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (key < a.n) x = *(const float4*)(vbase + (uint64_t)key * HD + col);
+    vblk[r][col] = x.x;
+    vblk[r][col + 1] = x.y;
+    vblk[r][col + 2] = x.z;
+    vblk[r][col + 3] = x.w;
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+  }
 #pragma unroll
-  for (int t = 0; t < NT; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
-  float m[4], l[4];
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int ev = exp_of(__float_as_uint(mx));
+  if (tid == 0) w.vexp[(uint64_t)hk * nkb + b] = ev;
+  const float sc = ldexpf(1.f, 14 - ev);
+  // thread: V^T row d (< HP), 16-byte chunk c of its 64 keys
+  for (int u = tid; u < HP * 8; u += kPrepThreads) {
+    const int d = u >> 3, c = u & 7;
+    h8 hi, lo;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
+    for (int k = 0; k < 8; k++) {
+      const float y = d < HD ? vblk[8 * c + k][d] * sc : 0.f;
+      hi[k] = (_Float16)y;
+      lo[k] = (_Float16)(y - (float)hi[k]);
+    }
+    const uint64_t off = (((uint64_t)hk * nkb + b) * HP + d) * kKB + 8 * c;
+    *(h8*)(w.vh + off) = hi;
+    *(h8*)(w.vl + off) = lo;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention: grid 1-D over (query block, head), heaviest query blocks first.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a, PrepWs w) {
+  using D = Dims<HD>;
+  constexpr int HP = D::HP, NCH = D::NCH, NKS = D::NKS, NT = D::NT;
+  constexpr int UK = kKB * NCH * 2 / kThreads;  // K chunks per thread (both planes)
+  constexpr int UV = HP * 8 * 2 / kThreads;     // V^T chunks per thread
+  __shared__ __attribute__((aligned(16))) _Float16 Kh[kKB * HP], Kl[kKB * HP];
+  __shared__ __attribute__((aligned(16))) _Float16 Vh[HP * kKB], Vl[HP * kKB];
+  __shared__ int kexp_s[kKB];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fi = lane & 15, fg = lane >> 4;
+  const uint32_t nqb = (a.n + kQ - 1) / kQ;
+  const uint32_t qb = nqb - 1 - blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads;
+  const uint32_t q0 = qb * kQ, group = a.n_heads / a.n_kv_heads, hk = h / group;
+  const uint32_t qd = a.n_heads * HD;
+  const uint32_t nkb_all = (a.n + kKB - 1) / kKB, npad = nkb_all * kKB;
+  const float rsq = 1.0f / sqrtf((float)HD);
+
+  // ---- this lane's query (fi) as the B operand of S^T = K Q^T, in registers ----
+  const uint32_t qt = q0 + 16 * wave + fi;
+  h8 qh[NKS], ql[NKS];
+  float qinv;
+  {
+    float v[NKS][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const int col = 32 * ks + 8 * fg;
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[ks][k] = 0.f;
+      if (qt < a.n && col < HD) {
+        const float* src = a.q + (uint64_t)qt * qd + h * HD + col;
+        const float4 x0 = *(const float4*)src, x1 = *(const float4*)(src + 4);
+        v[ks][0] = x0.x; v[ks][1] = x0.y; v[ks][2] = x0.z; v[ks][3] = x0.w;
+        v[ks][4] = x1.x; v[ks][5] = x1.y; v[ks][6] = x1.z; v[ks][7] = x1.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) mx = fmaxf(mx, fabsf(v[ks][k]));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const int e = exp_of(__float_as_uint(mx));
+    qinv = ldexpf(1.f, e - 14);
+    const float sc = ldexpf(1.f, 14 - e);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++)
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float y = v[ks][k] * sc;
+        qh[ks][k] = (_Float16)y;
+        ql[ks][k] = (_Float16)(y - (float)qh[ks][k]);
+      }
   }
 
   const uint32_t last_q = min(q0 + kQ, a.n) - 1;
   const uint32_t kend = a.causal ? last_q + 1 : a.n;  // keys [0, kend)
   const uint32_t nkb = (kend + kKB - 1) / kKB;
-  _Float16* Ph = Pb + wave * 2 * 16 * kKB;
-  _Float16* Pl = Ph + 16 * kKB;
 
-  // K/V staging roles: waves 0-1 stage K rows (two threads per row, KCH chunks
-  // each), waves 2-3 stage V as 8 x 8 tiles (8 keys x 8 dims) for the transpose
-  const bool krole = tid < 128;
-  const int kr = tid >> 1, khalf = tid & 1;  // K role
-  const int vt = tid - 128, vkc = vt / NCH, vdc = vt % NCH;  // V role (vt < 8 NCH)
-  const bool vtile = !krole && vt < 8 * NCH;
-  float st[64];  // the next block's K chunks or V tile, loaded one block ahead
-  auto load_block = [&](uint32_t k0) {
+  // ---- K / V^T block copies: the next block's chunks wait in registers ----
+  u4 rk[UK], rv[UV];
+  int rke = 0, rve = 0;
+  auto load_k = [&](uint32_t kb) __attribute__((always_inline)) {
+    const uint64_t kbase = ((uint64_t)hk * npad + kb * kKB) * HP;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-      if (krole) {
-        const int col = 8 * (khalf * KCH + i);
-        const uint32_t key = k0 + (uint32_t)kr;
-        if (i < KCH && key < kend && col < HD) {
-          const float* src = a.k_cache + ((uint64_t)hk * a.max_seq + a.row0 + key) * HD + col;
-          x0 = *(const float4*)src;
-          x1 = *(const float4*)(src + 4);
-        }
-      } else {
-        const int col = 8 * vdc;
-        const uint32_t key = k0 + (uint32_t)(8 * vkc + i);
-        if (vtile && key < kend && col < HD) {
-          const float* src = a.v_cache + ((uint64_t)hk * a.max_seq + a.row0 + key) * HD + col;
-          x0 = *(const float4*)src;
-          x1 = *(const float4*)(src + 4);
-        }
-      }
-      st[8 * i] = x0.x; st[8 * i + 1] = x0.y; st[8 * i + 2] = x0.z; st[8 * i + 3] = x0.w;
-      st[8 * i + 4] = x1.x; st[8 * i + 5] = x1.y; st[8 * i + 6] = x1.z; st[8 * i + 7] = x1.w;
+    for (int u = 0; u < UK; u++) {
+      const int c = tid + kThreads * u, pl = c / (kKB * NCH), rem = c % (kKB * NCH);
+      rk[u] = *(const u4*)((pl ? w.kl : w.kh) + kbase + (uint64_t)rem * 8);
     }
+    if (tid < kKB) rke = w.kexp[(uint64_t)hk * npad + kb * kKB + tid];
   };
-  load_block(0);
+  auto load_v = [&](uint32_t kb) __attribute__((always_inline)) {
+    const uint64_t vbase = ((uint64_t)hk * nkb_all + kb) * HP * kKB;
+#pragma unroll
+    for (int u = 0; u < UV; u++) {
+      const int c = tid + kThreads * u, pl = c / (HP * 8), rem = c % (HP * 8);
+      rv[u] = *(const u4*)((pl ? w.vl : w.vh) + vbase + (uint64_t)rem * 8);
+    }
+    rve = w.vexp[(uint64_t)hk * nkb_all + kb];
+  };
+  auto store_block = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < UK; u++) {
+      const int c = tid + kThreads * u, pl = c / (kKB * NCH), rem = c % (kKB * NCH);
+      *(u4*)((pl ? Kl : Kh) + swz<HP>(rem / NCH, rem % NCH)) = rk[u];
+    }
+#pragma unroll
+    for (int u = 0; u < UV; u++) {
+      const int c = tid + kThreads * u, pl = c / (HP * 8), rem = c % (HP * 8);
+      *(u4*)((pl ? Vl : Vh) + swzv(rem >> 3, rem & 7)) = rv[u];
+    }
+    if (tid < kKB) kexp_s[tid] = rke;
+  };
+
+  f4 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  int vref = -1000;  // reference V exponent of the accumulated output
+
+  load_k(0);
+  load_v(0);
   for (uint32_t kb = 0; kb < nkb; kb++) {
     const uint32_t k0 = kb * kKB;
-    // phase A: maxima of the staged block
-    float mx = 0.f;
-#pragma unroll
-    for (int k = 0; k < 64; k++) mx = fmaxf(mx, fabsf(st[k]));
-    if (krole) {
-      mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    } else {
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      if (lane == 0) vwmax[wave - 2] = mx;
-    }
-    // every wave is past the previous block's K/V/P reads
+    __syncthreads();  // every wave is past the previous block's reads
+    store_block();
+    const int ve = rve;
     __syncthreads();
-    // phase B: hi/lo into LDS
-    if (krole) {
-      const int e = exp_of(__float_as_uint(mx));
-      if (khalf == 0) kexp[kr] = e;
-      const float sc = ldexpf(1.f, 14 - e);
-#pragma unroll
-      for (int i = 0; i < KCH; i++) {
-        h8 hi, lo;
-        split8(&st[8 * i], sc, hi, lo);
-        *(h8*)&Kh[swz<HP>(kr, khalf * KCH + i)] = hi;
-        *(h8*)&Kl[swz<HP>(kr, khalf * KCH + i)] = lo;
-      }
-    } else if (vtile) {
-      const int e = exp_of(__float_as_uint(fmaxf(vwmax[0], vwmax[1])));
-      const float sc = ldexpf(1.f, 14 - e);
-#pragma unroll
-      for (int d = 0; d < 8; d++) {  // V^T row 8 vdc + d: keys 8 vkc .. 8 vkc + 7
-        float col[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) col[k] = st[8 * k + d];
-        h8 hi, lo;
-        split8(col, sc, hi, lo);
-        *(h8*)&Vh[swz<kKB>(8 * vdc + d, vkc)] = hi;
-        *(h8*)&Vl[swz<kKB>(8 * vdc + d, vkc)] = lo;
-      }
-    }
-    __syncthreads();
-    // the next block's loads fly during this block's products
-    if (kb + 1 < nkb) load_block(k0 + kKB);
-    const int ve = exp_of(__float_as_uint(fmaxf(vwmax[0], vwmax[1])));
-    const float vinv = ldexpf(1.f, ve - 14);
-    float qinv[4], kinv[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) qinv[r] = ldexpf(1.f, qexp[16 * wave + 4 * fg + r] - 14);
-#pragma unroll
-    for (int j = 0; j < 4; j++) kinv[j] = ldexpf(1.f, kexp[16 * j + fi] - 14);
+    // the next block's K now, its V after the scores (fewer registers held)
+    const bool more = kb + 1 < nkb;
+    if (more) load_k(kb + 1);
 
-    // ---- scores: 16 queries of this wave x 64 keys ----
+    // ---- S^T: keys 16j + 4fg + r (rows) x this lane's query fi (column) ----
+    // (one head-dim step at a time: four independent accumulator chains, and
+    // the fragments of one step live at once)
     f4 s[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) s[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) {
-      const int qr = 16 * wave + fi;
-      const h8 ah = *(const h8*)&Qh[swz<HP>(qr, 4 * ks + fg)];
-      const h8 al = *(const h8*)&Ql[swz<HP>(qr, 4 * ks + fg)];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int krow = 16 * j + fi;
-        const h8 bh = *(const h8*)&Kh[swz<HP>(krow, 4 * ks + fg)];
-        const h8 bl = *(const h8*)&Kl[swz<HP>(krow, 4 * ks + fg)];
-        s[j] = mfma3(ah, al, bh, bl, s[j]);
+        const h8 kh8 = *(const h8*)&Kh[swz<HP>(16 * j + fi, 4 * ks + fg)];
+        const h8 kl8 = *(const h8*)&Kl[swz<HP>(16 * j + fi, 4 * ks + fg)];
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh8, qh[ks], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh8, ql[ks], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl8, qh[ks], s[j], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // scale, mask, running max / sum; weights to LDS in A-operand order
-    float alpha[4];
+    // scale, mask, running max / sum over the block's keys for query qt
+    float bm = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint32_t qt = q0 + 16 * wave + 4 * fg + r;
-      float bm = -INFINITY;
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t key = k0 + 16 * j + fi;
+      for (int r = 0; r < 4; r++) {
+        const int kr = 16 * j + 4 * fg + r;
+        const uint32_t key = k0 + (uint32_t)kr;
         const bool ok = key < kend && (!a.causal || key <= qt);
-        s[j][r] = ok ? (s[j][r] * (qinv[r] * kinv[j])) / sqrt_hd : -INFINITY;
+        const float kinv = ldexpf(1.f, kexp_s[kr] - 14);
+        s[j][r] = ok ? (s[j][r] * (qinv * kinv)) * rsq : -INFINITY;
         bm = fmaxf(bm, s[j][r]);
       }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float alpha = mn == -INFINITY ? 1.f : expf(m - mn);
+    const int vnew = ve > vref ? ve : vref;
+    const float oscale = alpha * ldexpf(1.f, vref - vnew);  // the output's rescale
+    const float pscale = ldexpf(1.f, ve - vnew);            // this block's weights, <= 1
+    float ps = 0.f;
+    h4 ph[4], pl[4];
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
-      const float mn = fmaxf(m[r], bm);
-      alpha[r] = mn == -INFINITY ? 1.f : expf(m[r] - mn);
-      float ps = 0.f;
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int r = 0; r < 4; r++) {
         const float p = mn == -INFINITY ? 0.f : expf(s[j][r] - mn);
         ps += p;
-        const _Float16 ph = (_Float16)p;
-        const int row = 4 * fg + r, col = 16 * j + fi;
-        Ph[swz<kKB>(row, col >> 3) + (col & 7)] = ph;
-        Pl[swz<kKB>(row, col >> 3) + (col & 7)] = (_Float16)(p - (float)ph);
+        const float pw = p * pscale;
+        ph[j][r] = (_Float16)pw;
+        pl[j][r] = (_Float16)(pw - (float)ph[j][r]);
       }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+    m = mn;
+    vref = vnew;
+    if (more) load_v(kb + 1);
+    // ---- O^T = V^T P^T: dims 16t + 4fg + r x query fi (one key tile at a time) ----
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
-      l[r] = l[r] * alpha[r] + ps;
-      m[r] = mn;
-    }
-    __syncthreads();  // the weights written by all lanes are visible
-    // ---- O = alpha O + (P V_scaled) / s_v ----
-    h8 pah[kKB / 32], pal[kKB / 32];
+    for (int t = 0; t < NT; t++) o[t] *= oscale;
 #pragma unroll
-    for (int ks = 0; ks < kKB / 32; ks++) {
-      pah[ks] = *(const h8*)&Ph[swz<kKB>(fi, 4 * ks + fg)];
-      pal[ks] = *(const h8*)&Pl[swz<kKB>(fi, 4 * ks + fg)];
-    }
+    for (int j = 0; j < 4; j++) {
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      f4 tmp = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kKB / 32; ks++) {
-        const h8 bh = *(const h8*)&Vh[swz<kKB>(16 * t + fi, 4 * ks + fg)];
-        const h8 bl = *(const h8*)&Vl[swz<kKB>(16 * t + fi, 4 * ks + fg)];
-        tmp = mfma3(pah[ks], pal[ks], bh, bl, tmp);
+      for (int t = 0; t < NT; t++) {
+        const int vr = 16 * t + fi, vc = 16 * j + 4 * fg;
+        const h4 vh4 = *(const h4*)&Vh[swzv(vr, vc >> 3) + (vc & 7)];
+        const h4 vl4 = *(const h4*)&Vl[swzv(vr, vc >> 3) + (vc & 7)];
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh4, ph[j], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh4, pl[j], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vl4, ph[j], o[t], 0, 0, 0);
       }
-#pragma unroll
-      for (int r = 0; r < 4; r++) o[t][r] = o[t][r] * alpha[r] + tmp[r] * vinv;
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if (qt < a.n) {
+    const float inv = ldexpf(1.f, vref - 14) / l;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const uint32_t t = q0 + 16 * wave + 4 * fg + r;
-    if (t >= a.n) continue;
-    const float inv = 1.0f / l[r];
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) a.out[(uint64_t)t * qd + h * HD + 16 * tt + fi] = o[tt][r] * inv;
+    for (int t = 0; t < NT; t++) {
+      const int d = 16 * t + 4 * fg;
+      if (d < HD)
+        *(float4*)(a.out + (uint64_t)qt * qd + h * HD + d) =
+            make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+    }
   }
 }
 
 template <int HD>
 hipError_t go(const AttnPrefillArgs& a, hipStream_t st) {
-  constexpr int HP = (HD + 31) / 32 * 32;
-  const size_t lds = ((size_t)2 * kQ * HP + (size_t)2 * kKB * HP + (size_t)2 * HP * kKB + (size_t)4 * 2 * 16 * kKB) * 2;
-  static bool opted = false;
-  if (!opted) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_attn_prefill<HD>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
-    opted = true;
-  }
-  dim3 grid(((a.n + kQ - 1) / kQ) * a.n_heads);
-  hipLaunchKernelGGL(k_attn_prefill<HD>, grid, dim3(kThreads), lds, st, a);
+  using D = Dims<HD>;
+  const PrepWs w = prep_ws(a.ws, a.n, a.n_kv_heads, D::HP);
+  const uint32_t nkb = (a.n + kKB - 1) / kKB;
+  hipLaunchKernelGGL(k_kv_prep<HD>, dim3(nkb, a.n_kv_heads), dim3(kPrepThreads), 0, st, a, w);
+  const dim3 grid(((a.n + kQ - 1) / kQ) * a.n_heads);
+  hipLaunchKernelGGL(k_attn_prefill<HD>, grid, dim3(kThreads), 0, st, a, w);
   return hipGetLastError();
 }
 
@@ -327,9 +414,13 @@ hipError_t go(const AttnPrefillArgs& a, hipStream_t st) {
 
 bool attn_prefill_head_dim(uint32_t hd) { return hd == 48 || hd == 64 || hd == 96 || hd == 128; }
 
+uint64_t attn_prefill_ws_bytes(uint32_t n, uint32_t n_kv_heads, uint32_t head_dim) {
+  return prep_ws_bytes(n, n_kv_heads, (head_dim + 31) / 32 * 32);
+}
+
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t st) {
   if (a.n == 0) return hipSuccess;
-  if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads) return hipErrorInvalidValue;
+  if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || !a.ws) return hipErrorInvalidValue;
   switch (a.head_dim) {
     case 48: return go<48>(a, st);
     case 64: return go<64>(a, st);

@@ -130,8 +130,10 @@ struct AttnPrefillArgs {
   float* out;            // [n][n_heads * head_dim]
   uint32_t n, row0, n_heads, n_kv_heads, head_dim, max_seq;
   bool causal;
+  void* ws;              // attn_prefill_ws_bytes(n, n_kv_heads, head_dim): the split K/V
 };
 bool attn_prefill_head_dim(uint32_t head_dim);
+uint64_t attn_prefill_ws_bytes(uint32_t n, uint32_t n_kv_heads, uint32_t head_dim);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t st);
 
 // ---- small ops (kern_ops.hip) ----
