@@ -145,6 +145,25 @@ int ifx_generate(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t ma
  * picks; out_tokens[i] = argmax of step i's logits.  len grows by n_steps. */
 int ifx_decode_greedy(ifx_session* s, uint32_t token, uint64_t n_steps, uint32_t* out_tokens);
 
+/* Sampler::sample (src/sampler.rs:28-76) for ifx_generate_sampled: temperature
+ * (0: greedy argmax), top_k (0: off), top_p (1: off), and the seed of the
+ * draws.  Diverges from the reference by design: the logits are shifted by
+ * their maximum before exp (the reference's exp(z/T) overflows past 88) and
+ * the draws come from splitmix64(seed, step) instead of rand's thread_rng, so
+ * a run is reproducible.  Default: temperature 0.  No reference counterpart
+ * as a C entry point: the reference passes a Sampler to its CLI loop. */
+int ifx_session_set_sampler(ifx_session* s, float temperature, uint32_t top_k, float top_p, uint64_t seed);
+
+/* ifx_generate with every generated token drawn by the session's sampler on
+ * the device (k_sample between the logits and the state update). */
+int ifx_generate_sampled(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t max_tokens,
+                         uint32_t* out_tokens);
+
+/* One-off draws from host logits[vocab] (tests): n_draws draws, draw i with
+ * counter i, as generate step i would. */
+int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, uint32_t top_k, float top_p,
+                      uint64_t seed, uint32_t n_draws, uint32_t* out);
+
 /* KV state in the reference layout: k,v = [n_layers][len][n_kv_heads*head_dim]
  * f32 (src/model/cache.rs:8-24), host memory.  Import sets len. */
 int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len);

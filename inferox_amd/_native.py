@@ -49,6 +49,9 @@ SIGNATURES = {
     "ifx_forward": (i32, [vp, vp, u64, vp]),
     "ifx_generate": (i32, [vp, vp, u64, u64, vp]),
     "ifx_decode_greedy": (i32, [vp, u32, u64, vp]),
+    "ifx_session_set_sampler": (i32, [vp, C.c_float, u32, C.c_float, u64]),
+    "ifx_generate_sampled": (i32, [vp, vp, u64, u64, vp]),
+    "ifx_sample_logits": (i32, [vp, u32, C.c_float, u32, C.c_float, u64, u32, vp]),
     "ifx_kv_import": (i32, [vp, vp, vp, u64]),
     "ifx_kv_export": (i32, [vp, vp, vp, u64]),
     "ifx_session_last_elapsed_ms": (i32, [vp, P(f32)]),

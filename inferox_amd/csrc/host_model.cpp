@@ -60,8 +60,12 @@ struct ifx_session {
   DevState* state = nullptr;
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
   uint32_t attn_chunk = 64, max_chunks = 0;
-  hipGraphExec_t exec = nullptr;
+  hipGraphExec_t exec = nullptr;        // the greedy step
   bool graph_tried = false;
+  hipGraphExec_t exec_sample = nullptr;  // the step with k_sample before finalize
+  bool graph_tried_sample = false;
+  bool sampling = false;                 // set for the duration of ifx_generate_sampled
+  float* probs = nullptr;                // k_sample scratch [vocab]
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
   std::vector<void*> allocs;
@@ -209,6 +213,7 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       return IFX_OK;
     }
     case 7:
+      if (s->sampling) IFX_HIP(launch_sample(s->logits, s->probs, (uint32_t)c.vocab_size, s->state, st));
       IFX_HIP(launch_finalize(s->state, st));
       return IFX_OK;
     default:
@@ -292,8 +297,10 @@ uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->
 // Replay the captured step (capturing it on first use); direct launches if the
 // runtime refuses capture.
 int run_step(ifx_session* s) {
-  if (!s->graph_tried) {
-    s->graph_tried = true;
+  hipGraphExec_t& exec = s->sampling ? s->exec_sample : s->exec;
+  bool& tried = s->sampling ? s->graph_tried_sample : s->graph_tried;
+  if (!tried) {
+    tried = true;
     // IFX_NO_GRAPH=1: launch the step's kernels directly (used under profilers
     // that do not follow captured graphs)
     const char* ng = getenv("IFX_NO_GRAPH");
@@ -306,15 +313,15 @@ int run_step(ifx_session* s) {
       int rc = enqueue_step(s);
       hipError_t e = hipStreamEndCapture(s->stream, &g);
       if (rc == IFX_OK && e == hipSuccess && g) {
-        if (hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0) != hipSuccess) s->exec = nullptr;
+        if (hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) exec = nullptr;
       }
       if (g) (void)hipGraphDestroy(g);
       (void)hipGetLastError();
     }
   }
   s->steps++;
-  if (s->exec) {
-    IFX_HIP(hipGraphLaunch(s->exec, s->stream));
+  if (exec) {
+    IFX_HIP(hipGraphLaunch(exec, s->stream));
     return IFX_OK;
   }
   return enqueue_step(s);
@@ -417,6 +424,7 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
   gh.norm_w = m->out_norm;
   gh.eps = c.norm_eps;
   IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
+  if (s->sampling) IFX_HIP(launch_sample(s->logits, s->probs, (uint32_t)c.vocab_size, s->state, st));
   IFX_HIP(launch_finalize(s->state, st));
   if (logits_out) {
     const uint64_t V = c.vocab_size, rows = std::min<uint64_t>(n, 512);
@@ -457,6 +465,7 @@ void session_free(ifx_session* s) {
   if (s->ws.alloc) (void)hipFree(s->ws.alloc);
   if (s->ws.logits) (void)hipFree(s->ws.logits);
   if (s->exec) (void)hipGraphExecDestroy(s->exec);
+  if (s->exec_sample) (void)hipGraphExecDestroy(s->exec_sample);
   if (s->ev0) (void)hipEventDestroy(s->ev0);
   if (s->ev1) (void)hipEventDestroy(s->ev1);
   for (void* p : s->allocs) (void)hipFree(p);
@@ -604,6 +613,7 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   A((void**)&s->attn, D * 4);
   A((void**)&s->mid, F * 4);
   A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
+  A((void**)&s->probs, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
   A((void**)&s->partial, (uint64_t)c.n_kv_heads * s->max_chunks * attn_partial_floats(G, c.head_dim) * 4);
   A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
   A((void**)&s->state, sizeof(DevState));
@@ -632,6 +642,7 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   init.feed_ids = s->feed_ids;
   init.out_tokens = s->out_tokens;
   init.out_cap = (uint32_t)max_seq_len;
+  init.top_p = 1.0f;
   if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
@@ -789,6 +800,69 @@ int ifx_generate(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t ma
     out_tokens[i] &= 0x7fffffffu;
   }
   return rc == IFX_OK ? IFX_OK : set_error(rc, "NaN logit met by argmax");
+}
+
+int ifx_session_set_sampler(ifx_session* s, float temperature, uint32_t top_k, float top_p, uint64_t seed) {
+  clear_error();
+  if (!s) return set_error(IFX_E_INVALID_ARG, "null session");
+  if (!(temperature >= 0.f) || !isfinite(temperature) || !(top_p >= 0.f && top_p <= 1.f))
+    return set_error(IFX_E_INVALID_ARG, "sampler needs temperature >= 0 and 0 <= top_p <= 1");
+  StateOp op{STATE_SAMPLER, top_k, 0};
+  op.f0 = temperature;
+  op.f1 = top_p;
+  op.seed = seed;
+  IFX_HIP(launch_state(s->state, op, s->stream));
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  return IFX_OK;
+}
+
+int ifx_generate_sampled(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t max_tokens,
+                         uint32_t* out_tokens) {
+  if (!s) return set_error(IFX_E_INVALID_ARG, "null session");
+  // the prompt's last step and every generated step draw with the session's sampler
+  struct Guard {
+    ifx_session* s;
+    ~Guard() { s->sampling = false; }
+  } guard{s};
+  s->sampling = true;
+  return ifx_generate(s, prompt, n, max_tokens, out_tokens);
+}
+
+int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, uint32_t top_k, float top_p,
+                      uint64_t seed, uint32_t n_draws, uint32_t* out) {
+  clear_error();
+  if (!logits || (n_draws && !out) || vocab == 0 || vocab >= (1u << 24))
+    return set_error(IFX_E_INVALID_ARG, "sample: bad arguments");
+  if (!(temperature > 0.f) || !isfinite(temperature) || !(top_p >= 0.f && top_p <= 1.f))
+    return set_error(IFX_E_INVALID_ARG, "sample needs temperature > 0 and 0 <= top_p <= 1");
+  hipStream_t st = nullptr;
+  float *dl = nullptr, *dp = nullptr;
+  DevState* ds = nullptr;
+  uint32_t* dt = nullptr;
+  hipError_t e = hipMalloc(&dl, (size_t)vocab * 4);
+  if (e == hipSuccess) e = hipMalloc(&dp, (size_t)vocab * 4);
+  if (e == hipSuccess) e = hipMalloc(&ds, sizeof(DevState));
+  if (e == hipSuccess) e = hipMalloc(&dt, (size_t)std::max<uint32_t>(n_draws, 1) * 4);
+  if (e == hipSuccess) e = hipMemcpy(dl, logits, (size_t)vocab * 4, hipMemcpyHostToDevice);
+  DevState init{};
+  init.out_tokens = dt;
+  init.out_cap = n_draws;
+  init.temperature = temperature;
+  init.top_k = top_k;
+  init.top_p = top_p;
+  init.seed = seed;
+  if (e == hipSuccess) e = hipMemcpy(ds, &init, sizeof init, hipMemcpyHostToDevice);
+  // draw i uses step i, as generate step i would; finalize stores it and advances
+  for (uint32_t i = 0; i < n_draws && e == hipSuccess; i++) {
+    e = launch_sample(dl, dp, vocab, ds, st);
+    if (e == hipSuccess) e = launch_finalize(ds, st);
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess && n_draws) e = hipMemcpy(out, dt, (size_t)n_draws * 4, hipMemcpyDeviceToHost);
+  for (void* p : {(void*)dl, (void*)dp, (void*)ds, (void*)dt}) if (p) (void)hipFree(p);
+  if (e != hipSuccess) return set_error(IFX_E_HIP, "sample: %s", hipGetErrorString(e));
+  for (uint32_t i = 0; i < n_draws; i++) out[i] &= 0x7fffffffu;
+  return IFX_OK;
 }
 
 int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len) {

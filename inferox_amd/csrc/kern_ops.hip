@@ -189,6 +189,12 @@ __global__ void k_state(DevState* s, StateOp op) {
     case STATE_MODE:
       s->rope_mode = op.value;
       break;
+    case STATE_SAMPLER:
+      s->temperature = op.f0;
+      s->top_k = op.value;
+      s->top_p = op.f1;
+      s->seed = op.seed;
+      break;
     case STATE_DECODE:  // decode_step at the current length
       s->cur_token = op.value;
       s->prefill = 0;

@@ -28,6 +28,11 @@ struct DevState {
   uint32_t* out_tokens;           // greedy picks (device)
   uint32_t out_cap;
   uint32_t attn_end;     // 0: attend rows [attn_lo, len]; else rows [attn_lo, attn_end)
+  // sampler (k_sample; temperature 0: the greedy argmax)
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  unsigned long long seed;
 };
 
 // ---- dequantization (kern_dequant.hip) ----
@@ -148,11 +153,18 @@ hipError_t launch_rope(float* x, uint64_t seq, uint64_t heads, uint64_t hd, uint
                        float base, uint64_t pos0, hipStream_t st);
 hipError_t launch_argmax(const float* x, uint64_t n, uint32_t* out, int* status, hipStream_t st);
 hipError_t launch_finalize(DevState* state, hipStream_t st);
-enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT, STATE_BATCH };
+enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT, STATE_BATCH,
+                            STATE_SAMPLER };
+// ---- sampling (kern_sample.hip) ----
+// Overrides state->argmax_key with a temperature / top-k / top-p draw from
+// logits[vocab] when state->temperature > 0 (probs: vocab floats of scratch).
+hipError_t launch_sample(const float* logits, float* probs, uint32_t vocab, DevState* state, hipStream_t st);
 struct StateOp {
   uint32_t kind;
   uint32_t value;
   uint32_t len;
+  float f0 = 0.f, f1 = 0.f;  // STATE_SAMPLER: temperature, top_p (value: top_k)
+  unsigned long long seed = 0;
 };
 hipError_t launch_state(DevState* state, const StateOp& op, hipStream_t st);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t st);

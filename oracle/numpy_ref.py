@@ -159,3 +159,30 @@ def forward64(weights: dict, cfg: dict, ids, causal: bool, positions=None):
     h = _rms(x, weights["output_norm.weight"], cfg["eps"])
     w_out = weights.get("output.weight", weights["token_embd.weight"])
     return h @ w_out.T
+
+
+def sampler_probs(logits, temperature: float, top_k: int, top_p: float) -> np.ndarray:
+    """Sampler::sample (src/sampler.rs:28-76) as the distribution it draws
+    from, with the maxima shifted out of exp as the device sampler does
+    (exp((z - m) / T) / sum = exp(z / T) / sum in exact arithmetic).  The list
+    is sorted by decreasing probability with ties in index order (Rust's
+    stable sort_by); top-k truncates it, top-p keeps the prefix whose running
+    sum of the whole-vocabulary probabilities first reaches top_p; the kept
+    probabilities renormalised.  float64 throughout."""
+    z = np.asarray(logits, np.float64)
+    p = np.exp((z - z.max()) / temperature)
+    p /= p.sum()
+    order = sorted(range(len(p)), key=lambda i: -p[i])  # stable: ties keep index order
+    if top_k > 0:
+        order = order[:top_k]
+    if top_p < 1.0:
+        c, cut = 0.0, len(order)
+        for pos, i in enumerate(order):
+            c += p[i]
+            if c >= top_p:
+                cut = pos + 1
+                break
+        order = order[:cut]
+    out = np.zeros_like(p)
+    out[order] = p[order]
+    return out / out.sum()

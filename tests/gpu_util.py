@@ -141,6 +141,16 @@ class GpuSession:
                                         out.ctypes.data_as(C.c_void_p))
         return rc, out[:max_tokens]
 
+    def set_sampler(self, temperature: float, top_k: int, top_p: float, seed: int):
+        check(_native.lib().ifx_session_set_sampler(self.h, temperature, top_k, top_p, seed), "set_sampler")
+
+    def generate_sampled(self, prompt, max_tokens: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(max_tokens, 1), np.uint32)
+        rc = _native.lib().ifx_generate_sampled(self.h, prompt.ctypes.data_as(C.c_void_p), prompt.size, max_tokens,
+                                                out.ctypes.data_as(C.c_void_p))
+        return rc, out[:max_tokens]
+
     def decode_greedy(self, token: int, n: int):
         out = np.zeros(max(n, 1), np.uint32)
         rc = _native.lib().ifx_decode_greedy(self.h, token, n, out.ctypes.data_as(C.c_void_p))
