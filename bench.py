@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="direct launches instead of the step graph")
+    ap.add_argument("--kv", choices=["f32", "f16"], default="f32",
+                    help="KV cache element type: f32 (the reference's cache, the parity mode) or f16 (rounded rows)")
     ap.add_argument("--copy-probe", action="store_true", help="only a d2d copy of known size (counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
@@ -245,7 +247,7 @@ def main():
     K, W = args.steps, args.warmup
     max_seq = args.ctx + max(K, W) + args.profile_steps + 8
     sess = C.c_void_p()
-    check(L.ifx_session_create(model, max_seq, C.byref(sess)), "session_create")
+    check(L.ifx_session_create_kv(model, max_seq, 1 if args.kv == "f16" else 0, C.byref(sess)), "session_create")
     vocab = spec.vocab
 
     # warmup on an empty cache (graph capture, clocks), then the real context
@@ -341,8 +343,9 @@ def main():
         "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{spec.name}-shape Q4_K_M greedy decode, bs=1, {args.ctx}-token context from a GPU "
-                               f"prefill of seeded ids, {K} tokens", "ctx": args.ctx, "decode_tokens": K,
-                   "batch": 1},
+                               f"prefill of seeded ids, {K} tokens"
+                               + (", f16 KV cache" if args.kv == "f16" else ""), "ctx": args.ctx,
+                   "decode_tokens": K, "batch": 1, "kv_cache": args.kv},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "roofline_tok": {"bytes_per_token": int(b_tok), "weight_bytes": int(w_bytes), "kv_bytes_f16": int(kv_bytes),

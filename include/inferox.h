@@ -105,6 +105,17 @@ int ifx_model_weight_bytes(const ifx_model* model, uint64_t* device_bytes, uint6
 /* KvCache::new + DecodeBuffers::new (src/model/cache.rs:16-24,62-83): a device
  * KV cache of max_seq_len rows per layer, scratch and one HIP stream. */
 int ifx_session_create(ifx_model* model, uint64_t max_seq_len, ifx_session** out);
+/* Element type of a session's KV cache. */
+enum { IFX_KV_F32 = 0, IFX_KV_F16 = 1 };
+/* ifx_session_create with the KV cache stored as kv_type.  IFX_KV_F32 is the
+ * reference's f32 KvCache (what ifx_session_create makes).  IFX_KV_F16 has no
+ * reference counterpart: keys (after RoPE) and values are rounded to IEEE
+ * binary16 (to nearest, ties to even) as they are stored, which halves the
+ * cache and the attention's HBM traffic at long contexts; attention arithmetic
+ * stays f32, so results differ from the reference by that rounding.
+ * ifx_kv_import rounds the same way, ifx_kv_export widens exactly.  Needs
+ * head_dim % 8 == 0 (IFX_E_INVALID_ARG otherwise). */
+int ifx_session_create_kv(ifx_model* model, uint64_t max_seq_len, int kv_type, ifx_session** out);
 void ifx_session_destroy(ifx_session* s);
 int ifx_session_clear(ifx_session* s);                 /* KvCache::clear (cache.rs:26-28) */
 int ifx_session_len(const ifx_session* s, uint64_t* len);  /* KvCache::len (cache.rs:31-33) */

@@ -38,6 +38,7 @@ SIGNATURES = {
     "ifx_model_config": (i32, [vp, P(IfxConfig)]),
     "ifx_model_weight_bytes": (i32, [vp, P(u64), P(u64)]),
     "ifx_session_create": (i32, [vp, u64, P(vp)]),
+    "ifx_session_create_kv": (i32, [vp, u64, i32, P(vp)]),
     "ifx_session_destroy": (None, [vp]),
     "ifx_session_clear": (i32, [vp]),
     "ifx_session_len": (i32, [vp, P(u64)]),

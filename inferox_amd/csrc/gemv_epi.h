@@ -75,8 +75,9 @@ struct EpiQkv {
       e.q_out[r] = v;
     } else {
       const uint64_t off = ((uint64_t)(r / e.head_dim) * e.max_seq + w.len) * e.head_dim + r % e.head_dim;
-      if (s == 1) e.k_cache[off] = v;
-      else e.v_cache[off] = v;
+      void* c = s == 1 ? e.k_cache : e.v_cache;
+      if (e.kv_f16) ((_Float16*)c)[off] = (_Float16)v;  // round to nearest even
+      else ((float*)c)[off] = v;
     }
   }
   __device__ void finish(Wave&, int) const {}

@@ -53,7 +53,8 @@ struct ifx_session {
   uint64_t max_seq = 0, len = 0, steps = 0;
   int rope_mode = IFX_ROPE_REFERENCE;
   hipStream_t stream = nullptr;
-  float *kc = nullptr, *vc = nullptr;
+  uint8_t *kc = nullptr, *vc = nullptr;  // [layer][kv head][max_seq][head_dim] of kv_es-byte elements
+  uint32_t kv_es = 4;                    // 4: f32 (IFX_KV_F32), 2: binary16 (IFX_KV_F16)
   float *hidden = nullptr, *q = nullptr, *attn = nullptr, *mid = nullptr, *logits = nullptr;
   float* partial = nullptr;
   float2* rope_cs = nullptr;
@@ -220,8 +221,9 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       break;
   }
   const LayerDev& L = m->layers[l];
-  float* kc = s->kc + l * s->max_seq * kvd;
-  float* vc = s->vc + l * s->max_seq * kvd;
+  void* kc = s->kc + l * s->max_seq * kvd * s->kv_es;
+  void* vc = s->vc + l * s->max_seq * kvd * s->kv_es;
+  const uint32_t kv16 = s->kv_es == 2;
   switch (k) {
     case 1: {
       GemvLaunch g;
@@ -234,14 +236,14 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       g.norm_w = L.attn_norm;
       g.eps = c.norm_eps;
       QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd,
-               (uint32_t)s->max_seq};
+               (uint32_t)s->max_seq, kv16};
       IFX_HIP(gemv_qkv(g, e, st));
       return IFX_OK;
     }
     case 2: {
       AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
-                 (uint32_t)s->max_seq};
+                 (uint32_t)s->max_seq, kv16};
       IFX_HIP(launch_attn_decode(a, st));
       return IFX_OK;
     }
@@ -395,16 +397,17 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
   IFX_HIP(launch_embed_rows(devw(m->embd), s->feed_ids, n, w.x, st));
   for (size_t l = 0; l < m->layers.size(); l++) {
     const LayerDev& L = m->layers[l];
-    float* kc = s->kc + l * s->max_seq * kvd;
-    float* vc = s->vc + l * s->max_seq * kvd;
+    void* kc = s->kc + l * s->max_seq * kvd * s->kv_es;
+    void* vc = s->vc + l * s->max_seq * kvd * s->kv_es;
+    const bool kv16 = s->kv_es == 2;
     const GemmIn in = op(N, D);
     IFX_HIP(launch_prep_rows(w.x, N, D, D, L.attn_norm, c.norm_eps, in, st));
     const uint64_t kv_hs = s->max_seq * hd;  // head stride of the head-major cache
     IFX_HIP(gemm_rope(in, gw(L.q), w.q, D, hd, 0, pos0, hd, rd, s->rope_cs, st));
-    IFX_HIP(gemm_rope(in, gw(L.k), kc, hd, kv_hs, row0, pos0, hd, rd, s->rope_cs, st));
-    IFX_HIP(gemm_rows(in, gw(L.v), vc, hd, kv_hs, row0, hd, st));
+    IFX_HIP(gemm_rope(in, gw(L.k), kc, hd, kv_hs, row0, pos0, hd, rd, s->rope_cs, st, kv16));
+    IFX_HIP(gemm_rows(in, gw(L.v), vc, hd, kv_hs, row0, hd, st, kv16));
     const AttnPrefillArgs aa{w.q, kc, vc, w.att, N, row0, (uint32_t)c.n_heads, (uint32_t)c.n_kv_heads, hd,
-                             (uint32_t)s->max_seq, causal, w.kv_split};
+                             (uint32_t)s->max_seq, causal, w.kv_split, kv16};
     IFX_HIP(launch_attn_prefill(aa, st));
     IFX_HIP(launch_prep_rows(w.att, N, D, D, nullptr, 0.f, in, st));
     IFX_HIP(gemm_residual(in, gw(L.o), w.x, D, st));
@@ -592,22 +595,30 @@ int ifx_model_weight_bytes(const ifx_model* m, uint64_t* dev, uint64_t* gguf) {
 }
 
 int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
+  return ifx_session_create_kv(m, max_seq_len, IFX_KV_F32, out);
+}
+
+int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_session** out) {
   clear_error();
-  if (!m || !out || max_seq_len == 0 || max_seq_len > 0x7fffffffull)
+  if (!m || !out || max_seq_len == 0 || max_seq_len > 0x7fffffffull || (kv_type != IFX_KV_F32 && kv_type != IFX_KV_F16))
     return set_error(IFX_E_INVALID_ARG, "bad session arguments");
   *out = nullptr;
   IFX_TRY(check_dims(m));
   const ifx_config& c = m->cfg;
+  if (!attn_decode_head_dim((uint32_t)c.head_dim, kv_type == IFX_KV_F16))
+    return set_error(IFX_E_INVALID_ARG, "head_dim %llu has no %s-cache attention", (unsigned long long)c.head_dim,
+                     kv_type == IFX_KV_F16 ? "f16" : "f32");
   ifx_session* s = new ifx_session();
   s->m = m;
   s->max_seq = max_seq_len;
+  s->kv_es = kv_type == IFX_KV_F16 ? 2 : 4;
   const uint64_t D = c.hidden_size, F = c.intermediate_size, kvd = c.n_kv_heads * c.head_dim;
   const uint64_t G = c.n_heads / c.n_kv_heads;
   s->max_chunks = (uint32_t)((max_seq_len + s->attn_chunk - 1) / s->attn_chunk);
   int rc = IFX_OK;
   auto A = [&](void** p, size_t b) { if (rc == IFX_OK) rc = dev_alloc(s->allocs, p, b); };
-  A((void**)&s->kc, c.n_layers * max_seq_len * kvd * 4);
-  A((void**)&s->vc, c.n_layers * max_seq_len * kvd * 4);
+  A((void**)&s->kc, c.n_layers * max_seq_len * kvd * s->kv_es);
+  A((void**)&s->vc, c.n_layers * max_seq_len * kvd * s->kv_es);
   A((void**)&s->hidden, D * 4);
   A((void**)&s->q, D * 4);
   A((void**)&s->attn, D * 4);
@@ -645,8 +656,8 @@ int ifx_session_create(ifx_model* m, uint64_t max_seq_len, ifx_session** out) {
   init.top_p = 1.0f;
   if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
-      hipMemset(s->vc, 0, c.n_layers * max_seq_len * kvd * 4) != hipSuccess ||
+      hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * s->kv_es) != hipSuccess ||
+      hipMemset(s->vc, 0, c.n_layers * max_seq_len * kvd * s->kv_es) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     session_free(s);
     return set_error(IFX_E_HIP, "session initialisation failed");
@@ -865,17 +876,66 @@ int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, ui
   return IFX_OK;
 }
 
+// IEEE binary16 <-> binary32 for the f16 KV cache's import and export:
+// round to nearest, ties to even; overflow to infinity; NaN stays NaN.
+static uint16_t f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // >= 65520 rounds past 65504
+  if (ax < 0x38800000u) {                                     // below 2^-14: subnormal or zero
+    if (ax <= 0x33000000u) return (uint16_t)sign;             // <= 2^-25 (the tie goes to 0)
+    const uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u, r = 126 - e;  // units of 2^-24
+    uint32_t q = m >> r;
+    const uint32_t rem = m & ((1u << r) - 1), half = 1u << (r - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t h = (ax - 0x38000000u) >> 13;  // exponent rebiased 127 -> 15, 10 mantissa bits
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+static float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+  float f;
+  if (e == 0) {
+    f = ldexpf((float)m, -24);
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    x |= sign;
+    memcpy(&f, &x, 4);
+    return f;
+  }
+  const uint32_t x = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+  memcpy(&f, &x, 4);
+  return f;
+}
+
 int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len) {
   if (!s || (len && (!k || !v))) return set_error(IFX_E_INVALID_ARG, "null argument");
   if (len > s->max_seq) return set_error(IFX_E_KV_FULL, "import of %llu rows", (unsigned long long)len);
   const ifx_config& c = s->m->cfg;
-  const uint64_t kvd = c.n_kv_heads * c.head_dim, hd = c.head_dim;
+  const uint64_t kvd = c.n_kv_heads * c.head_dim, hd = c.head_dim, es = s->kv_es;
   // reference rows [t][kv_dim] -> the head-major device cache, one strided copy per (layer, head)
+  // (an f16 cache: one rounded head block at a time)
+  std::vector<uint16_t> blk(s->kv_es == 2 ? len * hd : 0);
+  if (es == 2) IFX_HIP(hipStreamSynchronize(s->stream));  // the blocking copies below bypass the stream
   for (uint64_t l = 0; l < c.n_layers && len; l++)
     for (uint64_t h = 0; h < c.n_kv_heads; h++) {
-      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd, host = l * len * kvd + h * hd;
-      IFX_HIP(hipMemcpy2DAsync(s->kc + dev, hd * 4, k + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
-      IFX_HIP(hipMemcpy2DAsync(s->vc + dev, hd * 4, v + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
+      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd * es, host = l * len * kvd + h * hd;
+      if (es == 4) {
+        IFX_HIP(hipMemcpy2DAsync(s->kc + dev, hd * 4, k + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
+        IFX_HIP(hipMemcpy2DAsync(s->vc + dev, hd * 4, v + host, kvd * 4, hd * 4, len, hipMemcpyHostToDevice, s->stream));
+        continue;
+      }
+      for (int which = 0; which < 2; which++) {
+        const float* src = (which ? v : k) + host;
+        for (uint64_t t = 0; t < len; t++)
+          for (uint64_t d = 0; d < hd; d++) blk[t * hd + d] = f32_to_f16(src[t * kvd + d]);
+        IFX_HIP(hipMemcpy((which ? s->vc : s->kc) + dev, blk.data(), len * hd * 2, hipMemcpyHostToDevice));
+      }
     }
   IFX_TRY(state_op(s, STATE_RESET, 0, (uint32_t)len));
   IFX_HIP(hipStreamSynchronize(s->stream));
@@ -889,13 +949,23 @@ int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len) {
   if (len > s->len) return set_error(IFX_E_INVALID_ARG, "export of %llu rows, %llu cached", (unsigned long long)len, (unsigned long long)s->len);
   const ifx_config& c = s->m->cfg;
   const uint64_t kvd = c.n_kv_heads * c.head_dim;
-  const uint64_t hd = c.head_dim;
+  const uint64_t hd = c.head_dim, es = s->kv_es;
   IFX_HIP(hipStreamSynchronize(s->stream));
+  std::vector<uint16_t> blk(s->kv_es == 2 ? len * hd : 0);
   for (uint64_t l = 0; l < c.n_layers && len; l++)
     for (uint64_t h = 0; h < c.n_kv_heads; h++) {
-      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd, host = l * len * kvd + h * hd;
-      IFX_HIP(hipMemcpy2D(k + host, kvd * 4, s->kc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
-      IFX_HIP(hipMemcpy2D(v + host, kvd * 4, s->vc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
+      const uint64_t dev = (l * c.n_kv_heads + h) * s->max_seq * hd * es, host = l * len * kvd + h * hd;
+      if (es == 4) {
+        IFX_HIP(hipMemcpy2D(k + host, kvd * 4, s->kc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
+        IFX_HIP(hipMemcpy2D(v + host, kvd * 4, s->vc + dev, hd * 4, hd * 4, len, hipMemcpyDeviceToHost));
+        continue;
+      }
+      for (int which = 0; which < 2; which++) {
+        IFX_HIP(hipMemcpy(blk.data(), (which ? s->vc : s->kc) + dev, len * hd * 2, hipMemcpyDeviceToHost));
+        float* dst = (which ? v : k) + host;
+        for (uint64_t t = 0; t < len; t++)
+          for (uint64_t d = 0; d < hd; d++) dst[t * kvd + d] = f16_to_f32(blk[t * hd + d]);
+      }
     }
   return IFX_OK;
 }
@@ -946,9 +1016,9 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   const LayerDev& L0 = m->layers.empty() ? LayerDev{} : m->layers[0];
   bytes[0] = 0;
   bytes[1] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.q) + tensor_stream_bytes(L0.k) + tensor_stream_bytes(L0.v);
-  // attention streams the f32 K and V rows it attends (the state after the steps)
+  // attention streams the K and V rows it attends (the state after the steps)
   const uint64_t kvd = m->cfg.n_kv_heads * m->cfg.head_dim;
-  bytes[2] = 2 * (len0 + n_steps) * kvd * 4;
+  bytes[2] = 2 * (len0 + n_steps) * kvd * s->kv_es;
   bytes[3] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.o);
   bytes[4] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.gate) + tensor_stream_bytes(L0.up);
   bytes[5] = m->layers.empty() ? 0 : tensor_stream_bytes(L0.down);
@@ -1010,22 +1080,23 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
   }
   for (size_t l = 0; l < m->layers.size() && rc == IFX_OK; l++) {
     const LayerDev& L = m->layers[l];
-    float* kc = s->kc + l * s->max_seq * kvd;
-    float* vc = s->vc + l * s->max_seq * kvd;
+    void* kc = s->kc + l * s->max_seq * kvd * s->kv_es;
+    void* vc = s->vc + l * s->max_seq * kvd * s->kv_es;
+    const uint32_t kv16 = s->kv_es == 2;
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
       hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
       GemvLaunch g;
       g.seg[0] = seg_of(L.q); g.seg[1] = seg_of(L.k); g.seg[2] = seg_of(L.v);
       g.nseg = 3; g.cols = (uint32_t)D; g.x = X + t * D; g.norm_w = L.attn_norm; g.eps = c.norm_eps;
       QkvEpi e{Q + t * D, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, (uint32_t)kvd,
-               (uint32_t)s->max_seq};
+               (uint32_t)s->max_seq, kv16};
       hip(gemv_qkv(g, e, st));
     }
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
       hip(launch_state(s->state, StateOp{STATE_TOKEN_AT, (uint32_t)t, (uint32_t)n}, st));
       AttnArgs a{Q + t * D, kc, vc, A + t * D, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
-                 (uint32_t)s->max_seq};
+                 (uint32_t)s->max_seq, kv16};
       hip(launch_attn_decode(a, st));
     }
     for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {

@@ -6,14 +6,20 @@
 //
 // Grid = (chunk index, kv head).  A workgroup handles one kv head and kChunk
 // cache rows for all `group` query heads that share it, so each K/V row is read
-// from HBM once per token.  All K and V loads of the chunk are issued before the
-// first wait, so a workgroup costs one memory round trip.  It writes a partial
+// from HBM once per token.  The q, K and V loads of the chunk are all issued
+// before the first wait (q, then K, then V: the scores start while V is still
+// arriving), so a workgroup costs one memory round trip.  It writes a partial
 // record (unnormalised o, running max, sum) for its chunk.  A second launch,
 // one workgroup per query head, merges the records with the usual
 // max-rescaling (a kernel boundary publishes them: no counters or fences,
 // which cost more than the launch on this part).
 // The cache rows attended are [attn_lo, len] (or [attn_lo, attn_end)), read
-// from the session state, so the launch is identical for every token.
+// from the session state, so the launch is identical for every token.  The
+// cache holds f32 (the reference's KvCache) or, in an f16-KV session,
+// binary16 elements (E = _Float16), widened to f32 as they are loaded; all
+// arithmetic is f32 either way.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace ifx {
@@ -36,6 +42,31 @@ __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
 }
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // 16 raw bytes, kept in registers
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// two adjacent V elements as loaded (f32 pair, or an f16 pair in one dword)
+template <typename E>
+using VPair = typename std::conditional<sizeof(E) == 4, float2, uint32_t>::type;
+__device__ __forceinline__ float2 widen(float2 v) { return v; }
+__device__ __forceinline__ float2 widen(uint32_t u) {
+  const h2 h = __builtin_bit_cast(h2, u);
+  return make_float2((float)h[0], (float)h[1]);
+}
+// elements 4j .. 4j + 3 of a 16-byte K chunk
+template <typename E>
+__device__ __forceinline__ float4 chunk4(u4 raw, int j) {
+  if constexpr (sizeof(E) == 4) {
+    const f4v f = __builtin_bit_cast(f4v, raw);
+    return make_float4(f[0], f[1], f[2], f[3]);
+  } else {
+    const h8 h = __builtin_bit_cast(h8, raw);
+    return make_float4((float)h[4 * j], (float)h[4 * j + 1], (float)h[4 * j + 2], (float)h[4 * j + 3]);
+  }
 }
 
 // ---- wave reductions on the DPP network (no LDS round trips) ----
@@ -76,23 +107,35 @@ __device__ __forceinline__ float quad_sum(float v) {
 
 constexpr int kRowsPerWave = kChunk / (kThreads / 64);  // 16
 
+// Cache rows [lo, hi) the current token attends to.  The three fields are read
+// unconditionally, so that they come in one memory round trip (a conditional
+// read of len would be a second one).
+__device__ __forceinline__ void attended_rows(const DevState* st, uint32_t& lo, uint32_t& hi) {
+  const uint32_t len = st->len, attn_lo = st->attn_lo, attn_end = st->attn_end;
+  lo = attn_lo;
+  hi = attn_end ? attn_end : len + 1;
+}
+
 // HDT: the head dim when > 0 (register arrays sized exactly), 0 for any
-// multiple of 4 up to kMaxHd.  GT: the query heads per kv head when > 0, 0 for
-// any up to kMaxGroup.  With both fixed the unrolled loops carry no branches.
+// multiple of 16 / sizeof(E) up to kMaxHd.  GT: the query heads per kv head
+// when > 0, 0 for any up to kMaxGroup.  With both fixed the unrolled loops
+// carry no branches.
 //
 // Each wave owns 16 cache rows of the chunk end to end:
-//   scores  lane = (row l/4, quarter l%4): the quarter's float4 columns
+//   scores  lane = (row l/4, quarter l%4): the quarter's 16-byte K chunks
 //           ch = l%4 + 4i, q from LDS, a quad reduction on the DPP network;
 //   softmax max / sum over the wave's rows on the DPP network;
 //   p . V   lane = columns 2l, 2l+1 (+128 j) of all 16 rows, the row weights
 //           broadcast with readlane: no cross-lane reduction.
 // The four waves are combined once through LDS into the chunk's record.
-template <int HDT, int GT>
+template <int HDT, int GT, typename E>
 __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
+  constexpr int EPC = 16 / (int)sizeof(E);     // cache elements per 16-byte K chunk
   constexpr int GM = GT > 0 ? GT : kMaxGroup;  // loop bound over query heads
-  constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;      // float4 per head row
-  constexpr int KPT = (NC4M + 3) / 4;                      // K float4 per lane
+  constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;      // float4 of q per head row
+  constexpr int KPT = (NC4M * 4 / EPC + 3) / 4;            // K chunks per lane
   constexpr int VJ = ((HDT > 0 ? HDT : kMaxHd) + 127) / 128;  // column pairs per lane
+  constexpr int QPT = (GM * NC4M + kThreads - 1) / kThreads;  // q float4 per thread
   __shared__ float4 qs[GM * NC4M];
   __shared__ float wst[kThreads / 64][2][GM];                      // per wave: max, sum
   __shared__ float2 wo[kThreads / 64][GM][NC4M * 2];               // per wave: unnormalised o
@@ -100,9 +143,9 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
 
   const uint32_t c = blockIdx.x, hk = blockIdx.y;
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
-  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
-  const uint32_t lo = a.state->attn_lo;
-  const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4, nck = HD / EPC;
+  uint32_t lo, hi;
+  attended_rows(a.state, lo, hi);
   const uint32_t nrows = hi > lo ? hi - lo : 0;
   const uint32_t nch = (nrows + kChunk - 1) / kChunk;
   if (c >= nch) return;
@@ -113,31 +156,44 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
   // rows past the chunk's end read the last real row (weight 0)
   auto cache_row = [&](uint32_t r) -> uint64_t { return ((uint64_t)hk * a.max_seq + t0 + min(r, n - 1)) * HD; };
 
-  // ---- K, V and q loads, all in flight together ----
-  const uint32_t kr_row = r0 + lane / 4, kq = lane & 3;
-  float4 kr[KPT];
+  // ---- q, K and V loads, all in flight together (in this order: the loads
+  // complete in issue order, so the q copy to LDS waits for q alone and the
+  // scores for q and K) ----
+  float4 qr[QPT];
   {
-    const float4* k4 = (const float4*)(a.k_cache + cache_row(kr_row));
+    const float4* q4 = (const float4*)(a.q + (uint64_t)hk * G * HD);
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+      const uint32_t at = tid + kThreads * i;
+      qr[i] = at < G * nc4 ? q4[at] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const uint32_t kr_row = r0 + lane / 4, kq = lane & 3;
+  u4 kr[KPT];
+  {
+    const E* krow = (const E*)a.k_cache + cache_row(kr_row);
 #pragma unroll
     for (int i = 0; i < KPT; i++) {
       const uint32_t ch = kq + 4 * i;
-      kr[i] = ch < nc4 ? k4[ch] : make_float4(0.f, 0.f, 0.f, 0.f);
+      kr[i] = ch < nck ? *(const u4*)(krow + EPC * ch) : u4{0u, 0u, 0u, 0u};
     }
   }
-  float2 vr[kRowsPerWave][VJ];
+  __builtin_amdgcn_sched_barrier(0);  // every K load issues before the first V load
+  VPair<E> vr[kRowsPerWave][VJ];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; r++) {
-    const float* vrow = a.v_cache + cache_row(r0 + r);
+    const E* vrow = (const E*)a.v_cache + cache_row(r0 + r);
 #pragma unroll
     for (int jj = 0; jj < VJ; jj++) {
       const uint32_t col = 2 * lane + 128 * jj;
-      vr[r][jj] = col < HD ? *(const float2*)(vrow + col) : make_float2(0.f, 0.f);
+      vr[r][jj] = col < HD ? *(const VPair<E>*)(vrow + col) : VPair<E>{};
     }
   }
-  for (uint32_t i = tid; i < G * nc4; i += kThreads) qs[i] = ((const float4*)(a.q + (uint64_t)hk * G * HD))[i];
-  // the compiler may issue the q load first and wait for it alone; waiting
-  // for everything here keeps K, V and q in one memory round trip
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < QPT; i++) {
+    const uint32_t at = tid + kThreads * i;
+    if (at < G * nc4) qs[at] = qr[i];
+  }
   __syncthreads();
 
   // ---- scores (src/model/forward.rs:388-397) and the wave's softmax statistics
@@ -154,18 +210,22 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < KPT; i++) {
     const uint32_t ch = kq + 4 * i;
-    if (ch < nc4) {
-      float4 qv[GM];
+    if (ch < nck) {
 #pragma unroll
-      for (int g = 0; g < GM; g++)
-        if (g < (int)G) qv[g] = qs[g * nc4 + ch];
+      for (int j = 0; j < EPC / 4; j++) {
+        const float4 kv = chunk4<E>(kr[i], j);
+        float4 qv[GM];
 #pragma unroll
-      for (int g = 0; g < GM; g++) {
-        if (g < (int)G) {
-          sg[g] = fmaf(qv[g].x, kr[i].x, sg[g]);
-          sg[g] = fmaf(qv[g].y, kr[i].y, sg[g]);
-          sg[g] = fmaf(qv[g].z, kr[i].z, sg[g]);
-          sg[g] = fmaf(qv[g].w, kr[i].w, sg[g]);
+        for (int g = 0; g < GM; g++)
+          if (g < (int)G) qv[g] = qs[g * nc4 + (EPC / 4) * ch + j];
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+          if (g < (int)G) {
+            sg[g] = fmaf(qv[g].x, kv.x, sg[g]);
+            sg[g] = fmaf(qv[g].y, kv.y, sg[g]);
+            sg[g] = fmaf(qv[g].z, kv.z, sg[g]);
+            sg[g] = fmaf(qv[g].w, kv.w, sg[g]);
+          }
         }
       }
     }
@@ -201,13 +261,16 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
     float e[GM];
 #pragma unroll
     for (int g = 0; g < GM; g++) e[g] = es[wave][r][g];
+    float2 v[VJ];
+#pragma unroll
+    for (int jj = 0; jj < VJ; jj++) v[jj] = widen(vr[r][jj]);
 #pragma unroll
     for (int g = 0; g < GM; g++) {
       if (g < (int)G) {
 #pragma unroll
         for (int jj = 0; jj < VJ; jj++) {
-          o[g][jj].x = fmaf(e[g], vr[r][jj].x, o[g][jj].x);
-          o[g][jj].y = fmaf(e[g], vr[r][jj].y, o[g][jj].y);
+          o[g][jj].x = fmaf(e[g], v[jj].x, o[g][jj].x);
+          o[g][jj].y = fmaf(e[g], v[jj].y, o[g][jj].y);
         }
       }
     }
@@ -273,8 +336,8 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
   const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
   const uint32_t h = blockIdx.x, hk = h / G, g = h % G;
-  const uint32_t lo = a.state->attn_lo;
-  const uint32_t hi = a.state->attn_end ? a.state->attn_end : a.state->len + 1;
+  uint32_t lo, hi;
+  attended_rows(a.state, lo, hi);
   const uint32_t nrows = hi > lo ? hi - lo : 0;
   const uint32_t nch = (nrows + kChunk - 1) / kChunk;
   if (nch == 0) return;
@@ -342,18 +405,13 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
-  if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > kMaxGroup ||
-      a.head_dim == 0 || a.head_dim > kMaxHd || a.head_dim % 4 || a.chunk != kChunk || a.max_chunks > kMaxMerge ||
-      a.max_chunks == 0)
-    return hipErrorInvalidValue;
+template <typename E>
+void launch_typed(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.max_chunks, a.n_kv_heads);
   const uint32_t G = a.n_heads / a.n_kv_heads;
 #define IFX_ATTN(HD_, G_)                                                                          \
   do {                                                                                             \
-    hipLaunchKernelGGL((k_attn_decode<HD_, G_>), grid, dim3(kThreads), 0, st, a);                 \
+    hipLaunchKernelGGL((k_attn_decode<HD_, G_, E>), grid, dim3(kThreads), 0, st, a);              \
     hipLaunchKernelGGL((k_attn_merge<HD_, G_>), dim3(a.n_heads), dim3(kThreads), 0, st, a);       \
   } while (0)
   if (a.head_dim == 128 && G == 4) IFX_ATTN(128, 4);        // Llama-3 8B
@@ -363,6 +421,21 @@ hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
   else if (a.head_dim == 64 && G == 1) IFX_ATTN(64, 1);
   else IFX_ATTN(0, 0);
 #undef IFX_ATTN
+}
+
+}  // namespace
+
+bool attn_decode_head_dim(uint32_t head_dim, bool kv_f16) {
+  return head_dim > 0 && head_dim <= kMaxHd && head_dim % (kv_f16 ? 8 : 4) == 0;
+}
+
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
+  if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > kMaxGroup ||
+      !attn_decode_head_dim(a.head_dim, a.kv_f16) || a.chunk != kChunk || a.max_chunks > kMaxMerge ||
+      a.max_chunks == 0)
+    return hipErrorInvalidValue;
+  if (a.kv_f16) launch_typed<_Float16>(a, st);
+  else launch_typed<float>(a, st);
   return hipGetLastError();
 }
 

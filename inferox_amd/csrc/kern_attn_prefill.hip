@@ -106,10 +106,33 @@ __device__ __forceinline__ int swz(int r, int c) {
 // distinct banks (16 lanes over 64 banks; 8-lane groups see 8 distinct chunks)
 __device__ __forceinline__ int swzv(int r, int c) { return r * kKB + 8 * (c ^ ((r ^ (r >> 3)) & 7)); }
 
+// Cache elements (E = float, or _Float16 for the f16 KV cache) as floats.
+template <typename E>
+__device__ __forceinline__ void load8(const E* p, float* v) {
+  if constexpr (sizeof(E) == 4) {
+    const float4 x0 = *(const float4*)p, x1 = *(const float4*)(p + 4);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  } else {
+    const h8 x = *(const h8*)p;
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = (float)x[k];
+  }
+}
+template <typename E>
+__device__ __forceinline__ float4 load4(const E* p) {
+  if constexpr (sizeof(E) == 4) {
+    return *(const float4*)p;
+  } else {
+    const h4 x = *(const h4*)p;
+    return make_float4((float)x[0], (float)x[1], (float)x[2], (float)x[3]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // K/V preparation: grid (key block, kv head).
 // ---------------------------------------------------------------------------
-template <int HD>
+template <int HD, typename E>
 __global__ void __launch_bounds__(kPrepThreads) k_kv_prep(AttnPrefillArgs a, PrepWs w) {
   using D = Dims<HD>;
   constexpr int HP = D::HP, CPT = D::NCH / 4;  // K: four threads per key row
@@ -118,8 +141,8 @@ __global__ void __launch_bounds__(kPrepThreads) k_kv_prep(AttnPrefillArgs a, Pre
   const uint32_t b = blockIdx.x, hk = blockIdx.y, k0 = b * kKB;
   const uint32_t nkb = gridDim.x, npad = nkb * kKB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* kbase = a.k_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
-  const float* vbase = a.v_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
+  const E* kbase = (const E*)a.k_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
+  const E* vbase = (const E*)a.v_cache + ((uint64_t)hk * a.max_seq + a.row0) * HD;
 
   // K: row kr, chunks qq * CPT .. + CPT - 1; the row scale from the four threads' maxima
   {
@@ -132,12 +155,7 @@ __global__ void __launch_bounds__(kPrepThreads) k_kv_prep(AttnPrefillArgs a, Pre
       const int col = 8 * (qq * CPT + i);
 #pragma unroll
       for (int k = 0; k < 8; k++) v[i][k] = 0.f;
-      if (key < a.n && col < HD) {
-        const float4 x0 = *(const float4*)(kbase + (uint64_t)key * HD + col);
-        const float4 x1 = *(const float4*)(kbase + (uint64_t)key * HD + col + 4);
-        v[i][0] = x0.x; v[i][1] = x0.y; v[i][2] = x0.z; v[i][3] = x0.w;
-        v[i][4] = x1.x; v[i][5] = x1.y; v[i][6] = x1.z; v[i][7] = x1.w;
-      }
+      if (key < a.n && col < HD) load8(kbase + (uint64_t)key * HD + col, v[i]);
 #pragma unroll
       for (int k = 0; k < 8; k++) mx = fmaxf(mx, fabsf(v[i][k]));
     }
@@ -168,7 +186,7 @@ __global__ void __launch_bounds__(kPrepThreads) k_kv_prep(AttnPrefillArgs a, Pre
     const int r = c / (HD / 4), col = 4 * (c % (HD / 4));
     const uint32_t key = k0 + (uint32_t)r;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (key < a.n) x = *(const float4*)(vbase + (uint64_t)key * HD + col);
+    if (key < a.n) x = load4(vbase + (uint64_t)key * HD + col);
     vblk[r][col] = x.x;
     vblk[r][col + 1] = x.y;
     vblk[r][col + 2] = x.z;
@@ -404,7 +422,8 @@ hipError_t go(const AttnPrefillArgs& a, hipStream_t st) {
   using D = Dims<HD>;
   const PrepWs w = prep_ws(a.ws, a.n, a.n_kv_heads, D::HP);
   const uint32_t nkb = (a.n + kKB - 1) / kKB;
-  hipLaunchKernelGGL(k_kv_prep<HD>, dim3(nkb, a.n_kv_heads), dim3(kPrepThreads), 0, st, a, w);
+  if (a.kv_f16) hipLaunchKernelGGL((k_kv_prep<HD, _Float16>), dim3(nkb, a.n_kv_heads), dim3(kPrepThreads), 0, st, a, w);
+  else hipLaunchKernelGGL((k_kv_prep<HD, float>), dim3(nkb, a.n_kv_heads), dim3(kPrepThreads), 0, st, a, w);
   const dim3 grid(((a.n + kQ - 1) / kQ) * a.n_heads);
   hipLaunchKernelGGL(k_attn_prefill<HD>, grid, dim3(kThreads), 0, st, a, w);
   return hipGetLastError();

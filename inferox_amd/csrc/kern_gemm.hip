@@ -307,11 +307,18 @@ __device__ __forceinline__ uint64_t head_addr(uint32_t t, uint32_t n, uint32_t r
 
 // RoPE on adjacent pairs (src/ops.rs:273-284) at position pos0 + t; `partner`
 // is column n ^ 1 of the same token.
+// y_f16: y holds binary16 (the f16 KV cache), rounded to nearest even.
+__device__ __forceinline__ void store_y(void* y, bool f16, uint64_t i, float v) {
+  if (f16) ((_Float16*)y)[i] = (_Float16)v;
+  else ((float*)y)[i] = v;
+}
+
 struct EpRope {
-  float* y;
+  void* y;
   uint64_t hstride;
   uint32_t ld, row0, pos0, head_dim, rope_dim, half;
   const float2* cs;  // [pos][rope_dim / 2]
+  bool y_f16;
   __device__ void operator()(uint32_t t, uint32_t n, float v, float partner) const {
     const uint32_t c = n % head_dim;
     float out = v;
@@ -319,16 +326,17 @@ struct EpRope {
       const float2 r = cs[(uint64_t)(pos0 + t) * half + (c >> 1)];
       out = (c & 1u) ? (partner * r.y) + (v * r.x) : (v * r.x) - (partner * r.y);
     }
-    y[head_addr(t, n, row0, ld, hstride, head_dim)] = out;
+    store_y(y, y_f16, head_addr(t, n, row0, ld, hstride, head_dim), out);
   }
 };
 
 struct EpRows {  // the V cache append
-  float* y;
+  void* y;
   uint64_t hstride;
   uint32_t ld, row0, head_dim;
+  bool y_f16;
   __device__ void operator()(uint32_t t, uint32_t n, float v, float) const {
-    y[head_addr(t, n, row0, ld, hstride, head_dim)] = v;
+    store_y(y, y_f16, head_addr(t, n, row0, ld, hstride, head_dim), v);
   }
 };
 
@@ -760,17 +768,18 @@ hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ld
   return dispatch(args_of(in, w, false), EpResid{x, ldx}, st);
 }
 
-hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
-                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st) {
+hipError_t gemm_rope(const GemmIn& in, const GemmW& w, void* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st,
+                     bool y_f16) {
   if (head_dim == 0 || head_dim % 2 || rope_dim % 2 || rope_dim > head_dim) return hipErrorInvalidValue;
-  return dispatch(args_of(in, w, false), EpRope{y, hstride, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs},
-                  st);
+  return dispatch(args_of(in, w, false),
+                  EpRope{y, hstride, ldy, row0, pos0, head_dim, rope_dim, rope_dim / 2, cs, y_f16}, st);
 }
 
-hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
-                     uint32_t head_dim, hipStream_t st) {
+hipError_t gemm_rows(const GemmIn& in, const GemmW& w, void* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t head_dim, hipStream_t st, bool y_f16) {
   if (head_dim == 0) return hipErrorInvalidValue;
-  return dispatch(args_of(in, w, false), EpRows{y, hstride, ldy, row0, head_dim}, st);
+  return dispatch(args_of(in, w, false), EpRows{y, hstride, ldy, row0, head_dim, y_f16}, st);
 }
 
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,

@@ -63,15 +63,17 @@ struct GemvLaunch {
 };
 
 // The device KV cache is head-major: per layer [n_kv_heads][max_seq][head_dim]
-// f32, so a kv head's rows are contiguous for the attention kernels (the
-// reference's [t][kv_dim] row order is what ifx_kv_import/export exchange).
+// f32 (or binary16 in a session created with IFX_KV_F16), so a kv head's rows
+// are contiguous for the attention kernels (the reference's [t][kv_dim] row
+// order is what ifx_kv_import/export exchange).
 struct QkvEpi {
   float* q_out;          // [q rows]
-  float* k_cache;        // layer base, [n_kv_heads][max_seq][head_dim]
-  float* v_cache;
+  void* k_cache;         // layer base, [n_kv_heads][max_seq][head_dim] f32, or f16 when kv_f16
+  void* v_cache;
   const float2* rope_cs; // [max_pos][rope_dim/2] (cos, sin)
   const DevState* state;
   uint32_t head_dim, rope_dim, kv_dim, max_seq;
+  uint32_t kv_f16;
 };
 
 hipError_t gemv_store(const GemvLaunch& L, float* y, hipStream_t st);
@@ -110,12 +112,14 @@ hipError_t gemm_residual(const GemmIn& in, const GemmW& w, float* x, uint32_t ld
 // Output (t, n) of the q/k/v GEMMs goes to y[(row0 + t) ldy + (n / head_dim) hstride + n % head_dim]:
 // row-major [t][heads * head_dim] with ldy = heads * head_dim, hstride = head_dim;
 // the head-major KV cache with ldy = head_dim, hstride = max_seq * head_dim.
+// y is f32, or binary16 (rounded to nearest even) when y_f16.
 // RoPE at position pos0 + t
-hipError_t gemm_rope(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
-                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st);
+hipError_t gemm_rope(const GemmIn& in, const GemmW& w, void* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t pos0, uint32_t head_dim, uint32_t rope_dim, const float2* cs, hipStream_t st,
+                     bool y_f16 = false);
 // the V cache append
-hipError_t gemm_rows(const GemmIn& in, const GemmW& w, float* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
-                     uint32_t head_dim, hipStream_t st);
+hipError_t gemm_rows(const GemmIn& in, const GemmW& w, void* y, uint32_t ldy, uint64_t hstride, uint32_t row0,
+                     uint32_t head_dim, hipStream_t st, bool y_f16 = false);
 // mid[t * ld + n] = swiglu(gate row n . A[t], up row n . A[t])
 hipError_t gemm_swiglu(const GemmIn& in, const GemmW& gate, const GemmW& up, float* mid, uint32_t ld,
                        hipStream_t st);
@@ -130,12 +134,13 @@ hipError_t launch_prep_rows(const float* x, uint32_t rows, uint32_t ld, uint32_t
 // (causal) or row0 .. row0 + n - 1; out[t] f32, the row's max |out| in rowmax.
 struct AttnPrefillArgs {
   const float* q;        // [n][n_heads * head_dim]
-  const float* k_cache;  // layer base [n_kv_heads][max_seq][head_dim]
-  const float* v_cache;
+  const void* k_cache;   // layer base [n_kv_heads][max_seq][head_dim], f32 or (kv_f16) f16
+  const void* v_cache;
   float* out;            // [n][n_heads * head_dim]
   uint32_t n, row0, n_heads, n_kv_heads, head_dim, max_seq;
   bool causal;
   void* ws;              // attn_prefill_ws_bytes(n, n_kv_heads, head_dim): the split K/V
+  bool kv_f16;
 };
 bool attn_prefill_head_dim(uint32_t head_dim);
 uint64_t attn_prefill_ws_bytes(uint32_t n, uint32_t n_kv_heads, uint32_t head_dim);
@@ -172,14 +177,17 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t st);
 // ---- attention (kern_attn.hip) ----
 struct AttnArgs {
   const float* q;        // [n_heads * head_dim]
-  const float* k_cache;  // layer base [n_kv_heads][max_seq][head_dim]
-  const float* v_cache;
+  const void* k_cache;   // layer base [n_kv_heads][max_seq][head_dim], f32 or (kv_f16) f16
+  const void* v_cache;
   float* out;            // [n_heads * head_dim]
   float* partial;        // [n_kv][max_chunks][attn_partial_floats(group, head_dim)]
   const DevState* state;
   uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk, max_seq;
+  uint32_t kv_f16;
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
+// head dims the decode attention takes: multiples of 4 (f32 cache) or 8 (f16) up to 256
+bool attn_decode_head_dim(uint32_t head_dim, bool kv_f16);
 // floats of one partial record (per kv head and chunk): o[group][head_dim],
 // max[group], sum[group], padded to a multiple of 4
 __host__ __device__ inline uint32_t attn_partial_floats(uint32_t group, uint32_t head_dim) {

@@ -53,6 +53,8 @@ _SIGS = {
     "orc_kv_new": (vp, [vp, u64]),
     "orc_kv_free": (None, [vp]),
     "orc_kv_clear": (None, [vp]),
+    "orc_kv_set_f16": (None, [vp, i32]),
+    "orc_round_f16": (f32, [f32]),
     "orc_kv_len": (u64, [vp]),
     "orc_kv_import": (i32, [vp, vp, vp, u64]),
     "orc_kv_export": (i32, [vp, vp, vp, u64]),
@@ -138,6 +140,13 @@ def add_in_place(o, b):
     return o
 
 
+def round_f16(x) -> np.ndarray:
+    """Elementwise orc_round_f16 (binary16 rounding of the f16-KV mode), as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    f = lib().orc_round_f16
+    return np.array([f(float(v)) for v in x], dtype=np.float32)
+
+
 def rope(x, seq, heads, hd, rope_dim, base, pos0=0):
     x = np.array(x, dtype=np.float32, copy=True)
     lib().orc_rope(_ptr(x), seq, heads, hd, rope_dim, base, pos0)
@@ -204,8 +213,12 @@ class Model:
             raise OracleError(rc, "tensor_bytes")
         return np.ctypeslib.as_array(C.cast(p, P(C.c_uint8)), shape=(n.value,)).copy()
 
-    def kv(self, max_seq_len: int) -> "KvCache":
-        return KvCache(self, max_seq_len)
+    def kv(self, max_seq_len: int, f16: bool = False) -> "KvCache":
+        """A cache; f16=True rounds every row stored to binary16 (the f16-KV mode)."""
+        kv = KvCache(self, max_seq_len)
+        if f16:
+            lib().orc_kv_set_f16(kv.h, 1)
+        return kv
 
     def decode_step(self, kv: "KvCache", token: int, mode=MODE_FAST, rope_mode=ROPE_REFERENCE):
         logits = np.zeros(max(self.vocab, 1), dtype=np.float32)

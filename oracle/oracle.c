@@ -441,7 +441,28 @@ struct orc_kv {
   uint64_t n_layers, max_seq_len, kv_dim, len;
   float** k;
   float** v;
+  int f16; /* rows rounded to binary16 as they are stored (the f16-KV session mode) */
 };
+
+/* x rounded to the nearest IEEE binary16 value (ties to even), returned as a
+ * float: the grid spacing of x's binade, 2^(e - 11) for x = m 2^e with m in
+ * [0.5, 1), no finer than the subnormal step 2^-24; rintf rounds half to even
+ * in the default rounding mode; beyond the largest finite half (65504) the
+ * result is infinite.  Not part of the reference (its cache is f32): the
+ * emulation of the f16 cache mode. */
+float orc_round_f16(float x) {
+  if (!isfinite(x) || x == 0.0f) return x;
+  int e;
+  frexpf(x, &e);
+  int q = e - 11;
+  if (q < -24) q = -24;
+  const float r = ldexpf(rintf(ldexpf(x, -q)), q);
+  return fabsf(r) > 65504.0f ? copysignf(INFINITY, x) : r;
+}
+
+static void round_f16_n(float* p, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) p[i] = orc_round_f16(p[i]);
+}
 
 typedef struct {
   const uint8_t* p;
@@ -754,6 +775,7 @@ void orc_kv_free(orc_kv* kv) {
 }
 
 void orc_kv_clear(orc_kv* kv) { kv->len = 0; }
+void orc_kv_set_f16(orc_kv* kv, int on) { kv->f16 = on != 0; }
 uint64_t orc_kv_len(const orc_kv* kv) { return kv->len; }
 
 /* Import/export in the reference layout [layer][t][kv_dim], t < len. */
@@ -886,7 +908,7 @@ static int check_dims(const orc_model* m) {
 
 /* Layer::decode_step (src/model/forward.rs:344-440). */
 static int layer_decode(const orc_model* m, const orc_layer* L, float* kc, float* vc,
-                        uint64_t cache_len, float* hidden, int mode, int rope_mode) {
+                        uint64_t cache_len, float* hidden, int mode, int rope_mode, int kv16) {
   const orc_config* c = &m->cfg;
   uint64_t H = c->hidden_size, hd = c->head_dim, kvd = c->n_kv_heads * hd, F = c->intermediate_size;
   uint64_t grp = c->n_heads / c->n_kv_heads;
@@ -906,6 +928,10 @@ static int layer_decode(const orc_model* m, const orc_layer* L, float* kc, float
   uint64_t pos0 = rope_mode == ORC_ROPE_ABSOLUTE ? cache_len : 0;
   orc_rope(q, 1, c->n_heads, hd, c->rope_dim, c->rope_base, pos0);
   orc_rope(k, 1, c->n_kv_heads, hd, c->rope_dim, c->rope_base, pos0);
+  if (kv16) {
+    round_f16_n(k, kvd);
+    round_f16_n(v, kvd);
+  }
   memcpy(kc + cache_len * kvd, k, kvd * 4);
   memcpy(vc + cache_len * kvd, v, kvd * 4);
   uint64_t nl = cache_len + 1;
@@ -958,7 +984,7 @@ int orc_decode_step(const orc_model* m, orc_kv* kv, uint32_t token, float* logit
   float* w = NULL;
   if ((rc = embed_row(m, token, hidden, mode))) goto done;
   for (uint64_t l = 0; l < c->n_layers; l++)
-    if ((rc = layer_decode(m, &m->layers[l], kv->k[l], kv->v[l], kv->len, hidden, mode, rope_mode)))
+    if ((rc = layer_decode(m, &m->layers[l], kv->k[l], kv->v[l], kv->len, hidden, mode, rope_mode, kv->f16)))
       goto done;
   if ((rc = norm_weight(m, m->output_norm, H, &w))) goto done;
   orc_rms_norm(hidden, w, H, c->norm_eps);
@@ -973,7 +999,7 @@ done:
 /* Shared body of Layer::prefill (src/model/forward.rs:215-337, causal, writes
  * the cache) and Layer::forward (src/model/forward.rs:62-207, no mask, no cache). */
 static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_t seq, float* kc,
-                       float* vc, uint64_t cache_start, int causal, int mode, int rope_mode) {
+                       float* vc, uint64_t cache_start, int causal, int mode, int rope_mode, int kv16) {
   const orc_config* c = &m->cfg;
   uint64_t H = c->hidden_size, hd = c->head_dim, kvd = c->n_kv_heads * hd, F = c->intermediate_size;
   uint64_t grp = c->n_heads / c->n_kv_heads, nh = c->n_heads;
@@ -993,6 +1019,10 @@ static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_
   uint64_t pos0 = (causal && rope_mode == ORC_ROPE_ABSOLUTE) ? cache_start : 0;
   orc_rope(q, seq, nh, hd, c->rope_dim, c->rope_base, pos0);
   orc_rope(k, seq, c->n_kv_heads, hd, c->rope_dim, c->rope_base, pos0);
+  if (kv16) { /* the chunk attends to its rows as the cache holds them */
+    round_f16_n(k, seq * kvd);
+    round_f16_n(v, seq * kvd);
+  }
   if (kc) {
     for (uint64_t t = 0; t < seq; t++) {
       memcpy(kc + (cache_start + t) * kvd, k + t * kvd, kvd * 4);
@@ -1060,7 +1090,7 @@ static int batch_forward(const orc_model* m, orc_kv* kv, const uint32_t* ids, ui
     if ((rc = embed_row(m, ids[i], x + i * H, mode))) goto done;
   for (uint64_t l = 0; l < c->n_layers; l++) {
     rc = layer_batch(m, &m->layers[l], x, n, kv ? kv->k[l] : NULL, kv ? kv->v[l] : NULL,
-                     kv ? kv->len : 0, kv != NULL, mode, rope_mode);
+                     kv ? kv->len : 0, kv != NULL, mode, rope_mode, kv ? kv->f16 : 0);
     if (rc) goto done;
   }
   if (kv) kv->len += n;

@@ -99,6 +99,11 @@ int orc_model_tensor_bytes(const orc_model* m, uint64_t idx, const uint8_t** dat
 orc_kv* orc_kv_new(const orc_model* m, uint64_t max_seq_len);
 void orc_kv_free(orc_kv* kv);
 void orc_kv_clear(orc_kv* kv);
+/* The f16-KV session mode (no reference counterpart): rows stored from now on
+ * are rounded to binary16 (orc_round_f16) before any attention reads them;
+ * import stores what it is given. */
+void orc_kv_set_f16(orc_kv* kv, int on);
+float orc_round_f16(float x);
 uint64_t orc_kv_len(const orc_kv* kv);
 int orc_kv_import(orc_kv* kv, const float* k, const float* v, uint64_t len);
 int orc_kv_export(const orc_kv* kv, float* k, float* v, uint64_t len);

@@ -78,8 +78,8 @@ class GpuModel:
         check(_native.lib().ifx_model_batched_prefill(self.h, C.byref(e)), "batched_prefill")
         return bool(e.value)
 
-    def session(self, max_seq: int) -> "GpuSession":
-        return GpuSession(self, max_seq)
+    def session(self, max_seq: int, kv_f16: bool = False) -> "GpuSession":
+        return GpuSession(self, max_seq, kv_f16)
 
     def forward(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
@@ -90,10 +90,11 @@ class GpuModel:
 
 
 class GpuSession:
-    def __init__(self, model: GpuModel, max_seq: int):
+    def __init__(self, model: GpuModel, max_seq: int, kv_f16: bool = False):
         self.model = model
         self.h = C.c_void_p()
-        check(_native.lib().ifx_session_create(model.h, max_seq, C.byref(self.h)), "session_create")
+        check(_native.lib().ifx_session_create_kv(model.h, max_seq, 1 if kv_f16 else 0, C.byref(self.h)),
+              "session_create_kv")
 
     def close(self):
         if self.h:
