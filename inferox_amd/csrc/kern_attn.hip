@@ -128,8 +128,11 @@ __device__ __forceinline__ void attended_rows(const DevState* st, uint32_t& lo, 
 //   p . V   lane = columns 2l, 2l+1 (+128 j) of all 16 rows, the row weights
 //           broadcast with readlane: no cross-lane reduction.
 // The four waves are combined once through LDS into the chunk's record.
+// At least 3 waves per SIMD: the 70B shape (group 8) otherwise takes 172
+// registers, 2 waves per SIMD, and its ~1040 workgroups at ctx 8192 run in 3
+// rounds instead of 2.
 template <int HDT, int GT, typename E>
-__global__ void __launch_bounds__(kThreads) k_attn_decode(AttnArgs a) {
+__global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnArgs a) {
   constexpr int EPC = 16 / (int)sizeof(E);     // cache elements per 16-byte K chunk
   constexpr int GM = GT > 0 ? GT : kMaxGroup;  // loop bound over query heads
   constexpr int NC4M = (HDT > 0 ? HDT : kMaxHd) / 4;      // float4 of q per head row

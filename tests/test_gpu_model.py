@@ -6,6 +6,8 @@ tokens) on the synthetic models; bit-exact KV export of imported state.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -176,19 +178,22 @@ def test_layer_forward_runs(tmp_path):
     g.close()
 
 
-def test_8b_shape_two_layers(tmpdir_session):
+@pytest.mark.parametrize("max_seq", [512, 4096])
+def test_8b_shape_two_layers(tmpdir_session, max_seq):
     """Full-width Llama-3-8B shape (Q4_K / Q6_K mix, GQA 32/8, vocab 128256), two
-    layers so the oracle finishes in seconds: decode from a seeded KV context."""
+    layers so the oracle finishes in seconds: decode from a seeded KV context,
+    in a 512-row and a 4096-row cache (64 chunk records per kv head to merge)."""
     spec = synth.reduced(synth.LLAMA3_8B, n_layers=2, ctx=512)
     p = str(tmpdir_session / "l8b_2l.gguf")
-    synth.write_llama(p, spec, seed=8)
+    if not os.path.exists(p):
+        synth.write_llama(p, spec, seed=8)
     g, o = GpuModel(p), orc.Model(p)
     c = o.cfg
     L = 200
     kvd = c.n_kv_heads * c.head_dim
     k = synth.normal_f32(c.n_layers * L * kvd, seed=21)
     v = synth.normal_f32(c.n_layers * L * kvd, seed=22)
-    s, kv = g.session(512), o.kv(512)
+    s, kv = g.session(max_seq), o.kv(max_seq)
     assert s.kv_import(k, v, L) == 0 and kv.import_(k, v, L) == 0
     tok = 1000
     for step in range(4):
@@ -201,20 +206,22 @@ def test_8b_shape_two_layers(tmpdir_session):
     g.close()
 
 
-def test_70b_shape_two_layers(tmpdir_session):
+@pytest.mark.parametrize("max_seq", [512, 2048])
+def test_70b_shape_two_layers(tmpdir_session, max_seq):
     """Llama-3-70B widths (dim 8192, ffn 28672, GQA 64/8, vocab 128256), two
     layers: decode from a seeded KV context (group-8 attention, 28672-column
     down projection) and a batched prefill chunk, against the oracle."""
     spec = synth.reduced(synth.LLAMA3_70B, n_layers=2, ctx=512)
     p = str(tmpdir_session / "l70b_2l.gguf")
-    synth.write_llama(p, spec, seed=70)
+    if not os.path.exists(p):
+        synth.write_llama(p, spec, seed=70)
     g, o = GpuModel(p), orc.Model(p)
     c = o.cfg
     L = 300
     kvd = c.n_kv_heads * c.head_dim
     k = synth.normal_f32(c.n_layers * L * kvd, seed=23)
     v = synth.normal_f32(c.n_layers * L * kvd, seed=24)
-    s, kv = g.session(512), o.kv(512)
+    s, kv = g.session(max_seq), o.kv(max_seq)
     assert s.kv_import(k, v, L) == 0 and kv.import_(k, v, L) == 0
     tok = 4242
     for step in range(3):
