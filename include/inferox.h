@@ -46,6 +46,8 @@ enum {
   IFX_E_INVALID_TENSOR_INDEX = 10,/* Error::InvalidTensorIndex */
   IFX_E_TENSOR_OFFSET_OVERFLOW = 11, /* Error::TensorOffsetOverflow */
   IFX_E_UNSUPPORTED_ARCH = 12,    /* Error::UnsupportedArchitecture */
+  IFX_E_JSON = 13,                /* TokenizerError::Json (src/tokenizer/mod.rs:228-232) */
+  IFX_E_UNSUPPORTED_TOKENIZER = 14, /* TokenizerError::UnsupportedModel */
   IFX_E_INVALID_ARG = 20,         /* a reference assert!/slice panic */
   IFX_E_KV_FULL = 21,             /* KV append past max_seq_len (src/model/forward.rs:376) */
   IFX_E_HIP = 22,                 /* a HIP runtime call failed */
@@ -179,6 +181,28 @@ int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, ui
  * f32 (src/model/cache.rs:8-24), host memory.  Import sets len. */
 int ifx_kv_import(ifx_session* s, const float* k, const float* v, uint64_t len);
 int ifx_kv_export(ifx_session* s, float* k, float* v, uint64_t len);
+
+/* ---- text path: the byte-level BPE tokenizer (host only, no device) ---- */
+typedef struct ifx_tokenizer ifx_tokenizer;
+/* BpeTokenizer::from_file / from_json (src/tokenizer/mod.rs:61-114): a
+ * Hugging Face tokenizer.json of model type "BPE".  IFX_E_IO (unreadable, not
+ * UTF-8), IFX_E_JSON (malformed, a missing or mistyped field),
+ * IFX_E_UNSUPPORTED_TOKENIZER (another model type). */
+int ifx_tokenizer_from_file(const char* path, ifx_tokenizer** out);
+int ifx_tokenizer_from_json(const char* json, uint64_t len, ifx_tokenizer** out);
+void ifx_tokenizer_free(ifx_tokenizer* t);
+/* Tokenizer::encode (src/tokenizer/mod.rs:196-205) of len bytes of UTF-8
+ * text (IFX_E_INVALID_UTF8 otherwise): *n_ids = the id count, the first
+ * min(cap, count) ids written. */
+int ifx_tokenizer_encode(const ifx_tokenizer* t, const char* text, uint64_t len, uint32_t* ids, uint64_t cap,
+                         uint64_t* n_ids);
+/* Tokenizer::decode (src/tokenizer/mod.rs:207-225): the UTF-8 text (lossy, as
+ * String::from_utf8_lossy) of n ids; *len_out = its byte length, the first
+ * min(cap, length) bytes written, no terminator. */
+int ifx_tokenizer_decode(const ifx_tokenizer* t, const uint32_t* ids, uint64_t n, char* text, uint64_t cap,
+                         uint64_t* len_out);
+/* Entries of the vocabulary (no reference counterpart; for callers sizing buffers). */
+int ifx_tokenizer_vocab_size(const ifx_tokenizer* t, uint64_t* n);
 
 /* argmax (src/model/forward.rs:615-622) of the logits of the most recent
  * step — for a prefill, of its last row: the token generate feeds next. */

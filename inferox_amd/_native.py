@@ -39,6 +39,12 @@ SIGNATURES = {
     "ifx_model_weight_bytes": (i32, [vp, P(u64), P(u64)]),
     "ifx_session_create": (i32, [vp, u64, P(vp)]),
     "ifx_session_create_kv": (i32, [vp, u64, i32, P(vp)]),
+    "ifx_tokenizer_from_file": (i32, [cp, P(vp)]),
+    "ifx_tokenizer_from_json": (i32, [vp, u64, P(vp)]),
+    "ifx_tokenizer_free": (None, [vp]),
+    "ifx_tokenizer_encode": (i32, [vp, vp, u64, vp, u64, P(u64)]),
+    "ifx_tokenizer_decode": (i32, [vp, vp, u64, vp, u64, P(u64)]),
+    "ifx_tokenizer_vocab_size": (i32, [vp, P(u64)]),
     "ifx_session_destroy": (None, [vp]),
     "ifx_session_clear": (i32, [vp]),
     "ifx_session_len": (i32, [vp, P(u64)]),

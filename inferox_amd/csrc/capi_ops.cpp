@@ -169,6 +169,8 @@ const char* ifx_status_string(int s) {
     case IFX_E_INVALID_TENSOR_INDEX: return "tensor index out of bounds";
     case IFX_E_TENSOR_OFFSET_OVERFLOW: return "tensor byte range overflows file bounds";
     case IFX_E_UNSUPPORTED_ARCH: return "unsupported model architecture";
+    case IFX_E_JSON: return "json error";
+    case IFX_E_UNSUPPORTED_TOKENIZER: return "unsupported tokenizer model";
     case IFX_E_INVALID_ARG: return "invalid argument";
     case IFX_E_KV_FULL: return "KV cache full";
     case IFX_E_HIP: return "HIP runtime error";
