@@ -68,6 +68,13 @@ def build_product(jobs: int = 8, verbose: bool = False) -> str:
     tmp = out_so + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"])
     os.replace(tmp, out_so)
+    # the `inferox` command (src/main.rs), linked against the library beside it
+    cli_obj = os.path.join(OBJ, "cli_main.o")
+    _run([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, "cli_main.cpp"), "-o", cli_obj])
+    cli = os.path.join(LIB, "inferox")
+    _run([hipcc, f"--offload-arch={ARCH}", "-o", cli + ".tmp", cli_obj, "-L" + LIB, "-linferox",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(cli + ".tmp", cli)
     return out_so
 
 

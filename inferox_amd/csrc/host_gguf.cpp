@@ -171,8 +171,13 @@ int read_value(Reader& r, uint32_t type, GgufValue* v) {
       IFX_TRY(r.get(&it));
       if (it > 12) return set_error(IFX_E_UNKNOWN_VALUE_TYPE, "unknown array item type %u", it);
       IFX_TRY(r.get(&n));
-      GgufValue item;
-      for (uint64_t k = 0; k < n; k++) IFX_TRY(read_value(r, it, &item));
+      // every item takes at least one byte: a longer count runs past the end,
+      // which the reference meets as an io error while reading the items
+      if (n > r.n - r.pos) return set_error(IFX_E_IO, "unexpected end of file in an array of %llu items",
+                                            (unsigned long long)n);
+      v->item_type = it;
+      v->items.resize(n);
+      for (uint64_t k = 0; k < n; k++) IFX_TRY(read_value(r, it, &v->items[k]));
       return IFX_OK;
     }
     case 10: { uint64_t x; IFX_TRY(r.get(&x)); v->u = x; return IFX_OK; }

@@ -15,6 +15,8 @@ struct GgufValue {
   int64_t i = 0;
   double f = 0.0;
   std::string s;
+  uint32_t item_type = 0;        // arrays: Value::Array(item type, items)
+  std::vector<GgufValue> items;
 };
 
 struct GgufMeta {

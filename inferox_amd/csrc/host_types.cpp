@@ -61,11 +61,13 @@ bool dequant_supported(uint32_t t) {
          t == T_Q8K;
 }
 
+// TensorType::name (src/gguf/types.rs:146-178), indexed by the type id.
 const char* type_name(uint32_t t) {
-  switch (t) {
-    case 0: return "F32"; case 1: return "F16"; case 2: return "Q4_0"; case 7: return "Q8_0";
-    case 12: return "Q4_K"; case 14: return "Q6_K"; case 15: return "Q8_K"; default: return "?";
-  }
+  static const char* names[31] = {"F32",    "F16",     "Q4_0",   "Q4_1",  "?",     "Q5_0",    "Q5_1",   "Q8_0",
+                                  "Q8_1",   "?",       "Q2_K",   "Q3_K",  "Q4_K",  "Q5_K",    "Q6_K",   "Q8_K",
+                                  "I8",     "I16",     "I32",    "I64",   "F64",   "IQ1_S",   "IQ1_M",  "IQ2_XXS",
+                                  "IQ2_XS", "IQ2_S",   "IQ3_XXS", "IQ3_S", "IQ4_XS", "IQ4_NL", "IQ4_XSS"};
+  return t < 31 ? names[t] : "?";
 }
 
 bool layout_sizes(uint32_t type, uint64_t rows, uint64_t cols, uint64_t* body, uint64_t* scal) {
