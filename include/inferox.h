@@ -99,6 +99,14 @@ typedef struct {
  * resolution (src/model/mod.rs:34-48).  In addition every weight is uploaded to
  * HBM once, in its quantized form; nothing is dequantized to f32 in HBM. */
 int ifx_model_open(const char* path, ifx_model** out);
+/* Open flags (no reference counterpart).  IFX_OPEN_GGML_KQUANTS reads Q4_K
+ * and Q6_K tensors in ggml's block layout (llama.cpp block_q4_K: ggml's
+ * nibble-to-element order; block_q6_K: ql, qh, int8 scales, then d) instead of
+ * the reference's (Q4_K group-contiguous nibbles, Q6_K d first with u8
+ * scales), for GGUF files written by llama.cpp.  Q4_0, Q8_0, F32 and F16 read
+ * the same either way; a Q8_K tensor is refused (IFX_E_UNKNOWN_TENSOR_TYPE). */
+enum { IFX_OPEN_GGML_KQUANTS = 1 };
+int ifx_model_open_ex(const char* path, uint32_t flags, ifx_model** out);
 void ifx_model_close(ifx_model* model);
 int ifx_model_config(const ifx_model* model, ifx_config* out);
 /* Bytes of weights resident in HBM, and the stored GGUF bytes they came from. */
@@ -262,6 +270,10 @@ typedef struct ifx_tensor ifx_tensor;
  * cols contiguous) into the device layout the GEMV kernels read. */
 int ifx_tensor_upload(uint32_t type, const void* host_bytes, uint64_t n_bytes, uint64_t rows,
                       uint64_t cols, ifx_tensor** out);
+/* ifx_tensor_upload with IFX_OPEN_* flags (IFX_OPEN_GGML_KQUANTS: ggml's
+ * Q4_K / Q6_K block layout). */
+int ifx_tensor_upload_ex(uint32_t type, const void* host_bytes, uint64_t n_bytes, uint64_t rows, uint64_t cols,
+                         uint32_t flags, ifx_tensor** out);
 void ifx_tensor_free(ifx_tensor* t);
 int ifx_tensor_bytes(const ifx_tensor* t, uint64_t* device_bytes, uint64_t* gguf_bytes);
 /* Dequantize an uploaded matrix to f32 [rows x cols] on the device (bit-exact). */

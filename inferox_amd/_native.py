@@ -39,6 +39,8 @@ SIGNATURES = {
     "ifx_model_weight_bytes": (i32, [vp, P(u64), P(u64)]),
     "ifx_session_create": (i32, [vp, u64, P(vp)]),
     "ifx_session_create_kv": (i32, [vp, u64, i32, P(vp)]),
+    "ifx_model_open_ex": (i32, [cp, u32, P(vp)]),
+    "ifx_tensor_upload_ex": (i32, [u32, vp, u64, u64, u64, u32, P(vp)]),
     "ifx_tokenizer_from_file": (i32, [cp, P(vp)]),
     "ifx_tokenizer_from_json": (i32, [vp, u64, P(vp)]),
     "ifx_tokenizer_free": (None, [vp]),

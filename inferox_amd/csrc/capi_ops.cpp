@@ -46,7 +46,7 @@ int device_init() {
 static hipStream_t stream_of(void* s) { return s ? (hipStream_t)s : g_stream; }
 
 DevW devw(const ifx_tensor* t) {
-  return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal};
+  return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal, t->L.q6_signed};
 }
 
 // Runs fn(i0, i1) over [0, n) in contiguous ranges, one worker per core share.
@@ -66,8 +66,12 @@ static void parallel_ranges(uint64_t n, uint64_t min_per_worker, F fn) {
 }
 
 int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t rows, uint64_t cols,
-                  ifx_tensor** out) {
+                  ifx_tensor** out, uint32_t flags) {
   *out = nullptr;
+  std::vector<uint8_t> converted;  // ggml K-quant blocks rewritten as the reference's
+  const bool ggml = (flags & IFX_OPEN_GGML_KQUANTS) != 0;
+  if (ggml && type == T_Q8K)
+    return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "ggml's Q8_K is not a storage type of the reference's layout");
   if (!gemv_supported(type))
     return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "tensor type %u has no device layout", type);
   uint64_t expect;
@@ -77,6 +81,14 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
     return set_error(IFX_E_UNEXPECTED_EOF, "%llu bytes for a %s [%llu x %llu] matrix, %llu expected",
                      (unsigned long long)nbytes, type_name(type), (unsigned long long)rows,
                      (unsigned long long)cols, (unsigned long long)expect);
+  if (ggml && (type == T_Q4K || type == T_Q6K)) {
+    const uint64_t bb = type == T_Q4K ? 144 : 210, nb = nbytes / bb;
+    converted.resize(nbytes);
+    parallel_ranges(nb, 65536, [&](uint64_t b0, uint64_t b1) {
+      ggml_kquant_to_reference(type, src + b0 * bb, b1 - b0, converted.data() + b0 * bb);
+    });
+    src = converted.data();
+  }
   uint64_t body, scal;
   if (!layout_sizes(type, rows, cols, &body, &scal))
     return set_error(IFX_E_INVALID_ARG, "%s rows of %llu columns are not whole blocks", type_name(type),
@@ -95,6 +107,7 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
   t->L.body_bytes = body;
   t->L.scal_bytes = scal;
   t->L.gguf_bytes = nbytes;
+  t->L.q6_signed = ggml && type == T_Q6K;
   uint64_t be = 1, bb = 0;
   if (type == T_F32 || type == T_F16) { be = 1; bb = element_size(type); }
   else block_layout(type, &be, &bb);
@@ -248,7 +261,16 @@ int ifx_tensor_upload(uint32_t type, const void* host, uint64_t n_bytes, uint64_
   clear_error();
   IFX_TRY(device_init());
   if (!out || (!host && n_bytes)) return set_error(IFX_E_INVALID_ARG, "null argument");
-  return upload_matrix(type, (const uint8_t*)host, n_bytes, rows, cols, out);
+  return upload_matrix(type, (const uint8_t*)host, n_bytes, rows, cols, out, 0);
+}
+
+int ifx_tensor_upload_ex(uint32_t type, const void* host, uint64_t n_bytes, uint64_t rows, uint64_t cols,
+                         uint32_t flags, ifx_tensor** out) {
+  clear_error();
+  IFX_TRY(device_init());
+  if (!out || (!host && n_bytes)) return set_error(IFX_E_INVALID_ARG, "null argument");
+  if (flags & ~(uint32_t)IFX_OPEN_GGML_KQUANTS) return set_error(IFX_E_INVALID_ARG, "unknown flags %#x", flags);
+  return upload_matrix(type, (const uint8_t*)host, n_bytes, rows, cols, out, flags);
 }
 
 void ifx_tensor_free(ifx_tensor* t) {
@@ -275,7 +297,7 @@ int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream) {
   IFX_TRY(device_init());
   if (!w || !x || !y) return set_error(IFX_E_INVALID_ARG, "null argument");
   GemvLaunch L;
-  L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows};
+  L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.q6_signed};
   L.nseg = 1;
   L.cols = (uint32_t)w->L.cols;
   L.x = x;
@@ -302,7 +324,7 @@ int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, voi
                     part_bytes};
     hipError_t e = launch_prep_rows(a, (uint32_t)m, (uint32_t)k, (uint32_t)k, nullptr, 0.f, in, st);
     if (e == hipSuccess) {
-      const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols};
+      const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols, w->L.q6_signed};
       e = gemm_store(in, gw, c, (uint32_t)w->L.rows, st);
     }
     const hipError_t ef = hipFreeAsync(buf, st);
@@ -312,7 +334,7 @@ int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, voi
   }
   for (uint64_t i = 0; i < m; i++) {
     GemvLaunch L;
-    L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows};
+    L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.q6_signed};
     L.nseg = 1;
     L.cols = (uint32_t)w->L.cols;
     L.x = a + i * w->L.cols;

@@ -90,6 +90,7 @@ struct DevW {
   uint64_t cols;
   const uint8_t* body;
   const uint8_t* scal;
+  uint32_t q6_signed = 0;  // Q6_K: int8 scale bytes (ggml's), else u8 (the reference's)
 };
 
 // Element e (row-major flat index) of a matrix in the device layout; same
@@ -137,7 +138,9 @@ __device__ __forceinline__ float dev_elem(const DevW& w, uint64_t e) {
       uint32_t hi = (word >> (8 * ((k & 7) >> 1) + 2 * (k & 1) + 4 * (k >> 3))) & 3u;
       int q = (int)(lo | (hi << 4));
       float d = h2f(ld_u16_unaligned(u + 3328 + 2 * n));
-      return d * (float)u[3072 + 4 * lane + c] * (float)(q - 32);
+      const uint32_t sb = u[3072 + 4 * lane + c];
+      const float sc = w.q6_signed ? (float)(int8_t)sb : (float)sb;
+      return d * sc * (float)(q - 32);
     }
     case 15: {
       uint64_t b = e / 256;

@@ -24,7 +24,7 @@ using namespace ifx;
 namespace ifx {
 int device_init();
 int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t rows, uint64_t cols,
-                  ifx_tensor** out);
+                  ifx_tensor** out, uint32_t flags);
 DevW devw(const ifx_tensor* t);
 }  // namespace ifx
 
@@ -35,6 +35,7 @@ struct LayerDev {
 };
 
 struct ifx_model {
+  uint32_t flags = 0;  // IFX_OPEN_* of ifx_model_open_ex
   MappedFile map;
   GgufFile gguf;
   ifx_config cfg{};
@@ -134,7 +135,7 @@ int upload_weight(ifx_model* m, int64_t idx, uint64_t rows, uint64_t cols, ifx_t
     return set_error(IFX_E_INVALID_ARG, "%s has %llu elements, expected %llu x %llu", t.name.c_str(),
                      (unsigned long long)t.n_elements(), (unsigned long long)rows,
                      (unsigned long long)cols);
-  int rc = upload_matrix(t.type, data, sz, rows, cols, out);
+  int rc = upload_matrix(t.type, data, sz, rows, cols, out, m->flags);
   if (rc != IFX_OK) return rc;
   uint64_t db = (*out)->L.body_bytes + (*out)->L.scal_bytes;
   m->dev_bytes += db;
@@ -163,7 +164,7 @@ int check_dims(const ifx_model* m) {
 }
 
 GemvSeg seg_of(const ifx_tensor* t) {
-  return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows};
+  return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.q6_signed};
 }
 
 // The batched prefill GEMM takes the quantized matrices whose operands it can
@@ -181,7 +182,9 @@ bool gemm_eligible(const ifx_model* m) {
       if (!gemm_tensor_ok(t)) return false;
   return true;
 }
-GemmW gw(const ifx_tensor* t) { return GemmW{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.cols}; }
+GemmW gw(const ifx_tensor* t) {
+  return GemmW{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.cols, t->L.q6_signed};
+}
 
 // Kernel classes of one step (ifx_session_profile): 0 embed, 1 qkv + rope +
 // kv-append, 2 attention (partials + merge), 3 attn_output + residual,
@@ -480,11 +483,15 @@ void session_free(ifx_session* s) {
 
 extern "C" {
 
-int ifx_model_open(const char* path, ifx_model** out) {
+int ifx_model_open(const char* path, ifx_model** out) { return ifx_model_open_ex(path, 0, out); }
+
+int ifx_model_open_ex(const char* path, uint32_t flags, ifx_model** out) {
   clear_error();
   if (!out) return set_error(IFX_E_INVALID_ARG, "null output");
   *out = nullptr;
+  if (flags & ~(uint32_t)IFX_OPEN_GGML_KQUANTS) return set_error(IFX_E_INVALID_ARG, "unknown flags %#x", flags);
   ifx_model* m = new ifx_model();
+  m->flags = flags;
   int rc = m->map.open(path);
   if (rc == IFX_OK) rc = gguf_parse(m->map.data, m->map.size, &m->gguf);
   if (rc != IFX_OK) { model_free(m); return rc; }

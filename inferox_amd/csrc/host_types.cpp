@@ -154,6 +154,49 @@ static void pack_unit(uint32_t type, const uint8_t* const* blk, uint8_t* u) {
   }
 }
 
+// ggml's blocks (llama.cpp ggml-quants.c dequantize_row_q4_K / _q6_K) as the
+// reference's (src/gguf/dequant.rs:133-161, 182-197):
+//   Q4_K: same header; ggml's element 64 i + l is the low nibble of qs[32 i + l]
+//         (sub-block 2 i), element 64 i + 32 + l its high nibble (sub-block
+//         2 i + 1); the reference's element 32 g + l is nibble l % 2 of
+//         qs[16 g + l / 2].
+//   Q6_K: ggml: ql[128], qh[64], int8 scales[16], d; element 128 h + 32 j + l
+//         (j < 4, l < 32) has its low 4 bits in ql[64 h + l + 32 (j & 1)]
+//         (low nibble for j < 2, high for j >= 2) and its high 2 bits at bit
+//         2 j of qh[32 h + l]; its scale is scales[(128 h + 32 j + l) / 16].
+//         The reference: d, scales, ql (element e: nibble e % 2 of byte e / 2),
+//         qh (element e: bits 2 (e % 4) of byte e / 4); scales by e / 16.
+void ggml_kquant_to_reference(uint32_t type, const uint8_t* in, uint64_t n_blocks, uint8_t* out) {
+  for (uint64_t b = 0; b < n_blocks; b++) {
+    if (type == T_Q4K) {
+      const uint8_t* g = in + 144 * b;
+      uint8_t* r = out + 144 * b;
+      memcpy(r, g, 16);
+      memset(r + 16, 0, 128);
+      for (int sb = 0; sb < 8; sb++)
+        for (int l = 0; l < 32; l++) {
+          const uint8_t byte = g[16 + 32 * (sb / 2) + l];
+          const uint8_t v = (sb & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 15);
+          r[16 + 16 * sb + l / 2] |= (uint8_t)(v << (4 * (l & 1)));
+        }
+    } else {
+      const uint8_t* g = in + 210 * b;
+      uint8_t* r = out + 210 * b;
+      memset(r, 0, 210);
+      memcpy(r, g + 208, 2);       // d
+      memcpy(r + 2, g + 192, 16);  // the int8 scale bytes, unchanged
+      for (int e = 0; e < 256; e++) {
+        const int h = e / 128, j = (e % 128) / 32, l = e % 32;
+        const uint8_t lb = g[64 * h + l + 32 * (j & 1)];
+        const uint32_t lo = j < 2 ? (lb & 15u) : (uint32_t)(lb >> 4);
+        const uint32_t hi = (g[128 + 32 * h + l] >> (2 * j)) & 3u;
+        r[18 + e / 2] |= (uint8_t)(lo << (4 * (e & 1)));
+        r[146 + e / 4] |= (uint8_t)(hi << (2 * (e & 3)));
+      }
+    }
+  }
+}
+
 void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t cols, uint64_t t0, uint64_t t1,
                   uint8_t* body) {
   const uint64_t nbr = cols / 256, bb = type == T_Q4K ? 144 : 210;

@@ -83,7 +83,15 @@ struct DevLayout {
   uint64_t gguf_bytes = 0;    // stored GGUF bytes of the same matrix
   float abs_bound = 0.f;      // bound on |element| from the block scales (inf: unbounded or non-finite)
   float dmin_max = 0.f;       // Q4_K: largest |dmin| (NaN if any is NaN)
+  uint32_t q6_signed = 0;     // Q6_K: scale bytes are int8 (ggml's layout), not the reference's u8
 };
+
+// ggml's K-quant blocks (llama.cpp ggml-common.h block_q4_K / block_q6_K)
+// rewritten as the reference's blocks: Q4_K loses nothing (only the
+// nibble-to-element order differs); Q6_K moves d first and re-places ql/qh
+// in the reference's element order, keeping the int8 scale bytes as they are
+// (the tensor is then read with q6_signed).  n_blocks blocks, in -> out.
+void ggml_kquant_to_reference(uint32_t type, const uint8_t* in, uint64_t n_blocks, uint8_t* out);
 
 // Host-side repack of one matrix from GGUF block bytes into the device layout
 // (dst_body/dst_scal sized by layout_sizes); the block-wise types.

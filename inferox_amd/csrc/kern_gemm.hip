@@ -170,14 +170,16 @@ struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
   static constexpr bool kMins = false, kPLo = true, kScaled = false;
   typedef SideD Side;
   uint2 ql;
-  uint32_t hw, sc, d;
+  uint32_t hw, d;
+  int32_t sc;  // u8, or int8 for a tensor read in ggml's layout
   __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t g, int h, bool sb0) {
     const uint32_t nt = row & 15u;
     const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (ks >> 3)) * kUnitQ6K;
     const uint32_t lane = nt + 16u * (g & 3u), c = 2u * (g >> 2) + (uint32_t)h;
     ql = *(const uint2*)(u + (g >> 2) * 1024u + lane * 16u + 8u * (uint32_t)h);
     hw = *(const uint32_t*)(u + 2048u + lane * 16u + 4u * c);
-    sc = u[3072u + 4u * lane + c];
+    const uint32_t sb = u[3072u + 4u * lane + c];
+    sc = w.q6_signed ? (int32_t)(int8_t)sb : (int32_t)sb;
     if (sb0) d = *(const uint16_t*)(u + 3328u + 2u * nt);
   }
   // q of elements (j, j + 4) of chunk cc: low nibbles from ql, high parts at

@@ -110,6 +110,11 @@ __device__ __forceinline__ v4i six(uint32_t l0, uint32_t l1, uint32_t h) {
 }
 
 __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xffu); }
+// byte b of v as a scale: u8 (the reference's Q6_K) or int8 (ggml's, sgn != 0)
+__device__ __forceinline__ float cvts(uint32_t v, int b, uint32_t sgn) {
+  const uint32_t x = (v >> (8 * b)) & 0xffu;
+  return sgn ? (float)(int)(int8_t)x : (float)x;
+}
 
 // One (tile, block) unit of a segment in registers.  dot() returns this lane's
 // share of row (lane & 15)'s dot product over the block: sub-blocks g and
@@ -132,7 +137,7 @@ struct KBuf<T_Q4K> {
   uint4 h, q0, q1;
   // u: wave-uniform unit base; 32-bit unsigned lane offsets keep the
   // scalar-base addressing form (no 64-bit address per lane)
-  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
+  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane, uint32_t) {
     h = ld16(u + 16u * (lane & 15u));
     q0 = ld16(u + (256u + 16u * lane));
     q1 = ld16(u + (1280u + 16u * lane));
@@ -154,13 +159,15 @@ struct KBuf<T_Q4K> {
   }
 };
 
-// Q6_K (reference layout, src/gguf/dequant.rs:165-199): w = (d * sc) * (q - 32).
+// Q6_K (reference layout, src/gguf/dequant.rs:165-199): w = (d * sc) * (q - 32),
+// sc u8, or int8 for a tensor read in ggml's layout (sgn).
 template <>
 struct KBuf<T_Q6K> {
   static constexpr uint64_t kUnit = kUnitQ6K;
   uint4 l0, l1, hq;
-  uint32_t sc, d;
-  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane) {
+  uint32_t sc, d, sgn;
+  __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane, uint32_t q6_signed) {
+    sgn = q6_signed;
     l0 = ld16(u + 16u * lane);
     l1 = ld16(u + (1024u + 16u * lane));
     hq = ld16(u + (2048u + 16u * lane));
@@ -176,10 +183,10 @@ struct KBuf<T_Q6K> {
     const v4i c1 = mfma(A[1], six(l0.z, l0.w, hq.y), z);
     const v4i c2 = mfma(A[2], six(l1.x, l1.y, hq.z), z);
     const v4i c3 = mfma(A[3], six(l1.z, l1.w, hq.w), z);
-    float v = (df * cvtb(sc, 0)) * fmaf(xa.x, digits(c0), xa.z);
-    v = fmaf(df * cvtb(sc, 1), fmaf(xa.x, digits(c1), xa.w), v);
-    v = fmaf(df * cvtb(sc, 2), fmaf(xb.x, digits(c2), xb.z), v);
-    return fmaf(df * cvtb(sc, 3), fmaf(xb.x, digits(c3), xb.w), v);
+    float v = (df * cvts(sc, 0, sgn)) * fmaf(xa.x, digits(c0), xa.z);
+    v = fmaf(df * cvts(sc, 1, sgn), fmaf(xa.x, digits(c1), xa.w), v);
+    v = fmaf(df * cvts(sc, 2, sgn), fmaf(xb.x, digits(c2), xb.z), v);
+    return fmaf(df * cvts(sc, 3, sgn), fmaf(xb.x, digits(c3), xb.w), v);
   }
 };
 
@@ -378,7 +385,8 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
         ntl = min(ntl, nt - 1);
         const uint32_t nb = min(j + S * nm, nbr - 1);
 #pragma unroll
-        for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, ntl, nb), lane);
+        for (int t = 0; t < NT; t++)
+          buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, ntl, nb), lane, a.seg[NT == 2 ? t : s].q6_signed);
         // keep the ring order: the next block's decode may not be hoisted above
         // these loads (it would wait for every buffer at once)
         __builtin_amdgcn_sched_barrier(0);
@@ -424,7 +432,8 @@ __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D
     if (i < i0 || i >= i1) continue;
     const uint32_t b = min(j + a.split * i, a.nbr - 1);
 #pragma unroll
-    for (int t = 0; t < NT; t++) buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane);
+    for (int t = 0; t < NT; t++)
+      buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane, a.seg[NT == 2 ? t : s].q6_signed);
     // issue the slots in ring order: the loop's waits assume slot i is older
     // than slot i + 1 on every path into it (reordered prefetches made each
     // step wait for the whole ring)

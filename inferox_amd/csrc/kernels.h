@@ -50,6 +50,7 @@ struct GemvSeg {
   const uint8_t* scal;
   uint32_t type;
   uint32_t rows;
+  uint32_t q6_signed = 0;  // Q6_K with int8 scale bytes (ggml's layout)
 };
 
 struct GemvLaunch {
@@ -91,6 +92,7 @@ struct GemmW {
   uint32_t type;
   uint32_t rows;
   uint64_t cols;
+  uint32_t q6_signed = 0;  // Q6_K with int8 scale bytes (ggml's layout)
 };
 // The activation operand as k_prep_rows leaves it (launch_prep_rows): m rows
 // of k columns scaled per row into the fp16 range and split into hi + lo fp16

@@ -7,7 +7,10 @@ numpy float32 arithmetic is one IEEE rounding per operation with no fused
 multiply-add, like the Rust reference.
 
 Also a float64 forward of the llama block (no quantization rounding of the
-activations) used as a loose brute-force check of the oracle's model code.
+activations) used as a loose brute-force check of the oracle's model code,
+and restatements of ggml's Q4_K / Q6_K dequantizers (llama.cpp
+ggml-quants.c, the published block_q4_K / block_q6_K definitions; not part of
+the reference), the checker of the ggml-layout mode.
 """
 from __future__ import annotations
 
@@ -76,6 +79,47 @@ def dequant_q6_k(raw: np.ndarray) -> np.ndarray:
     q = (lo | (hi << 4)) - 32
     scale = np.repeat(sc, 16, axis=1)
     return ((d * scale) * q.astype(np.float32)).reshape(-1)
+
+
+def dequant_q4_k_ggml(raw: np.ndarray) -> np.ndarray:
+    """ggml's Q4_K (llama.cpp ggml-quants.c dequantize_row_q4_K; no reference
+    counterpart: the checker of IFX_OPEN_GGML_KQUANTS).  The 144-byte block
+    has the reference's header (d, dmin, 12 packed scale/min bytes, which
+    get_scale_min_k4 unpacks as q4k_scales does); each 64-element chunk i takes
+    qs[32 i .. 32 i + 32]: low nibbles for sub-block 2 i, high for 2 i + 1.
+    y = d1 q - m1, d1 = d sc, m1 = dmin m."""
+    blk = raw.reshape(-1, 144)
+    d = _f16(blk[:, 0:2])[:, None]
+    dmin = _f16(blk[:, 2:4])[:, None]
+    sc, mn = q4k_scales(blk[:, 4:16])
+    dall = d * sc.astype(np.float32)
+    dm = dmin * mn.astype(np.float32)
+    qs = blk[:, 16:144].reshape(-1, 4, 1, 32)
+    q = np.concatenate([qs & 15, qs >> 4], axis=2).reshape(-1, 8, 32).astype(np.float32)
+    return (dall[:, :, None] * q - dm[:, :, None]).reshape(-1)
+
+
+def dequant_q6_k_ggml(raw: np.ndarray) -> np.ndarray:
+    """ggml's Q6_K (llama.cpp ggml-quants.c dequantize_row_q6_K; no reference
+    counterpart): block ql[128], qh[64], int8 scales[16], f16 d.  Element
+    128 h + 32 j + l (j < 4, l < 32): low 4 bits from ql[64 h + l + 32 (j & 1)]
+    (low nibble for j < 2, high for j >= 2), high 2 bits at bit 2 j of
+    qh[32 h + l]; scale scales[8 h + l / 16 + 2 j]; y = (d sc) (q - 32)."""
+    blk = raw.reshape(-1, 210)
+    nb = blk.shape[0]
+    ql = blk[:, 0:128].reshape(nb, 2, 64).astype(np.int32)
+    qh = blk[:, 128:192].reshape(nb, 2, 32).astype(np.int32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float32)
+    d = _f16(blk[:, 208:210])[:, None]
+    q = np.empty((nb, 2, 4, 32), np.int32)
+    for j in range(4):
+        lo = ql[:, :, 32 * (j & 1): 32 * (j & 1) + 32]
+        nib = (lo & 15) if j < 2 else (lo >> 4)
+        q[:, :, j, :] = (nib | (((qh >> (2 * j)) & 3) << 4)) - 32
+    l = np.arange(32)
+    sidx = (8 * np.arange(2)[:, None, None] + 2 * np.arange(4)[None, :, None] + (l // 16)[None, None, :])
+    scale = sc[:, sidx]                                # [nb, 2, 4, 32]
+    return ((d[:, :, None, None] * scale) * q.astype(np.float32)).reshape(-1)
 
 
 def dequant_q8_k(raw: np.ndarray) -> np.ndarray:
