@@ -110,11 +110,6 @@ __device__ __forceinline__ v4i six(uint32_t l0, uint32_t l1, uint32_t h) {
 }
 
 __device__ __forceinline__ float cvtb(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xffu); }
-// byte b of v as a scale: u8 (the reference's Q6_K) or int8 (ggml's, sgn != 0)
-__device__ __forceinline__ float cvts(uint32_t v, int b, uint32_t sgn) {
-  const uint32_t x = (v >> (8 * b)) & 0xffu;
-  return sgn ? (float)(int)(int8_t)x : (float)x;
-}
 
 // One (tile, block) unit of a segment in registers.  dot() returns this lane's
 // share of row (lane & 15)'s dot product over the block: sub-blocks g and
@@ -165,9 +160,11 @@ template <>
 struct KBuf<T_Q6K> {
   static constexpr uint64_t kUnit = kUnitQ6K;
   uint4 l0, l1, hq;
-  uint32_t sc, d, sgn;
+  uint32_t sc, d, xm;
+  float off;  // int8 scales: each byte's top bit flipped (xm) and 128 taken off at use
   __device__ __forceinline__ void load(const uint8_t* u, uint32_t lane, uint32_t q6_signed) {
-    sgn = q6_signed;
+    xm = q6_signed ? 0x80808080u : 0u;
+    off = q6_signed ? 128.f : 0.f;
     l0 = ld16(u + 16u * lane);
     l1 = ld16(u + (1024u + 16u * lane));
     hq = ld16(u + (2048u + 16u * lane));
@@ -183,10 +180,11 @@ struct KBuf<T_Q6K> {
     const v4i c1 = mfma(A[1], six(l0.z, l0.w, hq.y), z);
     const v4i c2 = mfma(A[2], six(l1.x, l1.y, hq.z), z);
     const v4i c3 = mfma(A[3], six(l1.z, l1.w, hq.w), z);
-    float v = (df * cvts(sc, 0, sgn)) * fmaf(xa.x, digits(c0), xa.z);
-    v = fmaf(df * cvts(sc, 1, sgn), fmaf(xa.x, digits(c1), xa.w), v);
-    v = fmaf(df * cvts(sc, 2, sgn), fmaf(xb.x, digits(c2), xb.z), v);
-    return fmaf(df * cvts(sc, 3, sgn), fmaf(xb.x, digits(c3), xb.w), v);
+    const uint32_t s4 = sc ^ xm;
+    float v = (df * (cvtb(s4, 0) - off)) * fmaf(xa.x, digits(c0), xa.z);
+    v = fmaf(df * (cvtb(s4, 1) - off), fmaf(xa.x, digits(c1), xa.w), v);
+    v = fmaf(df * (cvtb(s4, 2) - off), fmaf(xb.x, digits(c2), xb.z), v);
+    return fmaf(df * (cvtb(s4, 3) - off), fmaf(xb.x, digits(c3), xb.w), v);
   }
 };
 
