@@ -13,8 +13,10 @@
 // logits by the device sampler (ifx_sample_logits: temperature softmax, no
 // top-k, top-p 1, as the CLI's Sampler); the reference draws from thread_rng,
 // this command from splitmix64 of a seed (IFX_SEED, else the clock) and the
-// step, so a run repeats from its seed.
+// step, so a run repeats from its seed.  IFX_GGML=1 in the environment opens
+// the model with IFX_OPEN_GGML_KQUANTS (a GGUF written by llama.cpp).
 #include <inttypes.h>
+#include <stdint.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -178,7 +180,9 @@ int inspect(const char* path) {
 int generate(const char* model_path, const char* tok_path, const char* prompt, uint64_t max_tokens,
              float temperature) {
   ifx_model* model = nullptr;
-  if (ifx_model_open(model_path, &model) != IFX_OK) {
+  const char* ggml_env = getenv("IFX_GGML");
+  const uint32_t flags = ggml_env && strcmp(ggml_env, "1") == 0 ? (uint32_t)IFX_OPEN_GGML_KQUANTS : 0u;
+  if (ifx_model_open_ex(model_path, flags, &model) != IFX_OK) {
     fprintf(stderr, "error: failed to load model '%s': %s\n", model_path, ifx_last_error());
     return 1;
   }
@@ -246,15 +250,26 @@ int generate(const char* model_path, const char* tok_path, const char* prompt, u
   return rc == IFX_OK ? 0 : 1;
 }
 
-// str::parse::<usize> / ::<f32>: the whole argument, else the default
+// str::parse::<usize>: an optional '+', then one or more decimal digits, in range
 bool parse_u64(const char* s, uint64_t* v) {
-  if (!*s || *s == '-') return false;
-  char* end;
-  *v = strtoull(s, &end, 10);
-  return *end == 0 && (s[0] != '+' || s[1] != 0) && (s[0] == '+' ? s[1] != ' ' : s[0] != ' ');
+  if (*s == '+') s++;
+  if (!*s) return false;
+  uint64_t x = 0;
+  for (const char* p = s; *p; p++) {
+    if (*p < '0' || *p > '9') return false;
+    const uint64_t d = (uint64_t)(*p - '0');
+    if (x > (UINT64_MAX - d) / 10) return false;
+    x = x * 10 + d;
+  }
+  *v = x;
+  return true;
 }
+
+// str::parse::<f32>: a decimal number with optional sign and exponent, or
+// inf / infinity / nan (any case); no blanks, no hexadecimal (which strtof
+// alone would take)
 bool parse_f32(const char* s, float* v) {
-  if (!*s || *s == ' ') return false;
+  if (!*s || strchr(s, 'x') || strchr(s, 'X') || strchr(s, ' ') || strchr(s, '\t') || strchr(s, '\n')) return false;
   char* end;
   *v = strtof(s, &end);
   return *end == 0;
