@@ -204,7 +204,8 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the token loop runs on a single MI355X; "
-                          "multi-GPU sharding is described in DESIGN.md but not built", "n_gpus": args.gpus}))
+                          "multi-GPU sharding (heads and FFN columns split per GPU) is not built",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
 
     from inferox_amd import _native, synth
