@@ -185,3 +185,20 @@ def test_kv_f16_bad_type(tiny):
     h = C.c_void_p()
     assert _native.lib().ifx_session_create_kv(g.h, 64, 2, C.byref(h)) == 20  # IFX_E_INVALID_ARG
     assert not h.value
+
+
+def test_kv_f16_needs_head_dim_multiple_of_8(tmp_path):
+    """head_dim 4 (the reference's forward-test model): an f32 cache is fine,
+    an f16 one is refused with IFX_E_INVALID_ARG; decode on the f32 one runs."""
+    from tests import fixtures_gguf as fx
+    p = str(tmp_path / "hd4.gguf")
+    fx.builder_llama_gguf(p, 1.0, hidden=8, heads=2)
+    g = GpuModel(p)
+    h = C.c_void_p()
+    assert _native.lib().ifx_session_create_kv(g.h, 16, 1, C.byref(h)) == 20
+    assert not h.value
+    s = g.session(16)
+    rc, lg = s.decode_step(3)
+    assert rc == 0 and np.all(np.isfinite(lg))
+    s.close()
+    g.close()
