@@ -10,7 +10,9 @@ in HBM when timing starts).
 
 Prints ONE JSON line (metric, value, roofline of the dominant kernel measured
 with HIP events over back-to-back launches, cpu_baseline of the CPU oracle on a
-bounded sample).
+bounded sample).  `value` uses the f32 KV cache (the reference's; --kv f16
+switches); `other_kv_cache` times the same decode with the other cache type,
+reported apart from `value`.
 
 Profiling aids: --no-graph launches each step's kernels directly instead of
 replaying the captured step graph (for kernel tracers); --copy-probe only runs
@@ -123,6 +125,30 @@ def prefill_flops(spec, n):
     per_row = 2 * spec.n_layers * (2 * D * D + 2 * D * KV + 3 * D * F)
     attn = spec.n_layers * spec.n_heads * (n * (n + 1) // 2) * spec.head_dim * 4
     return n * per_row + 2 * spec.vocab * D + attn
+
+
+def measure_other_kv(L, model, spec, kv_type, ctx, steps, warmup):
+    """The same decode with the other KV cache type (reported apart from `value`):
+    a fresh session, the same seeded context through the batched prefill, warmup,
+    then `steps` greedy tokens timed."""
+    from inferox_amd import synth
+    from inferox_amd._native import check
+    sess = C.c_void_p()
+    check(L.ifx_session_create_kv(model, ctx + max(steps, warmup) + 8, kv_type, C.byref(sess)), "session_create_kv")
+    out = np.zeros(max(steps, warmup, 1), np.uint32)
+    check(L.ifx_decode_greedy(sess, 1, warmup, out.ctypes.data_as(C.c_void_p)), "warmup")
+    check(L.ifx_session_clear(sess), "clear")
+    ids = synth.token_ids(ctx, spec.vocab, seed=2048)
+    check(L.ifx_prefill(sess, ids.ctypes.data_as(C.c_void_p), ids.size, None), "prefill")
+    first = C.c_uint32()
+    check(L.ifx_session_last_token(sess, C.byref(first)), "last_token")
+    check(L.ifx_stream_synchronize(None), "sync")
+    t0 = time.perf_counter()
+    check(L.ifx_decode_greedy(sess, first.value, steps, out.ctypes.data_as(C.c_void_p)), "decode")
+    wall = time.perf_counter() - t0
+    L.ifx_session_destroy(sess)
+    return {"kv_cache": "f16" if kv_type == 1 else "f32", "tok_s": round(steps / wall, 2),
+            "ms_per_step": round(wall / steps * 1e3, 4), "first_tokens": [int(x) for x in out[:4]]}
 
 
 def measure_prefill(L, model, spec, sizes, reps):
@@ -335,6 +361,10 @@ def main():
         log(f"cpu: {med:.2f} s/step; first pick cpu={toks[0]} gpu={int(out[0])}")
 
     L.ifx_session_destroy(sess)
+    other_kv = None
+    if not args.no_profile:
+        other_kv = measure_other_kv(L, model, spec, 0 if args.kv == "f16" else 1, args.ctx, K, W)
+        log(f"decode with the {other_kv['kv_cache']} KV cache: {other_kv['tok_s']} tok/s")
     prefill = None if args.no_profile else measure_prefill(
         L, model, spec, [int(x) for x in args.prefill_sizes.split(",")], 1)
     L.ifx_model_close(model)
@@ -354,6 +384,7 @@ def main():
         "device_tok_s": round(K / dev_s, 2),
         "prefill_tok_s": round(args.ctx / prefill_s, 1) if prefill_s else None,
         "prefill": prefill,
+        "other_kv_cache": other_kv,
         "kernels": prof or None,
     }
     print(json.dumps(line), flush=True)
