@@ -44,6 +44,7 @@ int device_init() {
 }
 
 static hipStream_t stream_of(void* s) { return s ? (hipStream_t)s : g_stream; }
+hipStream_t library_stream() { return g_stream; }
 
 DevW devw(const ifx_tensor* t) {
   return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal, t->L.q6_signed};
@@ -74,8 +75,14 @@ int upload_matrix(uint32_t type, const uint8_t* src, uint64_t nbytes, uint64_t r
     return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "ggml's Q8_K is not a storage type of the reference's layout");
   if (!gemv_supported(type))
     return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "tensor type %u has no device layout", type);
+  // the kernels index rows and columns in 32 bits; the product is checked so
+  // that no size below is taken modulo 2^64
+  uint64_t n_el;
+  if (rows == 0 || cols == 0 || rows >= (1ull << 31) || cols >= (1ull << 31) || !mul_u64(rows, cols, &n_el))
+    return set_error(IFX_E_INVALID_ARG, "matrix shape [%llu x %llu] out of range", (unsigned long long)rows,
+                     (unsigned long long)cols);
   uint64_t expect;
-  if (!byte_size(type, rows * cols, &expect))
+  if (!byte_size(type, n_el, &expect))
     return set_error(IFX_E_UNKNOWN_TENSOR_TYPE, "tensor type %u", type);
   if (expect != nbytes)
     return set_error(IFX_E_UNEXPECTED_EOF, "%llu bytes for a %s [%llu x %llu] matrix, %llu expected",

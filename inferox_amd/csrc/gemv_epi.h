@@ -28,7 +28,7 @@ struct EpiStore {
   __device__ void finish(Wave&, int) const {}
 };
 
-// Model::decode_step residual adds (src/model/forward.rs:450-488).
+// Layer::decode_step residual adds (src/model/forward.rs:418,437).
 struct EpiResidual {
   static constexpr bool kPaired = false, kNeighbor = false;
   float* h;
@@ -102,7 +102,7 @@ struct EpiSwiglu {
 
 // Orders floats as unsigned keys; the low word carries the row, so the max
 // key is the largest logit and, among equal logits, the last index
-// (ops::argmax, src/ops.rs:300-313).
+// (argmax, src/model/forward.rs:615-622).
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
   uint32_t b = __float_as_uint(v);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);

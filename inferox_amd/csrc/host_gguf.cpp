@@ -2,6 +2,8 @@
 #include "host_gguf.h"
 
 #include <fcntl.h>
+
+#include <algorithm>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -176,8 +178,13 @@ int read_value(Reader& r, uint32_t type, GgufValue* v) {
       if (n > r.n - r.pos) return set_error(IFX_E_IO, "unexpected end of file in an array of %llu items",
                                             (unsigned long long)n);
       v->item_type = it;
-      v->items.resize(n);
-      for (uint64_t k = 0; k < n; k++) IFX_TRY(read_value(r, it, &v->items[k]));
+      // grown item by item from a capped reservation (src/gguf/value.rs:60): a
+      // count the file cannot back ends in an io error, not in a huge allocation
+      v->items.reserve(std::min<uint64_t>(n, 1u << 20));
+      for (uint64_t k = 0; k < n; k++) {
+        v->items.emplace_back();
+        IFX_TRY(read_value(r, it, &v->items.back()));
+      }
       return IFX_OK;
     }
     case 10: { uint64_t x; IFX_TRY(r.get(&x)); v->u = x; return IFX_OK; }
@@ -202,18 +209,21 @@ int gguf_parse(const uint8_t* p, size_t n, GgufFile* out) {
   IFX_TRY(r.get(&n_tensors));
   IFX_TRY(r.get(&n_kv));
   if (n_kv > n || n_tensors > n) return set_error(IFX_E_IO, "counts exceed the file size");
-  out->meta.resize(n_kv);
+  // capped reservations, entries appended as they are read (src/gguf/file.rs:94,105)
+  out->meta.reserve(std::min<uint64_t>(n_kv, 1u << 20));
   for (uint64_t k = 0; k < n_kv; k++) {
-    GgufMeta& m = out->meta[k];
+    out->meta.emplace_back();
+    GgufMeta& m = out->meta.back();
     IFX_TRY(read_string(r, &m.key));
     uint32_t type;
     IFX_TRY(r.get(&type));
     if (type > 12) return set_error(IFX_E_UNKNOWN_VALUE_TYPE, "unknown metadata value type %u", type);
     IFX_TRY(read_value(r, type, &m.value));
   }
-  out->tensors.resize(n_tensors);
+  out->tensors.reserve(std::min<uint64_t>(n_tensors, 1u << 20));
   for (uint64_t k = 0; k < n_tensors; k++) {  // TensorInfo::read (src/gguf/tensor.rs:52-75)
-    GgufTensor& t = out->tensors[k];
+    out->tensors.emplace_back();
+    GgufTensor& t = out->tensors.back();
     IFX_TRY(read_string(r, &t.name));
     uint32_t n_dims;
     IFX_TRY(r.get(&n_dims));

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <new>
 #include <thread>
 #include <vector>
 
@@ -131,7 +132,8 @@ int upload_weight(ifx_model* m, int64_t idx, uint64_t rows, uint64_t cols, ifx_t
   uint64_t sz;
   IFX_TRY(gguf_tensor_bytes(m->gguf, m->map, idx, &data, &sz));
   const GgufTensor& t = m->gguf.tensors[idx];
-  if (t.n_elements() != rows * cols)
+  uint64_t n_el;
+  if (!mul_u64(rows, cols, &n_el) || t.n_elements() != n_el)
     return set_error(IFX_E_INVALID_ARG, "%s has %llu elements, expected %llu x %llu", t.name.c_str(),
                      (unsigned long long)t.n_elements(), (unsigned long long)rows,
                      (unsigned long long)cols);
@@ -155,7 +157,8 @@ void model_free(ifx_model* m) {
 
 int check_dims(const ifx_model* m) {
   const ifx_config& c = m->cfg;
-  if (c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.n_heads * c.head_dim != c.hidden_size ||
+  uint64_t qd;
+  if (c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || !mul_u64(c.n_heads, c.head_dim, &qd) || qd != c.hidden_size ||
       c.rope_dim > c.head_dim || (c.rope_dim & 1) || (c.head_dim & 1))
     return set_error(IFX_E_INVALID_ARG, "inconsistent attention shape (heads %llu/%llu, head_dim %llu, rope_dim %llu)",
                      (unsigned long long)c.n_heads, (unsigned long long)c.n_kv_heads,
@@ -173,7 +176,8 @@ GemvSeg seg_of(const ifx_tensor* t) {
 bool gemm_tensor_ok(const ifx_tensor* t) { return t && gemm_type(t->L.type) && gemm_layout_ok(t->L); }
 bool gemm_eligible(const ifx_model* m) {
   const ifx_config& c = m->cfg;
-  if (!attn_prefill_head_dim((uint32_t)c.head_dim) || c.hidden_size != c.n_heads * c.head_dim ||
+  uint64_t qd;
+  if (!attn_prefill_head_dim((uint32_t)c.head_dim) || !mul_u64(c.n_heads, c.head_dim, &qd) || c.hidden_size != qd ||
       c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.rope_dim > c.head_dim || c.rope_dim % 2)
     return false;
   if (!gemm_tensor_ok(m->output)) return false;
@@ -479,6 +483,8 @@ void session_free(ifx_session* s) {
   delete s;
 }
 
+int model_open(const char* path, uint32_t flags, ifx_model** out);
+
 }  // namespace
 
 extern "C" {
@@ -490,6 +496,20 @@ int ifx_model_open_ex(const char* path, uint32_t flags, ifx_model** out) {
   if (!out) return set_error(IFX_E_INVALID_ARG, "null output");
   *out = nullptr;
   if (flags & ~(uint32_t)IFX_OPEN_GGML_KQUANTS) return set_error(IFX_E_INVALID_ARG, "unknown flags %#x", flags);
+  // host allocations sized from the file (metadata, staging of a matrix) may
+  // fail; that is a status here, never an exception across the C ABI
+  try {
+    return model_open(path, flags, out);
+  } catch (const std::bad_alloc&) {
+    return set_error(IFX_E_OOM, "out of host memory opening %s", path ? path : "(null)");
+  }
+}
+
+}  // extern "C"
+
+namespace {
+
+int model_open(const char* path, uint32_t flags, ifx_model** out) {
   ifx_model* m = new ifx_model();
   m->flags = flags;
   int rc = m->map.open(path);
@@ -525,17 +545,21 @@ int ifx_model_open_ex(const char* path, uint32_t flags, ifx_model** out) {
   c.context_length = f.get_u32("llama.context_length", &u) ? u : 4096;
   c.vocab_size = f.get_u32("llama.vocab_size", &u) ? u : 0;
 
-  // name resolution (src/model/mod.rs:34-48,64-92)
-  std::vector<int64_t> idx(c.n_layers * 9);
+  // name resolution (src/model/mod.rs:34-48,64-92).  block_count comes from
+  // the file: the indices grow one layer at a time, so a count larger than the
+  // file's tensors can hold ends at the first missing blk.N tensor
+  // (TensorNotFound, as the reference reports it) without sizing anything by it.
+  std::vector<int64_t> idx;
   for (uint64_t l = 0; l < c.n_layers; l++)
     for (int r = 0; r < 9; r++) {
       char nm[128];
       snprintf(nm, sizeof nm, "blk.%llu.%s.weight", (unsigned long long)l, kRoleNames[r]);
-      idx[l * 9 + r] = f.tensor_index(nm);
-      if (idx[l * 9 + r] < 0) {
+      const int64_t ti = f.tensor_index(nm);
+      if (ti < 0) {
         model_free(m);
         return set_error(IFX_E_TENSOR_NOT_FOUND, "blk.%llu.*", (unsigned long long)l);
       }
+      idx.push_back(ti);
     }
   int64_t i_embd = f.tensor_index("token_embd.weight");
   if (i_embd < 0) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "token_embd.weight"); }
@@ -586,6 +610,10 @@ int ifx_model_open_ex(const char* path, uint32_t flags, ifx_model** out) {
   return IFX_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
 void ifx_model_close(ifx_model* m) { model_free(m); }
 
 int ifx_model_config(const ifx_model* m, ifx_config* out) {
@@ -622,10 +650,17 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
   const uint64_t D = c.hidden_size, F = c.intermediate_size, kvd = c.n_kv_heads * c.head_dim;
   const uint64_t G = c.n_heads / c.n_kv_heads;
   s->max_chunks = (uint32_t)((max_seq_len + s->attn_chunk - 1) / s->attn_chunk);
+  // bytes of the K (and of the V) cache, refused when they do not fit in 64 bits
+  uint64_t kv_bytes = 0;
+  if (!mul_u64(c.n_layers, max_seq_len, &kv_bytes) || !mul_u64(kv_bytes, kvd, &kv_bytes) ||
+      !mul_u64(kv_bytes, s->kv_es, &kv_bytes)) {
+    delete s;
+    return set_error(IFX_E_OOM, "a KV cache of %llu rows does not fit in memory", (unsigned long long)max_seq_len);
+  }
   int rc = IFX_OK;
   auto A = [&](void** p, size_t b) { if (rc == IFX_OK) rc = dev_alloc(s->allocs, p, b); };
-  A((void**)&s->kc, c.n_layers * max_seq_len * kvd * s->kv_es);
-  A((void**)&s->vc, c.n_layers * max_seq_len * kvd * s->kv_es);
+  A((void**)&s->kc, kv_bytes);
+  A((void**)&s->vc, kv_bytes);
   A((void**)&s->hidden, D * 4);
   A((void**)&s->q, D * 4);
   A((void**)&s->attn, D * 4);
@@ -663,8 +698,7 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
   init.top_p = 1.0f;
   if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(s->kc, 0, c.n_layers * max_seq_len * kvd * s->kv_es) != hipSuccess ||
-      hipMemset(s->vc, 0, c.n_layers * max_seq_len * kvd * s->kv_es) != hipSuccess ||
+      hipMemset(s->kc, 0, kv_bytes) != hipSuccess || hipMemset(s->vc, 0, kv_bytes) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     session_free(s);
     return set_error(IFX_E_HIP, "session initialisation failed");

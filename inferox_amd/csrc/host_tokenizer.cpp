@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <new>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -566,7 +567,11 @@ int ifx_tokenizer_from_json(const char* json, uint64_t len, ifx_tokenizer** out)
   clear_error();
   if (!out || (!json && len)) return set_error(IFX_E_INVALID_ARG, "null argument");
   *out = nullptr;
-  return tokenizer_from_json(json ? json : "", (size_t)len, out);
+  try {
+    return tokenizer_from_json(json ? json : "", (size_t)len, out);
+  } catch (const std::bad_alloc&) {
+    return set_error(IFX_E_OOM, "out of memory reading a tokenizer");
+  }
 }
 
 int ifx_tokenizer_from_file(const char* path, ifx_tokenizer** out) {
@@ -575,14 +580,20 @@ int ifx_tokenizer_from_file(const char* path, ifx_tokenizer** out) {
   *out = nullptr;
   FILE* f = fopen(path, "rb");
   if (!f) return set_error(IFX_E_IO, "io error: cannot open %s", path);
-  std::string raw;
-  char buf[1 << 16];
-  size_t n;
-  while ((n = fread(buf, 1, sizeof buf, f)) > 0) raw.append(buf, n);
-  const bool err = ferror(f) != 0;
-  fclose(f);
-  if (err) return set_error(IFX_E_IO, "io error: reading %s", path);
-  return tokenizer_from_json(raw.data(), raw.size(), out);
+  try {
+    std::string raw;
+    char buf[1 << 16];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof buf, f)) > 0) raw.append(buf, n);
+    const bool err = ferror(f) != 0;
+    fclose(f);
+    f = nullptr;
+    if (err) return set_error(IFX_E_IO, "io error: reading %s", path);
+    return tokenizer_from_json(raw.data(), raw.size(), out);
+  } catch (const std::bad_alloc&) {
+    if (f) fclose(f);
+    return set_error(IFX_E_OOM, "out of memory reading %s", path);
+  }
 }
 
 void ifx_tokenizer_free(ifx_tokenizer* t) { delete t; }

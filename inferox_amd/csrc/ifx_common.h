@@ -31,6 +31,9 @@ void clear_error();
     if (s_ != IFX_OK) return s_; \
   } while (0)
 
+// a * b when it fits in 64 bits (sizes taken from a file are multiplied with this)
+inline bool mul_u64(uint64_t a, uint64_t b, uint64_t* out) { return !__builtin_mul_overflow(a, b, out); }
+
 // ---------------------------------------------------------------------------
 // GGML tensor types (src/gguf/types.rs:70-229)
 // ---------------------------------------------------------------------------

@@ -30,7 +30,6 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 64;       // cache rows per workgroup (4 threads per row for the scores)
 constexpr int kMaxGroup = 8;
 constexpr int kMaxHd = 256;
-constexpr int kMaxMerge = 256;   // chunks per kv head (max_seq <= kMaxMerge * kChunk)
 constexpr int kMergeBatch = 8;   // partial o loads in flight per merging thread
 
 __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
@@ -329,12 +328,15 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
 // Combines the chunk records of query head h = blockIdx.x (kv head h / G):
 // o_h = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - M), M = max_c m_c
 // (softmax over all cached rows, src/model/forward.rs:398-409, taken chunk by
-// chunk).  Thread (split sp, float4 column): the chunks sp, sp + nsplit, ...;
-// the first batch of o loads is in flight while wave 0 forms the weights.
+// chunk).  Any number of chunks: M and the denominator are reduced over the
+// workgroup (thread t reads chunks t, t + 256, ...), then the weights are
+// staged in LDS 256 chunks at a time.  Thread (split sp, float4 column) sums
+// the batch's chunks sp, sp + nsplit, ...; the first loads of o are in flight
+// while M is formed.
 template <int HDT, int GT>
 __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
-  __shared__ float cw[kMaxMerge];
-  __shared__ float den_s;
+  __shared__ float cw[kThreads];
+  __shared__ float wred[2][kThreads / 64];
   __shared__ float4 red[kThreads];
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
   const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
@@ -346,6 +348,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
   if (nch == 0) return;
   const uint32_t rec = attn_partial_floats(G, HD);
   const float* base = a.partial + (uint64_t)hk * a.max_chunks * rec;
+  const float* ml = base + G * HD;  // chunk c: max at ml[c rec + g], sum at ml[c rec + G + g]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t nsplit = kThreads / nc4, sp = tid / nc4, col = tid % nc4;
   const bool worker = sp < nsplit;  // nc4 need not divide the workgroup
@@ -355,47 +358,49 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
     const uint32_t c = min(min(sp, nsplit - 1) + nsplit * k, nch - 1);  // clamped: loads stay unconditional
     ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
   }
-  if (wave == 0) {
-    float m[kMaxMerge / 64], l[kMaxMerge / 64];
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMaxMerge / 64; j++) {
-      const uint32_t c = lane + 64 * j;
-      const uint64_t at = (uint64_t)min(c, nch - 1) * rec + G * HD;
-      const float mv = base[at + g];
-      m[j] = c < nch ? mv : -INFINITY;
-      l[j] = base[at + G + g];
-      M = fmaxf(M, m[j]);
-    }
-    M = wave_max_dpp(M);
-    float den = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMaxMerge / 64; j++) {
-      const uint32_t c = lane + 64 * j;
-      const float w = c < nch ? expf(m[j] - M) : 0.f;
-      cw[c] = w;
-      den = fmaf(l[j], w, den);
-    }
-    den = wave_sum_dpp(den);
-    if (lane == 0) den_s = den;
+  // M over every chunk (chunk tid's max and sum are kept for the first batch)
+  float m0, l0;
+  {
+    const uint64_t at = (uint64_t)min((uint32_t)tid, nch - 1) * rec;
+    const float mv = ml[at + g], lv = ml[at + G + g];
+    m0 = (uint32_t)tid < nch ? mv : -INFINITY;
+    l0 = (uint32_t)tid < nch ? lv : 0.f;
   }
+  float M = m0;
+  for (uint32_t c = tid + kThreads; c < nch; c += kThreads) M = fmaxf(M, ml[(uint64_t)c * rec + g]);
+  M = wave_max_dpp(M);
+  if (lane == 0) wred[0][wave] = M;
   __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; w++) M = fmaxf(M, wred[0][w]);
+  const float w0 = (uint32_t)tid < nch ? expf(m0 - M) : 0.f;
+  float den = l0 * w0;
+  for (uint32_t c = tid + kThreads; c < nch; c += kThreads)
+    den = fmaf(ml[(uint64_t)c * rec + G + g], expf(ml[(uint64_t)c * rec + g] - M), den);
+  den = wave_sum_dpp(den);
+  if (lane == 0) wred[1][wave] = den;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (worker) {
-    for (uint32_t c0 = sp;; c0 += nsplit * kMergeBatch) {
-      if (c0 != sp) {
+  for (uint32_t b = 0; b < nch; b += kThreads) {
+    if (b) __syncthreads();  // the previous batch's weights are no longer read
+    cw[tid] = b == 0 ? w0 : (b + tid < nch ? expf(ml[(uint64_t)(b + tid) * rec + g] - M) : 0.f);
+    __syncthreads();
+    if (worker) {
+      const uint32_t end = min(nch, b + (uint32_t)kThreads);
+      for (uint32_t c0 = b + sp;; c0 += nsplit * kMergeBatch) {
+        if (c0 != sp) {
+#pragma unroll
+          for (int k = 0; k < kMergeBatch; k++) {
+            const uint32_t c = min(c0 + nsplit * k, nch - 1);
+            ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+          }
+        }
 #pragma unroll
         for (int k = 0; k < kMergeBatch; k++) {
-          const uint32_t c = min(c0 + nsplit * k, nch - 1);
-          ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+          const uint32_t c = c0 + nsplit * k;
+          if (c < end) acc = fma4(cw[c - b], ov[k], acc);
         }
+        if (c0 + nsplit * kMergeBatch >= end) break;
       }
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; k++) {
-        const uint32_t c = c0 + nsplit * k;
-        if (c < nch) acc = fma4(cw[c], ov[k], acc);
-      }
-      if (c0 + nsplit * kMergeBatch >= nch) break;
     }
   }
   red[tid] = acc;
@@ -403,8 +408,10 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
   if ((uint32_t)tid < nc4) {
     float4 o = red[tid];
     for (uint32_t q = 1; q < nsplit; q++) o = add4(o, red[q * nc4 + tid]);
-    const float den = den_s;
-    ((float4*)(a.out + (uint64_t)h * HD))[tid] = make_float4(o.x / den, o.y / den, o.z / den, o.w / den);
+    float dsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) dsum += wred[1][w];
+    ((float4*)(a.out + (uint64_t)h * HD))[tid] = make_float4(o.x / dsum, o.y / dsum, o.z / dsum, o.w / dsum);
   }
 }
 
@@ -434,7 +441,7 @@ bool attn_decode_head_dim(uint32_t head_dim, bool kv_f16) {
 
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
   if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > kMaxGroup ||
-      !attn_decode_head_dim(a.head_dim, a.kv_f16) || a.chunk != kChunk || a.max_chunks > kMaxMerge ||
+      !attn_decode_head_dim(a.head_dim, a.kv_f16) || a.chunk != kChunk ||
       a.max_chunks == 0)
     return hipErrorInvalidValue;
   if (a.kv_f16) launch_typed<_Float16>(a, st);

@@ -61,6 +61,9 @@ _SIGS = {
     "orc_set_threads": (None, [i32]),
     "orc_decode_step": (i32, [vp, vp, u32, vp, i32, i32]),
     "orc_prefill": (i32, [vp, vp, vp, u64, vp, i32, i32]),
+    "orc_prefill_rows": (i32, [vp, vp, vp, u64, vp, u64, vp, i32, i32]),
+    "orc_dequantize_fast": (i32, [u32, u64, vp, vp]),
+    "orc_forward_rows": (i32, [vp, vp, u64, vp, u64, vp, i32]),
     "orc_forward": (i32, [vp, vp, u64, vp, i32]),
     "orc_generate": (i32, [vp, vp, vp, u64, u64, vp, i32, i32]),
 }
@@ -93,6 +96,14 @@ def dequantize(ggml_type: int, raw: np.ndarray, n_elements: int, n_out: int | No
     out = np.zeros(max(n_out, 1), dtype=np.float32)
     rc = lib().orc_dequantize_f32(ggml_type, n_elements, _ptr(raw), raw.size, _ptr(out), n_out)
     return rc, out[:n_out]
+
+
+def dequantize_fast(ggml_type: int, raw: np.ndarray, n_elements: int):
+    """The FAST-mode dequantization of whole blocks (equals dequantize)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.zeros(max(n_elements, 1), dtype=np.float32)
+    rc = lib().orc_dequantize_fast(ggml_type, n_elements, _ptr(raw), _ptr(out))
+    return rc, out[:n_elements]
 
 
 def matmul_t(a: np.ndarray, b: np.ndarray, m: int, n: int, k: int, scalar: bool = False):
@@ -230,6 +241,23 @@ class Model:
         logits = np.zeros(max(ids.size * self.vocab, 1), dtype=np.float32)
         rc = lib().orc_prefill(self.h, kv.h, _ptr(ids), ids.size, _ptr(logits), mode, rope_mode)
         return rc, logits[: ids.size * self.vocab].reshape(ids.size, self.vocab)
+
+    def prefill_rows(self, kv: "KvCache", ids, rows, mode=MODE_FAST, rope_mode=ROPE_REFERENCE):
+        """prefill, with the logits of the listed rows only ([len(rows) x vocab])."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        rows = np.ascontiguousarray(rows, dtype=np.uint64)
+        logits = np.zeros(max(rows.size * self.vocab, 1), dtype=np.float32)
+        rc = lib().orc_prefill_rows(self.h, kv.h, _ptr(ids), ids.size, _ptr(rows), rows.size, _ptr(logits), mode,
+                                    rope_mode)
+        return rc, logits[: rows.size * self.vocab].reshape(rows.size, self.vocab)
+
+    def forward_rows(self, ids, rows, mode=MODE_FAST):
+        """forward, with the logits of the listed rows only ([len(rows) x vocab])."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        rows = np.ascontiguousarray(rows, dtype=np.uint64)
+        logits = np.zeros(max(rows.size * self.vocab, 1), dtype=np.float32)
+        rc = lib().orc_forward_rows(self.h, _ptr(ids), ids.size, _ptr(rows), rows.size, _ptr(logits), mode)
+        return rc, logits[: rows.size * self.vocab].reshape(rows.size, self.vocab)
 
     def forward(self, ids, mode=MODE_FAST):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)

@@ -702,8 +702,14 @@ int orc_model_open(const char* path, orc_model** out) {
   c->context_length = get_u32(m, "llama.context_length", &u) ? u : 4096;
   c->vocab_size = get_u32(m, "llama.vocab_size", &u) ? u : 0;
 
-  /* Model::open / Layer::from_weights name resolution */
-  m->layers = (orc_layer*)calloc(c->n_layers ? c->n_layers : 1, sizeof(orc_layer));
+  /* Model::open / Layer::from_weights name resolution.  Every layer needs 9
+   * distinct tensors, so a block_count beyond n_tensors / 9 meets a missing
+   * blk.N tensor (TensorNotFound) before the array sized here runs out. */
+  {
+    uint64_t cap = c->n_layers < m->n_tensors / 9 + 1 ? c->n_layers : m->n_tensors / 9 + 1;
+    m->layers = (orc_layer*)calloc(cap ? cap : 1, sizeof(orc_layer));
+    if (!m->layers) { rc = ORC_E_OOM; goto fail; }
+  }
   static const char* names[9] = {"attn_norm", "attn_q",   "attn_k", "attn_v",  "attn_output",
                                  "ffn_norm",  "ffn_gate", "ffn_up", "ffn_down"};
   for (uint64_t l = 0; l < c->n_layers; l++) {
@@ -822,6 +828,191 @@ static int tensor_f32(const orc_model* m, int64_t idx, float** out, uint64_t* n_
   return ORC_OK;
 }
 
+/* ------------------------------------------------------------------------- */
+/* FAST-mode kernels.  Same values as the restatements above, computed with    */
+/* AVX2: every element and every output sees the same IEEE operations in the  */
+/* same order (no fusion beyond the explicit 8-lane FMA of matmul_t), so FAST  */
+/* equals FAITHFUL bit for bit; only independent work is interleaved.          */
+/* ------------------------------------------------------------------------- */
+
+/* 8 bytes (low half of v) as 8 floats */
+static inline __m256 u8x8_to_ps(__m128i v) { return _mm256_cvtepi32_ps(_mm256_cvtepu8_epi32(v)); }
+
+/* dq_q4_k: per group y = (dall * f32(q)) - dm with the nibble order of
+ * dequant.rs:155-159 (element 2i = low nibble of byte i, 2i+1 = high). */
+static void dq_q4_k_fast(const uint8_t* src, uint64_t nb, float* out) {
+  const __m128i m4 = _mm_set1_epi8(15);
+  for (uint64_t b = 0; b < nb; b++) {
+    const uint8_t* blk = src + b * 144;
+    const float d = ld_f16(blk), dmin = ld_f16(blk + 2);
+    const uint8_t* s = blk + 4;
+    const uint8_t* qs = blk + 16;
+    for (int g = 0; g < 8; g++) {
+      uint32_t sc, mn;
+      if (g < 4) {
+        sc = s[g] & 63u;
+        mn = s[g + 4] & 63u;
+      } else {
+        sc = (s[g + 4] & 15u) | ((uint32_t)(s[g - 4] >> 6) << 4);
+        mn = (uint32_t)(s[g + 4] >> 4) | ((uint32_t)(s[g] >> 6) << 4);
+      }
+      const __m256 vd = _mm256_set1_ps(d * (float)sc), vm = _mm256_set1_ps(dmin * (float)mn);
+      const __m128i raw = _mm_loadu_si128((const __m128i*)(qs + 16 * g));
+      const __m128i lo = _mm_and_si128(raw, m4), hi = _mm_and_si128(_mm_srli_epi16(raw, 4), m4);
+      const __m128i e0 = _mm_unpacklo_epi8(lo, hi), e1 = _mm_unpackhi_epi8(lo, hi);
+      float* o = out + b * 256 + 32 * g;
+      _mm256_storeu_ps(o, _mm256_sub_ps(_mm256_mul_ps(vd, u8x8_to_ps(e0)), vm));
+      _mm256_storeu_ps(o + 8, _mm256_sub_ps(_mm256_mul_ps(vd, u8x8_to_ps(_mm_srli_si128(e0, 8))), vm));
+      _mm256_storeu_ps(o + 16, _mm256_sub_ps(_mm256_mul_ps(vd, u8x8_to_ps(e1)), vm));
+      _mm256_storeu_ps(o + 24, _mm256_sub_ps(_mm256_mul_ps(vd, u8x8_to_ps(_mm_srli_si128(e1, 8))), vm));
+    }
+  }
+}
+
+/* the four 2-bit fields of a qh byte, one per byte of the word (element j of
+ * the four takes bits 2j, 2j+1: dequant.rs:189-192) */
+static uint32_t g_qh4[256];
+__attribute__((constructor)) static void qh4_init(void) {
+  for (int v = 0; v < 256; v++)
+    g_qh4[v] = (uint32_t)(v & 3) | ((uint32_t)((v >> 2) & 3) << 8) | ((uint32_t)((v >> 4) & 3) << 16) |
+               ((uint32_t)((v >> 6) & 3) << 24);
+}
+
+/* dq_q6_k: y = (d * f32(u8 sc)) * f32(q - 32) per 16-element part */
+static void dq_q6_k_fast(const uint8_t* src, uint64_t nb, float* out) {
+  const __m128i m4 = _mm_set1_epi8(15);
+  const __m256i c32 = _mm256_set1_epi32(32);
+  for (uint64_t b = 0; b < nb; b++) {
+    const uint8_t* blk = src + b * 210;
+    const float d = ld_f16(blk);
+    const uint8_t *sc = blk + 2, *ql = blk + 18, *qh = blk + 146;
+    for (int part = 0; part < 16; part++) {
+      /* elements 16 part .. +15: ql bytes 8 part .. +7, qh bytes 4 part .. +3 */
+      const __m128i raw = _mm_loadl_epi64((const __m128i*)(ql + 8 * part));
+      const __m128i lo = _mm_unpacklo_epi8(_mm_and_si128(raw, m4), _mm_and_si128(_mm_srli_epi16(raw, 4), m4));
+      const __m128i hi = _mm_set_epi32((int)g_qh4[qh[4 * part + 3]], (int)g_qh4[qh[4 * part + 2]],
+                                       (int)g_qh4[qh[4 * part + 1]], (int)g_qh4[qh[4 * part]]);
+      const __m128i q = _mm_or_si128(lo, _mm_slli_epi16(hi, 4));
+      const __m256 vs = _mm256_set1_ps(d * (float)sc[part]);
+      float* o = out + b * 256 + 16 * part;
+      _mm256_storeu_ps(o, _mm256_mul_ps(vs, _mm256_cvtepi32_ps(_mm256_sub_epi32(_mm256_cvtepu8_epi32(q), c32))));
+      _mm256_storeu_ps(o + 8, _mm256_mul_ps(vs, _mm256_cvtepi32_ps(
+                                                    _mm256_sub_epi32(_mm256_cvtepu8_epi32(_mm_srli_si128(q, 8)), c32))));
+    }
+  }
+}
+
+/* dq_q8_0: y = f32(i8 q) * delta */
+static void dq_q8_0_fast(const uint8_t* src, uint64_t nb, float* out) {
+  for (uint64_t b = 0; b < nb; b++) {
+    const uint8_t* blk = src + b * 34;
+    const __m256 vd = _mm256_set1_ps(ld_f16(blk));
+    for (int h = 0; h < 4; h++) {
+      const __m128i raw = _mm_loadl_epi64((const __m128i*)(blk + 2 + 8 * h));
+      _mm256_storeu_ps(out + b * 32 + 8 * h, _mm256_mul_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(raw)), vd));
+    }
+  }
+}
+
+static int dq_units_fast(uint32_t t, const uint8_t* src, uint64_t nunits, float* out) {
+  switch (t) {
+    case T_Q4K: dq_q4_k_fast(src, nunits, out); return ORC_OK;
+    case T_Q6K: dq_q6_k_fast(src, nunits, out); return ORC_OK;
+    case T_Q8_0: dq_q8_0_fast(src, nunits, out); return ORC_OK;
+    default: return dq_units(t, src, nunits, out);
+  }
+}
+
+static int dq_range_fast(uint32_t t, const uint8_t* data, uint64_t e0, uint64_t n, float* out,
+                         float* scratch) {
+  uint64_t ue, ub;
+  int rc = unit_of(t, &ue, &ub);
+  if (rc) return rc;
+  uint64_t u0 = e0 / ue, u1 = (e0 + n + ue - 1) / ue;
+  if (u0 * ue == e0 && u1 * ue == e0 + n) return dq_units_fast(t, data + u0 * ub, u1 - u0, out);
+  rc = dq_units_fast(t, data + u0 * ub, u1 - u0, scratch);
+  memcpy(out, scratch + (e0 - u0 * ue), n * 4);
+  return rc;
+}
+
+/* Test hook: dequantize_f32 through the FAST routines (must equal the restatement). */
+int orc_dequantize_fast(uint32_t t, uint64_t n_elements, const uint8_t* bytes, float* out) {
+  uint64_t ue, ub;
+  if (unit_of(t, &ue, &ub) != ORC_OK || n_elements % ue) return ORC_E_INVALID_ARG;
+  return dq_units_fast(t, bytes, n_elements / ue, out);
+}
+
+/* dot_ref's hsum tree and scalar tail, from a finished 8-lane accumulator */
+static inline float finish_ref(__m256 acc, const float* a, const float* b, uint64_t l, uint64_t k) {
+  float lane[8];
+  _mm256_storeu_ps(lane, acc);
+  float s0 = lane[0] + lane[4], s1 = lane[1] + lane[5], s2 = lane[2] + lane[6], s3 = lane[3] + lane[7];
+  float sum = (s0 + s1) + (s2 + s3);
+  for (; l < k; l++) sum = sum + a[l] * b[l];
+  return sum;
+}
+
+/* 3 rows of a x 4 rows of w: twelve dot_ref chains advanced together */
+static inline void tile_3x4(const float* a0, const float* a1, const float* a2, const float* w0, const float* w1,
+                            const float* w2, const float* w3, uint64_t k, float* c, uint64_t ldc) {
+  __m256 c00 = _mm256_setzero_ps(), c01 = c00, c02 = c00, c03 = c00, c10 = c00, c11 = c00, c12 = c00, c13 = c00,
+         c20 = c00, c21 = c00, c22 = c00, c23 = c00;
+  uint64_t l = 0;
+  for (; l + 8 <= k; l += 8) {
+    const __m256 x0 = _mm256_loadu_ps(a0 + l), x1 = _mm256_loadu_ps(a1 + l), x2 = _mm256_loadu_ps(a2 + l);
+    __m256 y = _mm256_loadu_ps(w0 + l);
+    c00 = _mm256_fmadd_ps(x0, y, c00); c10 = _mm256_fmadd_ps(x1, y, c10); c20 = _mm256_fmadd_ps(x2, y, c20);
+    y = _mm256_loadu_ps(w1 + l);
+    c01 = _mm256_fmadd_ps(x0, y, c01); c11 = _mm256_fmadd_ps(x1, y, c11); c21 = _mm256_fmadd_ps(x2, y, c21);
+    y = _mm256_loadu_ps(w2 + l);
+    c02 = _mm256_fmadd_ps(x0, y, c02); c12 = _mm256_fmadd_ps(x1, y, c12); c22 = _mm256_fmadd_ps(x2, y, c22);
+    y = _mm256_loadu_ps(w3 + l);
+    c03 = _mm256_fmadd_ps(x0, y, c03); c13 = _mm256_fmadd_ps(x1, y, c13); c23 = _mm256_fmadd_ps(x2, y, c23);
+  }
+  c[0] = finish_ref(c00, a0, w0, l, k); c[1] = finish_ref(c01, a0, w1, l, k);
+  c[2] = finish_ref(c02, a0, w2, l, k); c[3] = finish_ref(c03, a0, w3, l, k);
+  c[ldc] = finish_ref(c10, a1, w0, l, k); c[ldc + 1] = finish_ref(c11, a1, w1, l, k);
+  c[ldc + 2] = finish_ref(c12, a1, w2, l, k); c[ldc + 3] = finish_ref(c13, a1, w3, l, k);
+  c[2 * ldc] = finish_ref(c20, a2, w0, l, k); c[2 * ldc + 1] = finish_ref(c21, a2, w1, l, k);
+  c[2 * ldc + 2] = finish_ref(c22, a2, w2, l, k); c[2 * ldc + 3] = finish_ref(c23, a2, w3, l, k);
+}
+
+/* 1 row of a x 4 rows of w */
+static inline void tile_1x4(const float* a0, const float* w0, const float* w1, const float* w2, const float* w3,
+                            uint64_t k, float* c) {
+  __m256 c0 = _mm256_setzero_ps(), c1 = c0, c2 = c0, c3 = c0;
+  uint64_t l = 0;
+  for (; l + 8 <= k; l += 8) {
+    const __m256 x = _mm256_loadu_ps(a0 + l);
+    c0 = _mm256_fmadd_ps(x, _mm256_loadu_ps(w0 + l), c0);
+    c1 = _mm256_fmadd_ps(x, _mm256_loadu_ps(w1 + l), c1);
+    c2 = _mm256_fmadd_ps(x, _mm256_loadu_ps(w2 + l), c2);
+    c3 = _mm256_fmadd_ps(x, _mm256_loadu_ps(w3 + l), c3);
+  }
+  c[0] = finish_ref(c0, a0, w0, l, k); c[1] = finish_ref(c1, a0, w1, l, k);
+  c[2] = finish_ref(c2, a0, w2, l, k); c[3] = finish_ref(c3, a0, w3, l, k);
+}
+
+/* c[m x n] = a . W^T for W rows [j0, j0 + jn) held dequantized in wb (jn x k) */
+static void tiles(const float* a, uint64_t m, uint64_t k, const float* wb, uint64_t jn, uint64_t j0, float* c,
+                  uint64_t n) {
+  uint64_t i = 0;
+  for (; i + 3 <= m; i += 3) {
+    uint64_t r = 0;
+    for (; r + 4 <= jn; r += 4)
+      tile_3x4(a + i * k, a + (i + 1) * k, a + (i + 2) * k, wb + r * k, wb + (r + 1) * k, wb + (r + 2) * k,
+               wb + (r + 3) * k, k, c + i * n + j0 + r, n);
+    for (; r < jn; r++)
+      for (uint64_t ii = i; ii < i + 3; ii++) c[ii * n + j0 + r] = dot_ref(a + ii * k, wb + r * k, k);
+  }
+  for (; i < m; i++) {
+    uint64_t r = 0;
+    for (; r + 4 <= jn; r += 4)
+      tile_1x4(a + i * k, wb + r * k, wb + (r + 1) * k, wb + (r + 2) * k, wb + (r + 3) * k, k, c + i * n + j0 + r);
+    for (; r < jn; r++) c[i * n + j0 + r] = dot_ref(a + i * k, wb + r * k, k);
+  }
+}
+
 /* c[m x n] = a[m x k] . W^T with W = tensor idx ([n, k]) in the matmul_t order.
  * FAITHFUL dequantizes the whole tensor first (as the reference does on every
  * call); FAST dequantizes one row at a time inside a parallel loop.  Each c[i][j]
@@ -843,20 +1034,27 @@ static int linear(const orc_model* mdl, int64_t idx, const float* a, uint64_t m,
   }
   uint64_t ue, ub;
   if ((rc = unit_of(t->type, &ue, &ub))) return rc;
+  /* blocks of JB weight rows, dequantized once and swept by every row of a in
+   * 3 x 4 register tiles (the block stays in cache while a streams past) */
+  const uint64_t JB = m == 1 ? 16 : 64, nblk = (n + JB - 1) / JB;
   int err = ORC_OK;
 #pragma omp parallel
   {
-    float* row = (float*)malloc((k + 2 * ue) * 4);
+    float* wb = (float*)malloc((JB * k + 2 * ue) * 4);
     float* scratch = (float*)malloc((k + 2 * ue) * 4);
-#pragma omp for schedule(static)
-    for (uint64_t j = 0; j < n; j++) {
-      if (dq_range(t->type, data, j * k, k, row, scratch) != ORC_OK) {
+#pragma omp for schedule(dynamic, 1)
+    for (uint64_t bj = 0; bj < nblk; bj++) {
+      const uint64_t j0 = bj * JB, jn = n - j0 < JB ? n - j0 : JB;
+      int bad = 0;
+      for (uint64_t r = 0; r < jn; r++)
+        if (dq_range_fast(t->type, data, (j0 + r) * k, k, wb + r * k, scratch) != ORC_OK) bad = 1;
+      if (bad) {
         err = ORC_E_UNKNOWN_TENSOR_TYPE;
         continue;
       }
-      for (uint64_t i = 0; i < m; i++) c[i * n + j] = dot_ref(a + i * k, row, k);
+      tiles(a, m, k, wb, jn, j0, c, n);
     }
-    free(row);
+    free(wb);
     free(scratch);
   }
   return err;
@@ -906,6 +1104,28 @@ static int check_dims(const orc_model* m) {
   return ORC_OK;
 }
 
+/* One query head of the decode attention (src/model/forward.rs:383-414):
+ * s_t = (sum_d q_d k_td) / sqrt(hd) in sequence, softmax_rows, o_d = sum_t p_t v_td. */
+static void decode_head(const float* q, const float* kc, const float* vc, uint64_t nl, uint64_t h, uint64_t grp,
+                        uint64_t hd, uint64_t kvd, float* scores, float* head_out, float* attn) {
+  uint64_t hk = h / grp;
+  const float* qh = q + h * hd;
+  float rs = sqrtf((float)hd);
+  for (uint64_t t = 0; t < nl; t++) {
+    const float* kh = kc + t * kvd + hk * hd;
+    float s = 0.0f;
+    for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
+    scores[t] = s / rs;
+  }
+  orc_softmax_rows(scores, 1, nl);
+  for (uint64_t d = 0; d < hd; d++) head_out[d] = 0.0f;
+  for (uint64_t t = 0; t < nl; t++) {
+    const float* vh = vc + t * kvd + hk * hd;
+    for (uint64_t d = 0; d < hd; d++) head_out[d] = head_out[d] + scores[t] * vh[d];
+  }
+  memcpy(attn + h * hd, head_out, hd * 4);
+}
+
 /* Layer::decode_step (src/model/forward.rs:344-440). */
 static int layer_decode(const orc_model* m, const orc_layer* L, float* kc, float* vc,
                         uint64_t cache_len, float* hidden, int mode, int rope_mode, int kv16) {
@@ -935,23 +1155,20 @@ static int layer_decode(const orc_model* m, const orc_layer* L, float* kc, float
   memcpy(kc + cache_len * kvd, k, kvd * 4);
   memcpy(vc + cache_len * kvd, v, kvd * 4);
   uint64_t nl = cache_len + 1;
-  float rs = sqrtf((float)hd);
-  for (uint64_t h = 0; h < c->n_heads; h++) {
-    uint64_t hk = h / grp;
-    const float* qh = q + h * hd;
-    for (uint64_t t = 0; t < nl; t++) {
-      const float* kh = kc + t * kvd + hk * hd;
-      float s = 0.0f;
-      for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
-      scores[t] = s / rs;
+  if (mode == ORC_MODE_FAITHFUL) {
+    for (uint64_t h = 0; h < c->n_heads; h++)
+      decode_head(q, kc, vc, nl, h, grp, hd, kvd, scores, head_out, attn);
+  } else {
+    /* the heads are independent: FAST runs them in parallel, each exactly as above */
+#pragma omp parallel
+    {
+      float* sc_t = (float*)malloc(nl * 4);
+      float* ho_t = (float*)malloc(hd * 4);
+#pragma omp for schedule(static)
+      for (uint64_t h = 0; h < c->n_heads; h++) decode_head(q, kc, vc, nl, h, grp, hd, kvd, sc_t, ho_t, attn);
+      free(sc_t);
+      free(ho_t);
     }
-    orc_softmax_rows(scores, 1, nl);
-    for (uint64_t d = 0; d < hd; d++) head_out[d] = 0.0f;
-    for (uint64_t t = 0; t < nl; t++) {
-      const float* vh = vc + t * kvd + hk * hd;
-      for (uint64_t d = 0; d < hd; d++) head_out[d] = head_out[d] + scores[t] * vh[d];
-    }
-    memcpy(attn + h * hd, head_out, hd * 4);
   }
   if ((rc = linear(m, L->attn_output, attn, 1, H, H, hidden, mode))) goto done;
   orc_add_in_place(hidden, residual, H);
@@ -996,6 +1213,62 @@ done:
   return rc;
 }
 
+/* The chunk attention of layer_batch in FAST mode: query heads in parallel;
+ * the scores of 8 keys at once from the head's K transposed (lane t holds key
+ * t), each score the same sequential s = s + q_d k_d then / sqrt(hd) as the
+ * scalar loop; softmax_rows per head as before; p . V over 8 head-dim lanes,
+ * each the same sequential sum over keys. */
+static void batch_attention_fast(const float* q, const float* k, const float* v, float* attn, uint64_t seq,
+                                 uint64_t nh, uint64_t nkv, uint64_t hd, uint64_t H, int causal) {
+  const uint64_t grp = nh / nkv, seq8 = (seq + 7) / 8 * 8;
+  const __m256 vrs = _mm256_set1_ps(sqrtf((float)hd));
+#pragma omp parallel
+  {
+    float* scores = (float*)malloc(seq * seq * 4 + 4);
+    float* kt = (float*)malloc(hd * seq8 * 4 + 4);
+    float* row = (float*)malloc(seq8 * 4 + 4);
+    float* ho = (float*)malloc(hd * 4 + 4);
+#pragma omp for schedule(dynamic, 1)
+    for (uint64_t h = 0; h < nh; h++) {
+      const uint64_t hk = h / grp;
+      for (uint64_t d = 0; d < hd; d++) {
+        for (uint64_t t = 0; t < seq; t++) kt[d * seq8 + t] = k[(t * nkv + hk) * hd + d];
+        for (uint64_t t = seq; t < seq8; t++) kt[d * seq8 + t] = 0.0f;
+      }
+      for (uint64_t p = 0; p < seq; p++) {
+        const float* qh = q + (p * nh + h) * hd;
+        const uint64_t tend = causal ? p + 1 : seq;
+        for (uint64_t t0 = 0; t0 < tend; t0 += 8) {
+          __m256 sv = _mm256_setzero_ps();
+          for (uint64_t d = 0; d < hd; d++)
+            sv = _mm256_add_ps(sv, _mm256_mul_ps(_mm256_set1_ps(qh[d]), _mm256_loadu_ps(kt + d * seq8 + t0)));
+          _mm256_storeu_ps(row + t0, _mm256_div_ps(sv, vrs));
+        }
+        for (uint64_t t = tend; t < seq; t++) row[t] = -INFINITY;
+        memcpy(scores + p * seq, row, seq * 4);
+      }
+      orc_softmax_rows(scores, seq, seq);
+      for (uint64_t p = 0; p < seq; p++) {
+        const uint64_t tend = causal ? p + 1 : seq;
+        for (uint64_t d = 0; d < hd; d++) ho[d] = 0.0f;
+        for (uint64_t t = 0; t < tend; t++) {
+          const __m256 sc = _mm256_set1_ps(scores[p * seq + t]);
+          const float* vh = v + (t * nkv + hk) * hd;
+          uint64_t d = 0;
+          for (; d + 8 <= hd; d += 8)
+            _mm256_storeu_ps(ho + d, _mm256_add_ps(_mm256_loadu_ps(ho + d), _mm256_mul_ps(sc, _mm256_loadu_ps(vh + d))));
+          for (; d < hd; d++) ho[d] = ho[d] + scores[p * seq + t] * vh[d];
+        }
+        memcpy(attn + p * H + h * hd, ho, hd * 4);
+      }
+    }
+    free(scores);
+    free(kt);
+    free(row);
+    free(ho);
+  }
+}
+
 /* Shared body of Layer::prefill (src/model/forward.rs:215-337, causal, writes
  * the cache) and Layer::forward (src/model/forward.rs:62-207, no mask, no cache). */
 static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_t seq, float* kc,
@@ -1029,31 +1302,35 @@ static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_
       memcpy(vc + (cache_start + t) * kvd, v + t * kvd, kvd * 4);
     }
   }
-  float rs = sqrtf((float)hd);
-  for (uint64_t h = 0; h < nh; h++) {
-    uint64_t hk = h / grp;
-    for (uint64_t p = 0; p < seq; p++) {
-      const float* qh = q + (p * nh + h) * hd;
-      for (uint64_t t = 0; t < seq; t++) {
-        if (causal && t > p) { scores[p * seq + t] = -INFINITY; continue; }
-        const float* kh = k + (t * c->n_kv_heads + hk) * hd;
-        float s = 0.0f;
-        for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
-        scores[p * seq + t] = s / rs;
+  if (mode == ORC_MODE_FAITHFUL) {
+    float rs = sqrtf((float)hd);
+    for (uint64_t h = 0; h < nh; h++) {
+      uint64_t hk = h / grp;
+      for (uint64_t p = 0; p < seq; p++) {
+        const float* qh = q + (p * nh + h) * hd;
+        for (uint64_t t = 0; t < seq; t++) {
+          if (causal && t > p) { scores[p * seq + t] = -INFINITY; continue; }
+          const float* kh = k + (t * c->n_kv_heads + hk) * hd;
+          float s = 0.0f;
+          for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
+          scores[p * seq + t] = s / rs;
+        }
+      }
+      orc_softmax_rows(scores, seq, seq);
+      for (uint64_t p = 0; p < seq; p++) {
+        float* ho = head_out + p * hd;
+        for (uint64_t d = 0; d < hd; d++) ho[d] = 0.0f;
+        uint64_t tend = causal ? p + 1 : seq;
+        for (uint64_t t = 0; t < tend; t++) {
+          float sc = scores[p * seq + t];
+          const float* vh = v + (t * c->n_kv_heads + hk) * hd;
+          for (uint64_t d = 0; d < hd; d++) ho[d] = ho[d] + sc * vh[d];
+        }
+        memcpy(attn + p * H + h * hd, ho, hd * 4);
       }
     }
-    orc_softmax_rows(scores, seq, seq);
-    for (uint64_t p = 0; p < seq; p++) {
-      float* ho = head_out + p * hd;
-      for (uint64_t d = 0; d < hd; d++) ho[d] = 0.0f;
-      uint64_t tend = causal ? p + 1 : seq;
-      for (uint64_t t = 0; t < tend; t++) {
-        float sc = scores[p * seq + t];
-        const float* vh = v + (t * c->n_kv_heads + hk) * hd;
-        for (uint64_t d = 0; d < hd; d++) ho[d] = ho[d] + sc * vh[d];
-      }
-      memcpy(attn + p * H + h * hd, ho, hd * 4);
-    }
+  } else {
+    batch_attention_fast(q, k, v, attn, seq, nh, c->n_kv_heads, hd, H, causal);
   }
   if ((rc = linear(m, L->attn_output, attn, seq, H, H, x, mode))) goto done;
   orc_add_in_place(x, residual, seq * H);
@@ -1076,7 +1353,7 @@ done:
 /* Model::prefill (src/model/forward.rs:496-538) when kv != NULL, else
  * Model::forward (src/model/forward.rs:448-482).  Logits for every row. */
 static int batch_forward(const orc_model* m, orc_kv* kv, const uint32_t* ids, uint64_t n,
-                         float* logits, int mode, int rope_mode) {
+                         float* logits, int mode, int rope_mode, const uint64_t* rows, uint64_t n_rows) {
   const orc_config* c = &m->cfg;
   uint64_t H = c->hidden_size, V = c->vocab_size;
   int rc;
@@ -1096,7 +1373,17 @@ static int batch_forward(const orc_model* m, orc_kv* kv, const uint32_t* ids, ui
   if (kv) kv->len += n;
   if ((rc = norm_weight(m, m->output_norm, H, &w))) goto done;
   orc_rms_norm_rows(x, w, H, n, c->norm_eps);
-  rc = linear(m, out_weight(m), x, n, V, H, logits, mode);
+  if (rows) {
+    /* logits of the listed rows only (matmul_t's rows are independent) */
+    for (uint64_t r = 0; r < n_rows; r++)
+      if (rows[r] >= n) { rc = ORC_E_INVALID_ARG; goto done; }
+    float* xs = (float*)malloc((n_rows ? n_rows : 1) * H * 4);
+    for (uint64_t r = 0; r < n_rows; r++) memcpy(xs + r * H, x + rows[r] * H, H * 4);
+    rc = linear(m, out_weight(m), xs, n_rows, V, H, logits, mode);
+    free(xs);
+  } else {
+    rc = linear(m, out_weight(m), x, n, V, H, logits, mode);
+  }
 done:
   free(w);
   free(x);
@@ -1105,11 +1392,24 @@ done:
 
 int orc_prefill(const orc_model* m, orc_kv* kv, const uint32_t* ids, uint64_t n, float* logits,
                 int mode, int rope_mode) {
-  return batch_forward(m, kv, ids, n, logits, mode, rope_mode);
+  return batch_forward(m, kv, ids, n, logits, mode, rope_mode, NULL, 0);
+}
+
+/* orc_prefill with the logits of rows[0 .. n_rows) only, in that order
+ * ([n_rows x vocab]); the cache and every row's hidden state as orc_prefill. */
+int orc_prefill_rows(const orc_model* m, orc_kv* kv, const uint32_t* ids, uint64_t n, const uint64_t* rows,
+                     uint64_t n_rows, float* logits, int mode, int rope_mode) {
+  return batch_forward(m, kv, ids, n, logits, mode, rope_mode, rows, n_rows);
 }
 
 int orc_forward(const orc_model* m, const uint32_t* ids, uint64_t n, float* logits, int mode) {
-  return batch_forward(m, NULL, ids, n, logits, mode, ORC_ROPE_REFERENCE);
+  return batch_forward(m, NULL, ids, n, logits, mode, ORC_ROPE_REFERENCE, NULL, 0);
+}
+
+/* orc_forward with the logits of rows[0 .. n_rows) only. */
+int orc_forward_rows(const orc_model* m, const uint32_t* ids, uint64_t n, const uint64_t* rows, uint64_t n_rows,
+                     float* logits, int mode) {
+  return batch_forward(m, NULL, ids, n, logits, mode, ORC_ROPE_REFERENCE, rows, n_rows);
 }
 
 /* Model::generate (src/model/forward.rs:592-612): clear, prefill, then

@@ -40,6 +40,7 @@ enum {
   ORC_E_UNSUPPORTED_ARCH = 12,
   ORC_E_INVALID_ARG = 20,
   ORC_E_KV_FULL = 21,
+  ORC_E_OOM = 23,
   ORC_E_NAN_LOGIT = 24,
 };
 
@@ -59,6 +60,8 @@ int orc_block_layout(uint32_t type, uint64_t* block_elems, uint64_t* block_bytes
 int orc_byte_size(uint32_t type, uint64_t n_elements, uint64_t* bytes);
 int orc_dequantize_f32(uint32_t type, uint64_t n_elements, const uint8_t* bytes,
                        uint64_t n_bytes, float* out, uint64_t n_out);
+/* dequantize through the FAST-mode routines (a test hook: equals orc_dequantize_f32) */
+int orc_dequantize_fast(uint32_t type, uint64_t n_elements, const uint8_t* bytes, float* out);
 
 /* ---- ops ---- */
 void orc_matmul_t(const float* a, const float* b, float* c, uint64_t m, uint64_t n, uint64_t k);
@@ -113,7 +116,11 @@ int orc_decode_step(const orc_model* m, orc_kv* kv, uint32_t token, float* logit
                     int rope_mode);
 int orc_prefill(const orc_model* m, orc_kv* kv, const uint32_t* ids, uint64_t n, float* logits,
                 int mode, int rope_mode);
+int orc_prefill_rows(const orc_model* m, orc_kv* kv, const uint32_t* ids, uint64_t n, const uint64_t* rows,
+                     uint64_t n_rows, float* logits, int mode, int rope_mode);
 int orc_forward(const orc_model* m, const uint32_t* ids, uint64_t n, float* logits, int mode);
+int orc_forward_rows(const orc_model* m, const uint32_t* ids, uint64_t n, const uint64_t* rows, uint64_t n_rows,
+                     float* logits, int mode);
 int orc_generate(const orc_model* m, orc_kv* kv, const uint32_t* prompt, uint64_t n,
                  uint64_t max_tokens, uint32_t* out, int mode, int rope_mode);
 

@@ -238,3 +238,27 @@ def test_embedding_rows_bit_exact(t):
     got = dout.get(np.float32, ids.size * cols).reshape(ids.size, cols)
     _, full = orc.dequantize(t, raw, rows * cols)
     np.testing.assert_array_equal(got, full.reshape(rows, cols)[ids])
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_gemv_wide_dynamic_range_within_groups(t):
+    """The int8-MFMA GEMV stages x per 32-element group in fixed point scaled
+    to the group's largest magnitude (22 bits): an element 2^k below it keeps
+    22 - k bits.  Groups spanning 2^20 (one element of 1, the others ~2^-20)
+    still meet the per-row bound 1e-5 * sum |w||x|: what the small elements
+    lose is below 2^-22 of the group's largest term."""
+    rng = np.random.default_rng(2 ** 20 + t)
+    rows, cols = 512, 4096
+    raw = _raw(t, rows * cols, rng)
+    w = Tensor(t, raw, rows, cols)
+    x = (rng.standard_normal(cols) * 2.0 ** -20).astype(np.float32)
+    x[::32] = rng.choice([-1.0, 1.0], cols // 32).astype(np.float32)  # one large element per group
+    x[5::64] *= 2.0 ** 19                                            # intermediate magnitudes too
+    dx, dy = Dev.of(x), Dev(4 * rows)
+    assert _native.lib().ifx_gemv(w.h, dx.ptr, dy.ptr, None) == 0
+    y = dy.get(np.float32, rows)
+    _, wf = orc.dequantize(t, raw, rows * cols)
+    ref = orc.matmul_t(x, wf, 1, rows, cols)
+    bound = np.abs(wf.reshape(rows, cols)).astype(np.float64) @ np.abs(x).astype(np.float64)
+    assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-5 * bound + 1e-30)
+    assert rel_l2(y, ref) < 1e-5

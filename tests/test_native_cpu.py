@@ -157,3 +157,44 @@ def test_synth_8b_layout_bytes():
     assert per_layer == 138_936_320  # includes the two f32 norms
     head = synth.byte_size(synth.Q6_K, 128256 * 4096)
     assert head == 430_940_160
+
+
+def test_huge_block_count_is_tensor_not_found(tmp_path):
+    """llama.block_count is a u64 from the file: a count whose 9x product wraps
+    to 2 (2049638230412172402) must meet blk.1.* missing and report
+    TensorNotFound (src/model/mod.rs:69-72), not size a buffer from it."""
+    w = GGUFWriter()
+    w.add_string("general.architecture", "llama")
+    w.add_u32("llama.vocab_size", 100).add_u32("llama.embedding_length", 64)
+    w.add_u64("llama.block_count", 2049638230412172402)
+    assert (9 * 2049638230412172402) % (1 << 64) == 2
+    w.add_u32("llama.attention.head_count", 4).add_u32("llama.feed_forward_length", 128)
+    names = ["token_embd.weight", "output_norm.weight"] + [
+        f"blk.0.{r}.weight" for r in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm",
+                                      "ffn_gate", "ffn_up", "ffn_down")]
+    for n in names:
+        w.tensor_f32(n, [1, 1], [0.0])
+    p = str(tmp_path / "huge_blocks.gguf")
+    w.write(p)
+    assert orc.Model.open_status(p) == 9
+    assert _open_product(p) == 9
+
+
+def test_huge_counts_are_io_errors(tmp_path):
+    """Metadata, array and tensor counts larger than the file can back end in an
+    io error as the reference's reads would (src/gguf/file.rs:93-110,
+    src/gguf/value.rs:55-66), with no allocation sized by the count."""
+    # an array claiming 2^40 items of u8 in a tiny file
+    kv = _gguf_string("k") + struct.pack("<IIQ", 9, 0, 1 << 40)
+    p = str(tmp_path / "arr.gguf")
+    with open(p, "wb") as f:
+        f.write(_header(n_kv=1) + kv + b"\x00" * 64)
+    assert orc.Model.open_status(p) == 1
+    assert _open_product(p) == 1
+    # metadata and tensor counts just under the file size: entries run out first
+    for n_kv, n_t in ((200, 0), (0, 200)):
+        q = str(tmp_path / f"counts_{n_kv}_{n_t}.gguf")
+        with open(q, "wb") as f:
+            f.write(_header(n_tensors=n_t, n_kv=n_kv) + b"\x01" * 220)
+        assert orc.Model.open_status(q) == _open_product(q)
+        assert _open_product(q) in (1, 4, 5, 6, 7)

@@ -282,3 +282,64 @@ def test_model_error_paths(tiny_path):
     assert m.decode_step(kv, 1)[0] == 21                # KV full (the reference panics)
     assert m.prefill(m.kv(4), [1, m.vocab])[0] == 10
     assert m.prefill(m.kv(4), [1, 2, 3, 4, 5])[0] == 21
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
+def test_fast_dequant_equals_restatement(t):
+    """The FAST mode's vectorised dequantization (used only by FAST linear
+    layers) gives the restatement's bits on random blocks, every bit pattern
+    of d/dmin included."""
+    rng = np.random.default_rng(100 + t)
+    for special in (False, True):
+        raw, n = _random_raw(t, 8192, rng, special_d=special)
+        rc, ref = orc.dequantize(t, raw, n)
+        rc2, fast = orc.dequantize_fast(t, raw, n)
+        assert rc == rc2 == 0
+        assert _same(fast, ref)
+
+
+@pytest.fixture(scope="module")
+def kquant_small(tmp_path_factory):
+    """A Q4_K/Q6_K GQA model small enough for FAITHFUL prefill (head_dim 64,
+    vocab not a multiple of the 64-row weight blocks)."""
+    p = str(tmp_path_factory.mktemp("kq") / "kq.gguf")
+    spec = synth.reduced(synth.LLAMA3_8B, dim=512, ffn=768, n_layers=2, n_heads=8, n_kv_heads=2, vocab=1003,
+                         ctx=64)
+    synth.write_llama(p, spec, seed=77)
+    return p
+
+
+@pytest.mark.parametrize("n", [1, 5, 13])
+def test_fast_prefill_equals_faithful(tiny_path, tiny_prompt, kquant_small, n):
+    """FAST prefill/forward (register-tiled matmul_t, head-parallel attention
+    with 8-key score lanes) equal FAITHFUL (the reference's loops) bit for bit:
+    row counts off the 3-row tiles, head dims 48 (off the 8-lane p.V) and 64,
+    causal and full attention, and the cache rows written."""
+    ids = np.concatenate([tiny_prompt, tiny_prompt])[:n]
+    for path in (tiny_path, kquant_small):
+        m = orc.Model(path)
+        ids_m = ids % m.vocab
+        kv_a, kv_b = m.kv(32), m.kv(32)
+        ra, la = m.prefill(kv_a, ids_m, mode=orc.MODE_FAITHFUL)
+        rb, lb = m.prefill(kv_b, ids_m, mode=orc.MODE_FAST)
+        assert ra == rb == 0
+        np.testing.assert_array_equal(la, lb)
+        ka, va = kv_a.export(n)
+        kb, vb = kv_b.export(n)
+        np.testing.assert_array_equal(ka, kb)
+        np.testing.assert_array_equal(va, vb)
+        ra, fa = m.forward(ids_m, mode=orc.MODE_FAITHFUL)
+        rb, fb = m.forward(ids_m, mode=orc.MODE_FAST)
+        assert ra == rb == 0
+        np.testing.assert_array_equal(fa, fb)
+        # decode after the chunk: the head-parallel decode attention too
+        ra, da = m.decode_step(kv_a, 7, mode=orc.MODE_FAITHFUL)
+        rb, db = m.decode_step(kv_b, 7, mode=orc.MODE_FAST)
+        assert ra == rb == 0
+        np.testing.assert_array_equal(da, db)
+        # prefill_rows: the listed rows of prefill's logits, in order
+        rows = [n - 1, 0] if n > 1 else [0]
+        rc, lr = m.prefill_rows(m.kv(32), ids_m, rows)
+        assert rc == 0
+        np.testing.assert_array_equal(lr, lb[rows])
+        m.close()
