@@ -282,6 +282,15 @@ int ifx_tensor_dequant(const ifx_tensor* t, float* out, void* stream);
 int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream);
 /* C[m x rows] = A[m x cols] . W^T for m >= 1 (the prefill form of matmul_t). */
 int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream);
+/* ifx_matmul_qt without device allocation.  No reference counterpart: for
+ * callers that cannot call hipMalloc (code under HIP graph capture, serving
+ * loops, harnesses that forbid allocation).  The GEMM's activation operand and
+ * split-K workspace live in a fixed ~23 MiB device array that each GPU holds
+ * until the process ends; m <= 16384 and m * cols <= 2^22 for the GEMM path
+ * (IFX_E_INVALID_ARG beyond).  All calls on one GPU share that array: calls
+ * that overlap on one GPU (two streams or threads) race.  m = 1 and matrices
+ * the GEMM does not take use the GEMV, as ifx_matmul_qt does. */
+int ifx_matmul_qt_noalloc(const float* a, uint64_t m, const ifx_tensor* w, float* c, void* stream);
 
 /* ---------------------------------------------------------------------------
  * f32 operators on device buffers — replaces src/ops.rs

@@ -82,6 +82,7 @@ SIGNATURES = {
     "ifx_tensor_dequant": (i32, [vp, vp, vp]),
     "ifx_gemv": (i32, [vp, vp, vp, vp]),
     "ifx_matmul_qt": (i32, [vp, u64, vp, vp, vp]),
+    "ifx_matmul_qt_noalloc": (i32, [vp, u64, vp, vp, vp]),
     "ifx_ops_matmul_t": (i32, [vp, vp, vp, u64, u64, u64, vp]),
     "ifx_ops_rms_norm_rows": (i32, [vp, vp, u64, u64, f32, vp]),
     "ifx_ops_swiglu": (i32, [vp, vp, vp, u64, vp]),

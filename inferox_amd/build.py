@@ -23,7 +23,7 @@ LIB = os.path.join(HERE, "lib")
 ARCH = os.environ.get("IFX_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["kern_dequant.hip", "kern_gemv.hip", "kern_gemv_mfma.hip", "kern_ops.hip", "kern_attn.hip",
-               "kern_gemm.hip", "kern_attn_prefill.hip", "kern_sample.hip",
+               "kern_gemm.hip", "kern_attn_prefill.hip", "kern_sample.hip", "noalloc.hip",
                "host_types.cpp", "host_gguf.cpp", "host_model.cpp", "capi_ops.cpp", "host_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
