@@ -60,7 +60,8 @@ def parse():
     ap.add_argument("--ctx", type=int, default=None, help="context tokens before the timed decode (8b: 2048, 70b: 8192)")
     ap.add_argument("--model-dir", default=os.environ.get("IFX_BENCH_DIR", os.path.join(tempfile.gettempdir(), "inferox_bench")))
     ap.add_argument("--cpu-steps", type=int, default=None,
-                    help="oracle decode steps for cpu_baseline (0: skip; default 1 for 8b, 0 for 70b)")
+                    help="oracle decode steps for cpu_baseline (0: skip; default 3 for 8b, 0 for 70b)")
+    ap.add_argument("--no-micro", action="store_true", help="skip the GEMV microbench and the tiny-model run")
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="direct launches instead of the step graph")
@@ -75,7 +76,7 @@ def parse():
     big = args.model == "70b"
     args.steps = args.steps if args.steps is not None else (128 if big else 256)
     args.ctx = args.ctx if args.ctx is not None else (8192 if big else CTX)
-    args.cpu_steps = args.cpu_steps if args.cpu_steps is not None else (0 if big else 1)
+    args.cpu_steps = args.cpu_steps if args.cpu_steps is not None else (0 if big else 3)
     return args
 
 
@@ -182,6 +183,124 @@ def measure_prefill(L, model, spec, sizes, reps):
                         "mfma_frac": round(fl / (dev_ms * 1e-3) / MFMA_PEAK_F16, 4), "first_token": int(first.value)}
         log(f"prefill {n}: {out[f'p{n}']}")
     return out
+
+
+def host_cpu():
+    """The host the CPU baseline ran on: model name, cores visible to this
+    process, and whether the AVX2 / FMA paths of matmul_t apply."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model is None:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return {"cpu_model": model, "nproc": avail, "os_cpu_count": os.cpu_count(), "avx2": "avx2" in flags,
+            "fma": "fma" in flags, "avx512f": "avx512f" in flags}
+
+
+# The GEMV microbench: four weight shapes, x ~ N(0, 1) f32, timed over copies
+# of each matrix that together hold at least MICRO_BYTES (past the 256 MB
+# memory-side cache), each call on the next copy.
+MICRO_SHAPES = [("q4k_4096x4096", 12, 4096, 4096), ("q4k_14336x4096", 12, 14336, 4096),
+                ("q4k_4096x14336", 12, 4096, 14336), ("q6k_128256x4096", 14, 128256, 4096)]
+MICRO_BYTES = 512 << 20
+
+
+def gemv_microbench(L, rounds=8):
+    """Per shape: microseconds per call, algorithmic GB/s (weight bytes + f32 x
+    and y) and the fraction of 8 TB/s, HIP events around `rounds` passes over
+    the rotating copies on the library stream."""
+    from inferox_amd import synth
+    from inferox_amd._native import check
+    from inferox_amd.synth import byte_size
+    res = {}
+    for name, t, rows, cols in MICRO_SHAPES:
+        wb = byte_size(t, rows * cols)
+        n_copies = max(2, -(-MICRO_BYTES // wb))
+        raw = synth.random_blocks(t, rows * cols, seed=rows * 7 + cols)
+        tens = []
+        for _ in range(n_copies):
+            h = C.c_void_p()
+            check(L.ifx_tensor_upload(t, raw.ctypes.data_as(C.c_void_p), raw.size, rows, cols, C.byref(h)), "upload")
+            tens.append(h)
+        x = synth.normal_f32(cols, seed=cols)
+        dx, dy = C.c_void_p(), C.c_void_p()
+        check(L.ifx_malloc(C.byref(dx), cols * 4), "malloc")
+        check(L.ifx_malloc(C.byref(dy), rows * 4), "malloc")
+        check(L.ifx_memcpy_h2d(dx, x.ctypes.data_as(C.c_void_p), cols * 4), "h2d")
+        for h in tens:  # warm: one pass
+            check(L.ifx_gemv(h, dx, dy, None), "gemv")
+        check(L.ifx_timer_start(None), "timer")
+        for _ in range(rounds):
+            for h in tens:
+                check(L.ifx_gemv(h, dx, dy, None), "gemv")
+        ms = C.c_float()
+        check(L.ifx_timer_stop(None, C.byref(ms)), "timer")
+        calls = rounds * n_copies
+        us = ms.value * 1e3 / calls
+        b = wb + 4 * (rows + cols)
+        res[name] = {"rows": rows, "cols": cols, "type": "Q4_K" if t == 12 else "Q6_K", "bytes_per_call": b,
+                     "copies": n_copies, "calls": calls, "us": round(us, 3), "GB_s": round(b / (us * 1e-6) / 1e9, 1),
+                     "frac": round(b / (us * 1e-6) / HBM_PEAK, 4)}
+        log(f"gemv {name}: {res[name]}")
+        L.ifx_free(dx)
+        L.ifx_free(dy)
+        for h in tens:
+            L.ifx_tensor_free(h)
+    return res
+
+
+def tiny_run(L, model_dir, cpu: bool):
+    """The tiny Q8_0 workload end to end: a 16-token seeded prompt, then 128
+    greedy tokens (ctx 256), through ifx_generate; tok/s of the generated
+    tokens (prefill included, as the workload defines it), and the faithful
+    CPU restatement on one thread over the same workload when `cpu`."""
+    from inferox_amd import synth
+    from inferox_amd._native import check
+    path = os.path.join(model_dir, "tiny-seed1234.gguf")
+    if not os.path.exists(path):
+        synth.write_llama(path, synth.TINY, seed=1234)
+    prompt = synth.token_ids(16, synth.TINY.vocab, seed=4321)
+    model = C.c_void_p()
+    check(L.ifx_model_open(path.encode(), C.byref(model)), "tiny open")
+    sess = C.c_void_p()
+    check(L.ifx_session_create(model, 256, C.byref(sess)), "tiny session")
+    out = np.zeros(128, np.uint32)
+    check(L.ifx_generate(sess, prompt.ctypes.data_as(C.c_void_p), 16, 128, out.ctypes.data_as(C.c_void_p)), "warm")
+    best = None
+    for _ in range(3):
+        check(L.ifx_stream_synchronize(None), "sync")
+        t0 = time.perf_counter()
+        check(L.ifx_generate(sess, prompt.ctypes.data_as(C.c_void_p), 16, 128, out.ctypes.data_as(C.c_void_p)),
+              "tiny generate")
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    L.ifx_session_destroy(sess)
+    L.ifx_model_close(model)
+    r = {"workload": "tiny Q8_0 (dim 288, 6 layers, vocab 32000): 16-token prompt + 128 greedy tokens, ctx 256",
+         "tok_s": round(128 / best, 1), "ms_total": round(best * 1e3, 2), "first_tokens": [int(v) for v in out[:4]]}
+    if cpu:
+        from oracle import binding as orc
+        orc.set_threads(1)
+        m = orc.Model(path)
+        kv = m.kv(256)
+        t0 = time.perf_counter()
+        rc, ref = m.generate(kv, prompt, 128, mode=orc.MODE_FAITHFUL)
+        dt = time.perf_counter() - t0
+        m.close()
+        r["cpu_tok_s"] = round(128 / dt, 2)
+        r["cpu_kind"] = "port (faithful restatement, 1 thread)"
+        r["tokens_equal_cpu"] = bool(rc == 0 and ref.tolist() == out.tolist())
+    log(f"tiny: {r}")
+    return r
 
 
 def bytes_per_token(spec, ctx_avg):
@@ -341,6 +460,9 @@ def main():
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                     "traffic": traffic_for(KCLASS[dom]) if args.model == "8b" else None,
+                    "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch of this kernel at ctx 2048, "
+                                       "scaled by a copy of known size (profiles/traffic.json; counters cannot run "
+                                       "inside this process)") if args.model == "8b" else None,
                     "kernel": KERNEL_NAMES.get(dom, KCLASS[dom]), "kernel_class": KCLASS[dom],
                     "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2)}
         prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "launches_per_step": int(launches[k]),
@@ -357,7 +479,8 @@ def main():
         cpu = {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": 1, "kind": "port",
                "sample": f"{args.cpu_steps} decode step(s) of the same 8B model from the same {args.ctx}-row KV "
                          f"state, faithful CPU restatement (per-step full dequant, AVX2 matmul_t), median "
-                         f"{med:.2f} s/step; greedy pick {toks[0]} vs GPU {int(out[0])}"}
+                         f"{med:.2f} s/step; greedy picks {toks} vs GPU {[int(v) for v in out[:len(toks)]]}",
+               "host": host_cpu()}
         log(f"cpu: {med:.2f} s/step; first pick cpu={toks[0]} gpu={int(out[0])}")
 
     L.ifx_session_destroy(sess)
@@ -368,6 +491,10 @@ def main():
     prefill = None if args.no_profile else measure_prefill(
         L, model, spec, [int(x) for x in args.prefill_sizes.split(",")], 1)
     L.ifx_model_close(model)
+    micro = tiny = None
+    if not args.no_micro and args.model == "8b":
+        micro = gemv_microbench(L)
+        tiny = tiny_run(L, args.model_dir, cpu=do_cpu)
 
     line = {
         "metric": METRIC if args.model == "8b" else METRIC.replace("8B", "70B"), "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -386,6 +513,8 @@ def main():
         "prefill": prefill,
         "other_kv_cache": other_kv,
         "kernels": prof or None,
+        "gemv_microbench": micro,
+        "tiny": tiny,
     }
     print(json.dumps(line), flush=True)
 
