@@ -374,14 +374,18 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
           const float v = buf[i][t].dot(A, xa, xb, g);
           acc[t] += valid ? v : 0.f;
         }
-        // refill with block m + D of this item, or block i of the next one
+        // refill with block m + D of this item, or block i of the next one.
+        // Past the wave's last item the (unused) refill reads the segment's
+        // first unit, which every such refill on the XCD shares: an L2 hit,
+        // so the wave does not wait an HBM round trip for it before it ends.
         uint32_t nm = m + D, ntl = tile;
         if (nm >= NB) {
           nm -= NB;
           ntl += TG;
         }
-        ntl = min(ntl, nt - 1);
-        const uint32_t nb = min(j + S * nm, nbr - 1);
+        const bool past = ntl >= nt;
+        const uint32_t nb = past ? 0u : min(j + S * nm, nbr - 1);
+        ntl = past ? 0u : ntl;
 #pragma unroll
         for (int t = 0; t < NT; t++)
           buf[i][t].load(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, ntl, nb), lane, a.seg[NT == 2 ? t : s].q6_signed);
