@@ -333,14 +333,16 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
 // staged in LDS 256 chunks at a time.  Thread (split sp, float4 column) sums
 // the batch's chunks sp, sp + nsplit, ...; the first loads of o are in flight
 // while M is formed.
-template <int HDT, int GT>
+// CS workgroups per query head, each producing HD / CS of its columns (every
+// one forms the same weights from all records' max and sum).
+template <int HDT, int GT, int CS>
 __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
   __shared__ float cw[kThreads];
   __shared__ float wred[2][kThreads / 64];
   __shared__ float4 red[kThreads];
   const uint32_t G = GT > 0 ? (uint32_t)GT : a.n_heads / a.n_kv_heads;
-  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4;
-  const uint32_t h = blockIdx.x, hk = h / G, g = h % G;
+  const uint32_t HD = HDT > 0 ? (uint32_t)HDT : a.head_dim, nc4 = HD / 4 / CS;  // float4 columns of the slice
+  const uint32_t h = blockIdx.x / CS, hk = h / G, g = h % G, cb = (blockIdx.x % CS) * nc4;
   uint32_t lo, hi;
   attended_rows(a.state, lo, hi);
   const uint32_t nrows = hi > lo ? hi - lo : 0;
@@ -356,7 +358,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
 #pragma unroll
   for (int k = 0; k < kMergeBatch; k++) {
     const uint32_t c = min(min(sp, nsplit - 1) + nsplit * k, nch - 1);  // clamped: loads stay unconditional
-    ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+    ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[cb + col];
   }
   // M over every chunk (chunk tid's max and sum are kept for the first batch)
   float m0, l0;
@@ -391,7 +393,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
 #pragma unroll
           for (int k = 0; k < kMergeBatch; k++) {
             const uint32_t c = min(c0 + nsplit * k, nch - 1);
-            ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[col];
+            ov[k] = ((const float4*)(base + (uint64_t)c * rec + g * HD))[cb + col];
           }
         }
 #pragma unroll
@@ -411,7 +413,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
     float dsum = 0.f;
 #pragma unroll
     for (int w = 0; w < kThreads / 64; w++) dsum += wred[1][w];
-    ((float4*)(a.out + (uint64_t)h * HD))[tid] = make_float4(o.x / dsum, o.y / dsum, o.z / dsum, o.w / dsum);
+    ((float4*)(a.out + (uint64_t)h * HD))[cb + tid] = make_float4(o.x / dsum, o.y / dsum, o.z / dsum, o.w / dsum);
   }
 }
 
@@ -422,7 +424,8 @@ void launch_typed(const AttnArgs& a, hipStream_t st) {
 #define IFX_ATTN(HD_, G_)                                                                          \
   do {                                                                                             \
     hipLaunchKernelGGL((k_attn_decode<HD_, G_, E>), grid, dim3(kThreads), 0, st, a);              \
-    hipLaunchKernelGGL((k_attn_merge<HD_, G_>), dim3(a.n_heads), dim3(kThreads), 0, st, a);       \
+    constexpr int CS_ = (HD_ > 0 && (HD_ / 4) % 4 == 0) ? 4 : 1;                                  \
+    hipLaunchKernelGGL((k_attn_merge<HD_, G_, CS_>), dim3(a.n_heads * CS_), dim3(kThreads), 0, st, a); \
   } while (0)
   if (a.head_dim == 128 && G == 4) IFX_ATTN(128, 4);        // Llama-3 8B
   else if (a.head_dim == 128 && G == 8) IFX_ATTN(128, 8);   // Llama-3 70B
