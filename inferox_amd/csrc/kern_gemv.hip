@@ -664,6 +664,8 @@ hipError_t gemv_store(const GemvLaunch& L, float* y, hipStream_t st) {
 
 hipError_t gemv_residual(const GemvLaunch& L, float* hidden, hipStream_t st) {
   if (L.nseg != 1) return hipErrorInvalidValue;
+  const hipError_t e = launch_mfma_residual_ks(L, hidden, st);
+  if (e != hipErrorNotSupported) return e;
   return launch(L, EpiResidual{hidden}, st);
 }
 

@@ -519,6 +519,117 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
   epi.finish(ws, lane);
 }
 
+// ---------------------------------------------------------------------------
+// K-split residual GEMV: h += W x for the O and down projections.  The
+// kernel above gives each 16-row tile to the waves of one workgroup, so every
+// workgroup stages all of x, the previous kernel's output; staging it (the
+// loads queue behind the weight stream, then the quantization) is the longest
+// part of those launches (~6 us of the down projection's ~13.6 at 14336
+// columns).  Here K is cut into kKs slices: workgroup g takes slice g mod kKs
+// and each of its waves one tile per pass, so a workgroup stages 1 / kKs of
+// x (and workgroup g runs on XCD g mod 8, so each XCD's L2 serves one
+// slice).  The kKs partial dot products of a row meet in h through float
+// atomic adds at agent scope, which are coherent across the XCDs; their order,
+// and so the last bits of h, may differ from run to run.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kKs = 8;
+// one x chunk of 8 elements per thread: slices of up to 16 blocks (4096
+// columns), K up to 32768.  (A loop of clamped loads would leave dead
+// destinations the compiler waits on, and a conditional prefetch makes its
+// waits assume the shorter path.)
+constexpr uint32_t kKsMaxBlocks = kThreads * 8 / 256;
+
+struct KsArgs {
+  GemvSeg seg;
+  uint32_t ntiles, nbr, nbs;  // 16-row tiles, 256-column blocks, blocks per slice
+  const float* x;
+  float* h;
+  uint32_t xs_off, zero_off;  // LDS byte offsets (the slice's digit planes start at 0)
+};
+
+template <int T, int D>
+__global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nbs = a.nbs, b0 = (blockIdx.x % kKs) * nbs;
+  const uint32_t t0 = (blockIdx.x / kKs) * kWaves + wave, tstride = (gridDim.x / kKs) * kWaves;
+  // the wave's units: tiles t0, t0 + tstride, ... x the slice's nbs blocks
+  const uint32_t W = t0 < a.ntiles ? ((a.ntiles - 1 - t0) / tstride + 1) * nbs : 0u;
+
+  // the slice of x: elements [256 b0, 256 (b0 + nbs)), chunks of 8
+  const uint32_t nch = nbs * 32, c = (uint32_t)tid;
+  const float4* x4 = (const float4*)(a.x + (uint64_t)b0 * 256u) + 2 * min(c, nch - 1);  // clamped: unconditional
+  const float4 xv0 = x4[0], xv1 = x4[1];
+  // every wave's x loads enter the CU's memory queues before any weight load
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ring: slot i holds unit u = i (mod D); unit u is block b0 + u mod nbs of
+  // tile t0 + (u / nbs) tstride.  Loads past the wave's last unit (and all of
+  // a wave without tiles) read a unit of tile 0 of the slice: in bounds,
+  // unused, and unconditional, so that the waits below count one path.
+  const uint32_t q6s = a.seg.q6_signed;
+  KBuf<T> buf[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    const uint32_t u = (uint32_t)i < W ? (uint32_t)i : 0u, tl = W > 0 ? t0 + (u / nbs) * tstride : 0u;
+    buf[i].load(unit_ptr<T>(a.seg, a.nbr, tl, b0 + u % nbs), (uint32_t)lane, q6s);
+    __builtin_amdgcn_sched_barrier(0);  // slots in ring order
+  }
+
+  {  // whole 32-element groups are in or out of the slice (nch % 32 == 0)
+    float v[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
+    quantize_chunk(v, c, c < nch, lds, (float4*)(lds + a.xs_off));
+  }
+  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  if (W == 0) return;
+
+  const int ai = lane & 15, ag = lane >> 4;
+  const bool active = (ai >> 2) == ag && (ai & 3) < 3;
+  const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : a.zero_off;
+  const uint32_t a_step = active ? kBlockA : 0u;
+  const float4* xs4 = (const float4*)(lds + a.xs_off) + ag;
+  const uint32_t Wp = (W + D - 1) / D * D;
+  float acc = 0.f;
+  uint32_t bl = 0, tile = t0;  // unit u: local block, tile
+  uint32_t rb = (uint32_t)D % nbs, rt = t0 + ((uint32_t)D / nbs) * tstride;  // unit u + D
+  for (uint32_t u0 = 0; u0 < Wp; u0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      const uint32_t u = u0 + (uint32_t)i;
+      const uint8_t* ap = lds + a_base + a_step * bl;
+      const v4i A[4] = {*(const v4i*)ap, *(const v4i*)(ap + kPartBytes), *(const v4i*)(ap + 8 * kPartBytes),
+                        *(const v4i*)(ap + 9 * kPartBytes)};
+      const float4 xa = xs4[8 * bl], xb = xs4[8 * bl + 4];
+      const float v = buf[i].dot(A, xa, xb, ag);
+      acc += u < W ? v : 0.f;
+      const bool past = u + D >= W;
+      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? t0 : rt, b0 + (past ? 0u : rb)), (uint32_t)lane, q6s);
+      // keep the ring order (see run_seg)
+      __builtin_amdgcn_sched_barrier(0);
+      if (++rb == nbs) {
+        rb = 0;
+        rt += tstride;
+      }
+      if (++bl == nbs) {  // the tile's slice is done (uniform over the wave)
+        if (u < W) {
+          float r = acc;
+          r += __shfl_xor(r, 16, 64);
+          r += __shfl_xor(r, 32, 64);
+          const uint32_t row = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
+          if (lane < 16 && row < a.seg.rows) atomicAdd(a.h + row, r);
+        }
+        acc = 0.f;
+        bl = 0;
+        tile += tstride;
+      }
+    }
+  }
+}
+
 int cu_count() {
   static int n = 0;
   if (n == 0) {
@@ -626,6 +737,41 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     if (D == 2) return go_types<Epi, 2>(a, ta, tb, epi, blocks, lds, st);
     return go_types<Epi, 4>(a, ta, tb, epi, blocks, lds, st);
   }
+}
+
+// The K-split residual launch (k_gemv_ks) where it applies: one Q4_K / Q6_K
+// segment without a norm, K in whole slices of at most 16 blocks, and at least
+// one tile per wave of the grid.  hipErrorNotSupported otherwise (the caller
+// takes launch_mfma).
+hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st) {
+  if (L.nseg != 1 || L.norm_w || L.paired || !mfma_type(L.seg[0].type) || L.cols == 0 || L.cols % 256)
+    return hipErrorNotSupported;
+  const uint32_t nbr = L.cols / 256, blocks = (uint32_t)cu_count();
+  const uint32_t ntiles = (uint32_t)((L.seg[0].rows + kTileRows - 1) / kTileRows);
+  if (nbr % kKs || nbr / kKs > kKsMaxBlocks || blocks % kKs ||
+      ntiles < blocks / kKs * kWaves)
+    return hipErrorNotSupported;
+  KsArgs a{};
+  a.seg = L.seg[0];
+  a.ntiles = ntiles;
+  a.nbr = nbr;
+  a.nbs = nbr / kKs;
+  a.x = L.x;
+  a.h = h;
+  a.xs_off = 768u * a.nbs;              // digit planes: 48 bytes per 16 elements
+  a.zero_off = a.xs_off + 128u * a.nbs;  // group sums: 16 bytes per 32 elements
+  const size_t lds = a.zero_off + kZeroBytes;
+  // units per wave: a ring as deep as the work, up to 8
+  const uint32_t w = ((ntiles - 1) / (blocks / kKs * kWaves) + 1) * a.nbs;
+  const int D = w <= 2 ? 2 : w <= 4 ? 4 : 8;
+  const bool q6 = L.seg[0].type == T_Q6K;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a);
+    return hipGetLastError();
+  };
+  if (D == 2) return q6 ? go(k_gemv_ks<T_Q6K, 2>) : go(k_gemv_ks<T_Q4K, 2>);
+  if (D == 4) return q6 ? go(k_gemv_ks<T_Q6K, 4>) : go(k_gemv_ks<T_Q4K, 4>);
+  return q6 ? go(k_gemv_ks<T_Q6K, 8>) : go(k_gemv_ks<T_Q4K, 8>);
 }
 
 template hipError_t launch_mfma<EpiStore>(const GemvLaunch&, const EpiStore&, hipStream_t);
