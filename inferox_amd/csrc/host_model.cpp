@@ -63,11 +63,13 @@ struct ifx_session {
   DevState* state = nullptr;
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
   uint32_t attn_chunk = 64, max_chunks = 0;
-  hipGraphExec_t exec = nullptr;        // the greedy step
-  bool graph_tried = false;
-  hipGraphExec_t exec_sample = nullptr;  // the step with k_sample before finalize
-  bool graph_tried_sample = false;
+  // captured steps: [sampling][merge_o] (the greedy step, the step with
+  // k_sample before finalize; each with the attention merge in its own launch
+  // or in the O projection's prologue)
+  hipGraphExec_t exec[2][2] = {};
+  bool graph_tried[2][2] = {};
   bool sampling = false;                 // set for the duration of ifx_generate_sampled
+  bool merge_o = false;                  // the step being enqueued merges the attention in the O launch
   float* probs = nullptr;                // k_sample scratch [vocab]
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
@@ -247,20 +249,20 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       IFX_HIP(gemv_qkv(g, e, st));
       return IFX_OK;
     }
-    case 2: {
+    case 2:
+    case 3: {
       AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
                  (uint32_t)s->max_seq, kv16};
-      IFX_HIP(launch_attn_decode(a, st));
-      return IFX_OK;
-    }
-    case 3: {
       GemvLaunch go;
       go.seg[0] = seg_of(L.o);
       go.nseg = 1;
       go.cols = D;
       go.x = s->attn;
-      IFX_HIP(gemv_residual(go, s->hidden, st));
+      // the merge of the chunk records moves into the O launch's prologue
+      const bool fused = s->merge_o && merge_o_supported(go, a);
+      if (k == 2) IFX_HIP(fused ? launch_attn_partials(a, st) : launch_attn_decode(a, st));
+      else IFX_HIP(fused ? launch_mfma_residual_merge(go, a, s->hidden, st) : gemv_residual(go, s->hidden, st));
       return IFX_OK;
     }
     case 4: {
@@ -303,11 +305,23 @@ int enqueue_step(ifx_session* s) {
 
 uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->L.scal_bytes; }
 
+// The attention merge goes into the O launch's prologue while the attended
+// rows make at most merge_o_first_chunks() chunk records (every workgroup
+// reads them all; past that the separate merge launch is faster).  `rows`
+// bounds the rows the step attends (the cache rows before it + 1).
+// IFX_MERGE_O=0 / 1 takes the separate / the fused merge at any length.
+void choose_merge(ifx_session* s, uint64_t rows) {
+  const char* f = getenv("IFX_MERGE_O");
+  if (f && (f[0] == '0' || f[0] == '1') && f[1] == 0) s->merge_o = f[0] == '1';
+  else s->merge_o = (rows + s->attn_chunk - 1) / s->attn_chunk <= merge_o_first_chunks();
+}
+
 // Replay the captured step (capturing it on first use); direct launches if the
 // runtime refuses capture.
-int run_step(ifx_session* s) {
-  hipGraphExec_t& exec = s->sampling ? s->exec_sample : s->exec;
-  bool& tried = s->sampling ? s->graph_tried_sample : s->graph_tried;
+int run_step(ifx_session* s, uint64_t rows) {
+  choose_merge(s, rows);
+  hipGraphExec_t& exec = s->exec[s->sampling][s->merge_o];
+  bool& tried = s->graph_tried[s->sampling][s->merge_o];
   if (!tried) {
     tried = true;
     // IFX_NO_GRAPH=1: launch the step's kernels directly (used under profilers
@@ -474,8 +488,9 @@ void session_free(ifx_session* s) {
   if (s->stream) (void)hipStreamSynchronize(s->stream);
   if (s->ws.alloc) (void)hipFree(s->ws.alloc);
   if (s->ws.logits) (void)hipFree(s->ws.logits);
-  if (s->exec) (void)hipGraphExecDestroy(s->exec);
-  if (s->exec_sample) (void)hipGraphExecDestroy(s->exec_sample);
+  for (auto& row : s->exec)
+    for (hipGraphExec_t e : row)
+      if (e) (void)hipGraphExecDestroy(e);
   if (s->ev0) (void)hipEventDestroy(s->ev0);
   if (s->ev1) (void)hipEventDestroy(s->ev1);
   for (void* p : s->allocs) (void)hipFree(p);
@@ -754,7 +769,7 @@ int ifx_decode_step(ifx_session* s, uint32_t token, float* logits_out) {
   IFX_TRY(check_vocab(m));
   if (s->len >= s->max_seq) return set_error(IFX_E_KV_FULL, "KV cache full (%llu rows)", (unsigned long long)s->max_seq);
   IFX_TRY(state_op(s, STATE_DECODE, token, 0));
-  IFX_TRY(run_step(s));
+  IFX_TRY(run_step(s, s->len + 1));
   if (logits_out)
     IFX_HIP(hipMemcpyAsync(logits_out, s->logits, (size_t)m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, s->stream));
   IFX_HIP(hipStreamSynchronize(s->stream));
@@ -786,7 +801,7 @@ int ifx_prefill(ifx_session* s, const uint32_t* ids, uint64_t n, float* logits_o
   IFX_HIP(hipEventRecord(s->ev0, s->stream));
   const size_t V = m->cfg.vocab_size;
   for (uint64_t t = 0; t < n; t++) {
-    IFX_TRY(run_step(s));
+    IFX_TRY(run_step(s, s->len + t + 1));
     if (logits_out)
       IFX_HIP(hipMemcpyAsync(logits_out + t * V, s->logits, V * 4, hipMemcpyDeviceToHost, s->stream));
   }
@@ -808,7 +823,7 @@ int ifx_decode_greedy(ifx_session* s, uint32_t token, uint64_t n_steps, uint32_t
   const uint64_t first = s->steps;
   IFX_TRY(state_op(s, STATE_DECODE, token, 0));
   IFX_HIP(hipEventRecord(s->ev0, s->stream));
-  for (uint64_t i = 0; i < n_steps; i++) IFX_TRY(run_step(s));
+  for (uint64_t i = 0; i < n_steps; i++) IFX_TRY(run_step(s, s->len + i + 1));
   IFX_HIP(hipEventRecord(s->ev1, s->stream));
   IFX_HIP(hipStreamSynchronize(s->stream));
   (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
@@ -839,7 +854,7 @@ int ifx_generate(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t ma
   // the greedy loop continues on the device: the last prefill step left its
   // argmax as the next input token (src/model/forward.rs:605-609)
   IFX_HIP(hipEventRecord(s->ev0, s->stream));
-  for (uint64_t i = 0; i < max_tokens; i++) IFX_TRY(run_step(s));
+  for (uint64_t i = 0; i < max_tokens; i++) IFX_TRY(run_step(s, s->len + i + 1));
   IFX_HIP(hipEventRecord(s->ev1, s->stream));
   IFX_HIP(hipStreamSynchronize(s->stream));
   (void)hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1);
@@ -1032,6 +1047,7 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   if (s->len + n_steps + 1 > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
   const uint64_t len0 = s->len;
   IFX_TRY(state_op(s, STATE_DECODE, token, 0));
+  choose_merge(s, len0 + n_steps);  // the repeated launches below attend the last step's rows
   for (uint64_t i = 0; i < n_steps; i++) {
     IFX_TRY(enqueue_step(s));
     s->steps++;

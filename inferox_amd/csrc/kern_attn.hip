@@ -418,14 +418,15 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
 }
 
 template <typename E>
-void launch_typed(const AttnArgs& a, hipStream_t st) {
+void launch_typed(const AttnArgs& a, hipStream_t st, bool merge) {
   const dim3 grid(a.max_chunks, a.n_kv_heads);
   const uint32_t G = a.n_heads / a.n_kv_heads;
 #define IFX_ATTN(HD_, G_)                                                                          \
   do {                                                                                             \
     hipLaunchKernelGGL((k_attn_decode<HD_, G_, E>), grid, dim3(kThreads), 0, st, a);              \
     constexpr int CS_ = (HD_ > 0 && (HD_ / 4) % 4 == 0) ? 4 : 1;                                  \
-    hipLaunchKernelGGL((k_attn_merge<HD_, G_, CS_>), dim3(a.n_heads * CS_), dim3(kThreads), 0, st, a); \
+    if (merge)                                                                                     \
+      hipLaunchKernelGGL((k_attn_merge<HD_, G_, CS_>), dim3(a.n_heads * CS_), dim3(kThreads), 0, st, a); \
   } while (0)
   if (a.head_dim == 128 && G == 4) IFX_ATTN(128, 4);        // Llama-3 8B
   else if (a.head_dim == 128 && G == 8) IFX_ATTN(128, 8);   // Llama-3 70B
@@ -442,14 +443,19 @@ bool attn_decode_head_dim(uint32_t head_dim, bool kv_f16) {
   return head_dim > 0 && head_dim <= kMaxHd && head_dim % (kv_f16 ? 8 : 4) == 0;
 }
 
-hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
+namespace {
+hipError_t launch_attn(const AttnArgs& a, hipStream_t st, bool merge) {
   if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > kMaxGroup ||
       !attn_decode_head_dim(a.head_dim, a.kv_f16) || a.chunk != kChunk ||
       a.max_chunks == 0)
     return hipErrorInvalidValue;
-  if (a.kv_f16) launch_typed<_Float16>(a, st);
-  else launch_typed<float>(a, st);
+  if (a.kv_f16) launch_typed<_Float16>(a, st, merge);
+  else launch_typed<float>(a, st, merge);
   return hipGetLastError();
 }
+}  // namespace
+
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) { return launch_attn(a, st, true); }
+hipError_t launch_attn_partials(const AttnArgs& a, hipStream_t st) { return launch_attn(a, st, false); }
 
 }  // namespace ifx

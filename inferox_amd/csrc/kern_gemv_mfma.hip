@@ -40,6 +40,7 @@
 // to the next item), so HBM stays busy through reductions and epilogues.
 // Compiled with -ffp-contract=off: only the explicit fmaf below are fused.
 #include <algorithm>
+#include <type_traits>
 
 #include "gemv_epi.h"
 
@@ -524,13 +525,18 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
 // kernel above gives each 16-row tile to the waves of one workgroup, so every
 // workgroup stages all of x, the previous kernel's output; staging it (the
 // loads queue behind the weight stream, then the quantization) is the longest
-// part of those launches (~6 us of the down projection's ~13.6 at 14336
+// part of those launches (~3.4 us of the O projection's ~5.5 at 4096
 // columns).  Here K is cut into kKs slices: workgroup g takes slice g mod kKs
 // and each of its waves one tile per pass, so a workgroup stages 1 / kKs of
 // x (and workgroup g runs on XCD g mod 8, so each XCD's L2 serves one
 // slice).  The kKs partial dot products of a row meet in h through float
 // atomic adds at agent scope, which are coherent across the XCDs; their order,
 // and so the last bits of h, may differ from run to run.
+//
+// With 8 kv heads the O projection's slices are the kv heads' query-head
+// groups, so k_gemv_ks_merge can take the attention's chunk records in place
+// of x: its prologue merges the records of kv head g mod 8 (what k_attn_merge
+// does for every head) and quantizes the result as its slice of x.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kKs = 8;
 // one x chunk of 8 elements per thread: slices of up to 16 blocks (4096
@@ -545,57 +551,54 @@ struct KsArgs {
   const float* x;
   float* h;
   uint32_t xs_off, zero_off;  // LDS byte offsets (the slice's digit planes start at 0)
+  // k_gemv_ks_merge: the chunk records of the decode attention and the state
+  // that gives the attended rows
+  const float* partial;
+  const DevState* state;
+  uint32_t max_chunks, chunk;
 };
 
+// The wave's units: tiles t0, t0 + tstride, ... x the slice's nbs blocks.
+struct KsWave {
+  uint32_t t0, tstride, b0, W;
+  __device__ __forceinline__ KsWave(const KsArgs& a, uint32_t wave) {
+    b0 = (blockIdx.x % kKs) * a.nbs;
+    t0 = (blockIdx.x / kKs) * kWaves + wave;
+    tstride = (gridDim.x / kKs) * kWaves;
+    W = t0 < a.ntiles ? ((a.ntiles - 1 - t0) / tstride + 1) * a.nbs : 0u;
+  }
+};
+
+// Ring: slot i holds unit u = i (mod D); unit u is block b0 + u mod nbs of
+// tile t0 + (u / nbs) tstride.  Loads past the wave's last unit (and all of a
+// wave without tiles) read a unit of tile 0 of the slice: in bounds, unused,
+// and unconditional, so that the compiler's waits count one path.
 template <int T, int D>
-__global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t nbs = a.nbs, b0 = (blockIdx.x % kKs) * nbs;
-  const uint32_t t0 = (blockIdx.x / kKs) * kWaves + wave, tstride = (gridDim.x / kKs) * kWaves;
-  // the wave's units: tiles t0, t0 + tstride, ... x the slice's nbs blocks
-  const uint32_t W = t0 < a.ntiles ? ((a.ntiles - 1 - t0) / tstride + 1) * nbs : 0u;
-
-  // the slice of x: elements [256 b0, 256 (b0 + nbs)), chunks of 8
-  const uint32_t nch = nbs * 32, c = (uint32_t)tid;
-  const float4* x4 = (const float4*)(a.x + (uint64_t)b0 * 256u) + 2 * min(c, nch - 1);  // clamped: unconditional
-  const float4 xv0 = x4[0], xv1 = x4[1];
-  // every wave's x loads enter the CU's memory queues before any weight load
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ring: slot i holds unit u = i (mod D); unit u is block b0 + u mod nbs of
-  // tile t0 + (u / nbs) tstride.  Loads past the wave's last unit (and all of
-  // a wave without tiles) read a unit of tile 0 of the slice: in bounds,
-  // unused, and unconditional, so that the waits below count one path.
-  const uint32_t q6s = a.seg.q6_signed;
-  KBuf<T> buf[D];
+__device__ __forceinline__ void ks_prefetch(const KsArgs& a, const KsWave& w, KBuf<T> (&buf)[D], int lane) {
 #pragma unroll
   for (int i = 0; i < D; i++) {
-    const uint32_t u = (uint32_t)i < W ? (uint32_t)i : 0u, tl = W > 0 ? t0 + (u / nbs) * tstride : 0u;
-    buf[i].load(unit_ptr<T>(a.seg, a.nbr, tl, b0 + u % nbs), (uint32_t)lane, q6s);
+    const uint32_t u = (uint32_t)i < w.W ? (uint32_t)i : 0u, tl = w.W > 0 ? w.t0 + (u / a.nbs) * w.tstride : 0u;
+    buf[i].load(unit_ptr<T>(a.seg, a.nbr, tl, w.b0 + u % a.nbs), (uint32_t)lane, a.seg.q6_signed);
     __builtin_amdgcn_sched_barrier(0);  // slots in ring order
   }
+}
 
-  {  // whole 32-element groups are in or out of the slice (nch % 32 == 0)
-    float v[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
-    quantize_chunk(v, c, c < nch, lds, (float4*)(lds + a.xs_off));
-  }
-  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
-  __syncthreads();
-  if (W == 0) return;
-
+// The wave's units against the slice of x staged in LDS; each finished tile's
+// 16 row sums are added into h.
+template <int T, int D>
+__device__ __forceinline__ void ks_run(const KsArgs& a, const KsWave& w, KBuf<T> (&buf)[D], const uint8_t* lds,
+                                       int lane) {
+  if (w.W == 0) return;
+  const uint32_t nbs = a.nbs;
   const int ai = lane & 15, ag = lane >> 4;
   const bool active = (ai >> 2) == ag && (ai & 3) < 3;
   const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : a.zero_off;
   const uint32_t a_step = active ? kBlockA : 0u;
   const float4* xs4 = (const float4*)(lds + a.xs_off) + ag;
-  const uint32_t Wp = (W + D - 1) / D * D;
+  const uint32_t Wp = (w.W + D - 1) / D * D;
   float acc = 0.f;
-  uint32_t bl = 0, tile = t0;  // unit u: local block, tile
-  uint32_t rb = (uint32_t)D % nbs, rt = t0 + ((uint32_t)D / nbs) * tstride;  // unit u + D
+  uint32_t bl = 0, tile = w.t0;                                            // unit u: local block, tile
+  uint32_t rb = (uint32_t)D % nbs, rt = w.t0 + ((uint32_t)D / nbs) * w.tstride;  // unit u + D
   for (uint32_t u0 = 0; u0 < Wp; u0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
@@ -605,17 +608,18 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
                         *(const v4i*)(ap + 9 * kPartBytes)};
       const float4 xa = xs4[8 * bl], xb = xs4[8 * bl + 4];
       const float v = buf[i].dot(A, xa, xb, ag);
-      acc += u < W ? v : 0.f;
-      const bool past = u + D >= W;
-      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? t0 : rt, b0 + (past ? 0u : rb)), (uint32_t)lane, q6s);
+      acc += u < w.W ? v : 0.f;
+      const bool past = u + D >= w.W;
+      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? w.t0 : rt, w.b0 + (past ? 0u : rb)), (uint32_t)lane,
+                  a.seg.q6_signed);
       // keep the ring order (see run_seg)
       __builtin_amdgcn_sched_barrier(0);
       if (++rb == nbs) {
         rb = 0;
-        rt += tstride;
+        rt += w.tstride;
       }
       if (++bl == nbs) {  // the tile's slice is done (uniform over the wave)
-        if (u < W) {
+        if (u < w.W) {
           float r = acc;
           r += __shfl_xor(r, 16, 64);
           r += __shfl_xor(r, 32, 64);
@@ -624,10 +628,155 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
         }
         acc = 0.f;
         bl = 0;
-        tile += tstride;
+        tile += w.tstride;
       }
     }
   }
+}
+
+__device__ __forceinline__ void ks_zero(const KsArgs& a, uint8_t* lds, int tid) {
+  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// every wave's prologue loads enter the CU's memory queues before any weight load
+__device__ __forceinline__ void loads_first() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int T, int D>
+__global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const KsWave w(a, (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6));
+  // the slice of x: elements [256 b0, 256 (b0 + nbs)), chunk tid of 8
+  const uint32_t nch = a.nbs * 32, c = (uint32_t)tid;
+  const float4* x4 = (const float4*)(a.x + (uint64_t)w.b0 * 256u) + 2 * min(c, nch - 1);  // clamped: unconditional
+  const float4 xv0 = x4[0], xv1 = x4[1];
+  loads_first();
+  KBuf<T> buf[D];
+  ks_prefetch<T, D>(a, w, buf, lane);
+  {  // whole 32-element groups are in or out of the slice (nch % 32 == 0)
+    float v[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
+    quantize_chunk(v, c, c < nch, lds, (float4*)(lds + a.xs_off));
+  }
+  ks_zero(a, lds, tid);
+  __syncthreads();
+  ks_run<T, D>(a, w, buf, lds, lane);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
+  acc.x = fmaf(w, v.x, acc.x);
+  acc.y = fmaf(w, v.y, acc.y);
+  acc.z = fmaf(w, v.z, acc.z);
+  acc.w = fmaf(w, v.w, acc.w);
+  return acc;
+}
+
+// The O projection fed by the attention's chunk records (head dim 128, G
+// query heads per kv head; the slice of workgroup g is kv head g mod 8).
+// Per query head h of the slice, over the chunk records c (k_attn_decode:
+// unnormalised o_c, max m_c, sum l_c), as k_attn_merge forms them:
+//   M = max_c m_c,  x_h = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c
+// (softmax over all attended rows, src/model/forward.rs:398-409).  Wave g < G
+// reduces M and the denominator of head g; thread (split sp, float4 column)
+// sums chunks sp, sp + NS, ...; the first kMergeFirst chunks' loads are
+// issued with the prologue, later chunks (long contexts) are read in a loop.
+constexpr uint32_t kMergeFirst = 48;
+
+template <int T, int D, int G>
+__global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
+  constexpr int HD = 128, SD = G * HD, NC4 = SD / 4, NS = kThreads / NC4, KB = (int)kMergeFirst / NS;
+  static_assert(kThreads % NC4 == 0 && SD / 8 <= kThreads, "slice shape");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ float4 red[kThreads];
+  __shared__ __attribute__((aligned(16))) float xsl[SD];
+  __shared__ float sm[G], sd[G];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
+  const KsWave w(a, wave);
+  // attended rows (as k_attn_decode reads them) and their chunk records
+  const uint32_t len = a.state->len, attn_lo = a.state->attn_lo, attn_end = a.state->attn_end;
+  const uint32_t hi = attn_end ? attn_end : len + 1, nrows = hi > attn_lo ? hi - attn_lo : 0u;
+  const uint32_t nch = min((nrows + a.chunk - 1) / a.chunk, a.max_chunks);
+  const uint32_t rec = attn_partial_floats(G, HD);
+  const float* base = a.partial + (uint64_t)(blockIdx.x % kKs) * a.max_chunks * rec;
+  const float* ml = base + SD;  // chunk c: max at ml[c rec + g], sum at ml[c rec + G + g]
+  const uint32_t sp = (uint32_t)tid / NC4, col = (uint32_t)tid % NC4, g = col / (HD / 4);
+  // The first loads take chunks up to kMergeFirst - 1 clamped to the buffer,
+  // not to nch: their addresses do not wait for the state, and what lies past
+  // nch (records of earlier steps, or never written) is masked out by selects.
+  const uint32_t cl = a.max_chunks - 1;
+  // wave g < G: the max and sum of head g over chunks lane, lane + 64, ... (issued first)
+  float m0 = -INFINITY, l0 = 0.f;
+  if (wave < (uint32_t)G) {
+    const uint64_t at = (uint64_t)min((uint32_t)lane, cl) * rec;
+    m0 = ml[at + wave];
+    l0 = ml[at + G + wave];
+  }
+  float4 ov[KB];
+  float mk[KB];
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const uint64_t at = (uint64_t)min(sp + (uint32_t)(NS * k), cl) * rec;  // clamped: unconditional
+    ov[k] = ((const float4*)(base + at))[col];
+    mk[k] = ml[at + g];
+  }
+  loads_first();
+  KBuf<T> buf[D];
+  ks_prefetch<T, D>(a, w, buf, lane);
+
+  if (wave < (uint32_t)G) {
+    float M = (uint32_t)lane < nch ? m0 : -INFINITY;
+    for (uint32_t c = lane + 64; c < nch; c += 64) M = fmaxf(M, ml[(uint64_t)c * rec + wave]);
+    M = wave_max(M);
+    float den = (uint32_t)lane < nch ? l0 * expf(m0 - M) : 0.f;
+    for (uint32_t c = lane + 64; c < nch; c += 64)
+      den = fmaf(ml[(uint64_t)c * rec + G + wave], expf(ml[(uint64_t)c * rec + wave] - M), den);
+    den = wave_sum(den);
+    if (lane == 0) {
+      sm[wave] = M;
+      sd[wave] = den;
+    }
+  }
+  __syncthreads();
+  const float M = sm[g];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < KB; k++)
+    if (sp + (uint32_t)(NS * k) < nch) acc = fma4(expf(mk[k] - M), ov[k], acc);
+  for (uint32_t c = sp + kMergeFirst; c < nch; c += NS) {
+    const uint64_t at = (uint64_t)c * rec;
+    acc = fma4(expf(ml[at + g] - M), ((const float4*)(base + at))[col], acc);
+  }
+  red[tid] = acc;
+  __syncthreads();
+  if ((uint32_t)tid < NC4) {
+    float4 o = red[tid];
+#pragma unroll
+    for (int q = 1; q < NS; q++) {
+      const float4 r = red[q * NC4 + tid];
+      o = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+    }
+    const float den = sd[g];
+    *(float4*)&xsl[4 * tid] = nch > 0 ? make_float4(o.x / den, o.y / den, o.z / den, o.w / den)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __syncthreads();
+  if (wave < (uint32_t)(SD / 8 / 64)) {  // whole waves: chunk tid of 8 elements
+    const float4 u = *(const float4*)&xsl[8 * tid], v4 = *(const float4*)&xsl[8 * tid + 4];
+    float v[8] = {u.x, u.y, u.z, u.w, v4.x, v4.y, v4.z, v4.w};
+    quantize_chunk(v, (uint32_t)tid, true, lds, (float4*)(lds + a.xs_off));
+  }
+  ks_zero(a, lds, tid);
+  __syncthreads();
+  ks_run<T, D>(a, w, buf, lds, lane);
 }
 
 int cu_count() {
@@ -739,19 +888,20 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   }
 }
 
-// The K-split residual launch (k_gemv_ks) where it applies: one Q4_K / Q6_K
-// segment without a norm, K in whole slices of at most 16 blocks, and at least
-// one tile per wave of the grid.  hipErrorNotSupported otherwise (the caller
-// takes launch_mfma).
-hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st) {
+// The K-split residual launches where they apply: one Q4_K / Q6_K segment
+// without a norm, K in whole slices of at most 16 blocks, and at least one
+// tile per wave of the grid; hipErrorNotSupported otherwise (the caller takes
+// launch_mfma).
+namespace {
+hipError_t ks_plan(const GemvLaunch& L, float* h, KsArgs& a, uint32_t& blocks, size_t& lds, int& D) {
   if (L.nseg != 1 || L.norm_w || L.paired || !mfma_type(L.seg[0].type) || L.cols == 0 || L.cols % 256)
     return hipErrorNotSupported;
-  const uint32_t nbr = L.cols / 256, blocks = (uint32_t)cu_count();
+  const uint32_t nbr = L.cols / 256;
+  blocks = (uint32_t)cu_count();
   const uint32_t ntiles = (uint32_t)((L.seg[0].rows + kTileRows - 1) / kTileRows);
-  if (nbr % kKs || nbr / kKs > kKsMaxBlocks || blocks % kKs ||
-      ntiles < blocks / kKs * kWaves)
+  if (nbr % kKs || nbr / kKs > kKsMaxBlocks || blocks % kKs || ntiles < blocks / kKs * kWaves)
     return hipErrorNotSupported;
-  KsArgs a{};
+  a = KsArgs{};
   a.seg = L.seg[0];
   a.ntiles = ntiles;
   a.nbr = nbr;
@@ -760,18 +910,74 @@ hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st
   a.h = h;
   a.xs_off = 768u * a.nbs;              // digit planes: 48 bytes per 16 elements
   a.zero_off = a.xs_off + 128u * a.nbs;  // group sums: 16 bytes per 32 elements
-  const size_t lds = a.zero_off + kZeroBytes;
+  lds = a.zero_off + kZeroBytes;
   // units per wave: a ring as deep as the work, up to 8
   const uint32_t w = ((ntiles - 1) / (blocks / kKs * kWaves) + 1) * a.nbs;
-  const int D = w <= 2 ? 2 : w <= 4 ? 4 : 8;
-  const bool q6 = L.seg[0].type == T_Q6K;
+  D = w <= 2 ? 2 : w <= 4 ? 4 : 8;
+  return hipSuccess;
+}
+
+template <class F>
+hipError_t ks_go(bool q6, int D, F&& go) {
+  if (D == 2) return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 2>{})
+                        : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 2>{});
+  if (D == 4) return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 4>{})
+                        : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 4>{});
+  return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 8>{})
+            : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 8>{});
+}
+}  // namespace
+
+hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st) {
+  KsArgs a;
+  uint32_t blocks;
+  size_t lds;
+  int D;
+  const hipError_t e = ks_plan(L, h, a, blocks, lds, D);
+  if (e != hipSuccess) return e;
+  return ks_go(L.seg[0].type == T_Q6K, D, [&](auto t, auto d) {
+    hipLaunchKernelGGL((k_gemv_ks<decltype(t)::value, decltype(d)::value>), dim3(blocks), dim3(kThreads), lds, st, a);
+    return hipGetLastError();
+  });
+}
+
+uint32_t merge_o_first_chunks() { return kMergeFirst; }
+
+bool merge_o_supported(const GemvLaunch& L, const AttnArgs& at) {
+  KsArgs a;
+  uint32_t blocks;
+  size_t lds;
+  int D;
+  if (ks_plan(L, nullptr, a, blocks, lds, D) != hipSuccess) return false;
+  const uint32_t G = at.n_kv_heads ? at.n_heads / at.n_kv_heads : 0;
+  return at.n_kv_heads == kKs && at.n_heads == G * kKs && at.head_dim == 128 && (G == 4 || G == 8) &&
+         a.nbs * 256 == G * 128 && at.max_chunks > 0 && at.chunk > 0;
+}
+
+hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, float* h, hipStream_t st) {
+  if (!merge_o_supported(L, at)) return hipErrorInvalidValue;
+  KsArgs a;
+  uint32_t blocks;
+  size_t lds;
+  int D;
+  (void)ks_plan(L, h, a, blocks, lds, D);
+  a.x = nullptr;
+  a.partial = at.partial;
+  a.state = at.state;
+  a.max_chunks = at.max_chunks;
+  a.chunk = at.chunk;
+  // a ring of at most 4: the first merge batch holds up to 120 registers
+  const bool g8 = at.n_heads / at.n_kv_heads == 8, q6 = L.seg[0].type == T_Q6K;
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a);
     return hipGetLastError();
   };
-  if (D == 2) return q6 ? go(k_gemv_ks<T_Q6K, 2>) : go(k_gemv_ks<T_Q4K, 2>);
-  if (D == 4) return q6 ? go(k_gemv_ks<T_Q6K, 4>) : go(k_gemv_ks<T_Q4K, 4>);
-  return q6 ? go(k_gemv_ks<T_Q6K, 8>) : go(k_gemv_ks<T_Q4K, 8>);
+  if (D == 2) {
+    if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, 2, 8>) : go(k_gemv_ks_merge<T_Q4K, 2, 8>);
+    return q6 ? go(k_gemv_ks_merge<T_Q6K, 2, 4>) : go(k_gemv_ks_merge<T_Q4K, 2, 4>);
+  }
+  if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, 4, 8>) : go(k_gemv_ks_merge<T_Q4K, 4, 8>);
+  return q6 ? go(k_gemv_ks_merge<T_Q6K, 4, 4>) : go(k_gemv_ks_merge<T_Q4K, 4, 4>);
 }
 
 template hipError_t launch_mfma<EpiStore>(const GemvLaunch&, const EpiStore&, hipStream_t);

@@ -8,6 +8,9 @@
   loop equal to the oracle's picks.
 * 70B shape: decode over an 8192-row cache (two layers; 129 chunk records per
   kv head to merge).
+* The attention merge in the O projection's prologue (the default up to 48
+  chunk records) forced at 63 and 129 records, and the separate merge launch
+  forced at 33.
 * Long caches past one merge batch (256 chunks of 64 rows): 4200 and 20000
   rows at query-group sizes 1, 4 and 8, with the f32 and the f16 cache.
 * Tiny model prefill chunks of 129, 300 and 512 ids (several 128-query
@@ -98,6 +101,33 @@ def test_70b_decode_over_8192_rows(tmpdir_session):
     p = _model(tmpdir_session, "l70b_2l.gguf", spec, 70)
     g, o = GpuModel(p), orc.Model(p)
     _decode_from_import(g, o, 8192, 8320, 4, 4242, seed=45)
+    g.close()
+    o.close()
+
+
+@pytest.mark.parametrize("shape,rows", [("8b", 4000), ("70b", 8192)])
+def test_merge_in_o_projection_long(tmpdir_session, monkeypatch, shape, rows):
+    """The attention merge in the O projection's prologue (taken by default up
+    to 48 chunk records) forced at 63 and 129 records per kv head: the chunks
+    past its first batch, and past 64 for the maximum and the denominator, are
+    read in its loops."""
+    monkeypatch.setenv("IFX_MERGE_O", "1")
+    base, name, seed = (synth.LLAMA3_8B, "l8b_2l.gguf", 8) if shape == "8b" else (synth.LLAMA3_70B, "l70b_2l.gguf", 70)
+    spec = synth.reduced(base, n_layers=2, ctx=512)
+    p = _model(tmpdir_session, name, spec, seed)
+    g, o = GpuModel(p), orc.Model(p)
+    _decode_from_import(g, o, rows, rows + 8, 2, 321, seed=rows + 7)
+    g.close()
+    o.close()
+
+
+def test_separate_merge_short_context(tmpdir_session, monkeypatch):
+    """The separate merge launch forced where the fused one is the default (2048 rows)."""
+    monkeypatch.setenv("IFX_MERGE_O", "0")
+    spec = synth.reduced(synth.LLAMA3_8B, n_layers=2, ctx=512)
+    p = _model(tmpdir_session, "l8b_2l.gguf", spec, 8)
+    g, o = GpuModel(p), orc.Model(p)
+    _decode_from_import(g, o, 2048, 2304, 2, 1000, seed=51)
     g.close()
     o.close()
 
