@@ -38,9 +38,13 @@ CTX = 2048
 METRIC = "decode tok/s, 8B Q4_K_M bs=1, 1×MI355X; % of HBM-BW roofline"
 KCLASS = ["embed", "qkv_gemv", "attention", "attn_output_gemv", "ffn_gate_up_gemv", "ffn_down_gemv",
           "output_head_gemv", "finalize"]
-KERNEL_NAMES = {1: "k_gemv_mfma<EpiQkv, Q4_K, Q6_K>", 2: "k_attn_decode<128, G> + k_attn_merge<128, G>",
-                3: "k_gemv_mfma<EpiResidual, Q4_K>", 4: "k_gemv_mfma<EpiSwiglu, Q4_K>",
-                5: "k_gemv_mfma<EpiResidual, Q6_K>", 6: "k_gemv_mfma<EpiLogits, Q6_K>"}
+# kernels of each class in the 8B / 70B decode step (the attention's merge runs
+# in the O launch while a step attends at most 48 chunk records of 64 rows)
+KERNEL_NAMES = {1: "k_gemv_mfma<EpiQkv, Q4_K, Q6_K>",
+                2: "k_attn_decode<128, G> (+ k_attn_merge<128, G> past 48 chunks)",
+                3: "k_gemv_ks_merge<Q4_K> (merge + O + residual; k_gemv_ks<Q4_K> past 48 chunks)",
+                4: "k_gemv_mfma<EpiSwiglu, Q4_K>",
+                5: "k_gemv_ks<Q6_K> (down + residual)", 6: "k_gemv_mfma<EpiLogits, Q6_K>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_PROBE_BYTES = 256 << 20
 
