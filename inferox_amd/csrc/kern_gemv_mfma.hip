@@ -571,13 +571,15 @@ struct KsWave {
 
 // Ring: slot i holds unit u = i (mod D); unit u is block b0 + u mod nbs of
 // tile t0 + (u / nbs) tstride.  Loads past the wave's last unit (and all of a
-// wave without tiles) read a unit of tile 0 of the slice: in bounds, unused,
-// and unconditional, so that the compiler's waits count one path.
+// wave without tiles) read the slice's first unit (tile 0): in bounds, unused,
+// shared (an L2 hit), and unconditional, so that the compiler's waits count
+// one path.
 template <int T, int D>
 __device__ __forceinline__ void ks_prefetch(const KsArgs& a, const KsWave& w, KBuf<T> (&buf)[D], int lane) {
 #pragma unroll
   for (int i = 0; i < D; i++) {
-    const uint32_t u = (uint32_t)i < w.W ? (uint32_t)i : 0u, tl = w.W > 0 ? w.t0 + (u / a.nbs) * w.tstride : 0u;
+    const bool past = (uint32_t)i >= w.W;
+    const uint32_t u = past ? 0u : (uint32_t)i, tl = past ? 0u : w.t0 + (u / a.nbs) * w.tstride;
     buf[i].load(unit_ptr<T>(a.seg, a.nbr, tl, w.b0 + u % a.nbs), (uint32_t)lane, a.seg.q6_signed);
     __builtin_amdgcn_sched_barrier(0);  // slots in ring order
   }
@@ -609,8 +611,11 @@ __device__ __forceinline__ void ks_run(const KsArgs& a, const KsWave& w, KBuf<T>
       const float4 xa = xs4[8 * bl], xb = xs4[8 * bl + 4];
       const float v = buf[i].dot(A, xa, xb, ag);
       acc += u < w.W ? v : 0.f;
+      // past the wave's last unit: the slice's first unit, which every such
+      // refill shares (an L2 hit; the wave's own first unit is gone from L2
+      // under the stream)
       const bool past = u + D >= w.W;
-      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? w.t0 : rt, w.b0 + (past ? 0u : rb)), (uint32_t)lane,
+      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? 0u : rt, w.b0 + (past ? 0u : rb)), (uint32_t)lane,
                   a.seg.q6_signed);
       // keep the ring order (see run_seg)
       __builtin_amdgcn_sched_barrier(0);
