@@ -63,13 +63,15 @@ struct ifx_session {
   DevState* state = nullptr;
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
   uint32_t attn_chunk = 64, max_chunks = 0;
-  // captured steps: [sampling][merge_o] (the greedy step, the step with
-  // k_sample before finalize; each with the attention merge in its own launch
-  // or in the O projection's prologue)
-  hipGraphExec_t exec[2][2] = {};
-  bool graph_tried[2][2] = {};
+  // captured steps: [sampling][merge bound / 8] (the greedy step, the step
+  // with k_sample before finalize; each with the attention merge in its own
+  // launch (bound 0) or in the O projection's prologue, which loads the first
+  // `merge_bound` chunk records up front)
+  static constexpr int kMergeGraphs = 7;
+  hipGraphExec_t exec[2][kMergeGraphs] = {};
+  bool graph_tried[2][kMergeGraphs] = {};
   bool sampling = false;                 // set for the duration of ifx_generate_sampled
-  bool merge_o = false;                  // the step being enqueued merges the attention in the O launch
+  uint32_t merge_bound = 0;              // of the step being enqueued: 0, or a multiple of 8 up to 48
   float* probs = nullptr;                // k_sample scratch [vocab]
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
@@ -260,9 +262,9 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       go.cols = D;
       go.x = s->attn;
       // the merge of the chunk records moves into the O launch's prologue
-      const bool fused = s->merge_o && merge_o_supported(go, a);
+      const bool fused = s->merge_bound && merge_o_supported(go, a);
       if (k == 2) IFX_HIP(fused ? launch_attn_partials(a, st) : launch_attn_decode(a, st));
-      else IFX_HIP(fused ? launch_mfma_residual_merge(go, a, s->hidden, st) : gemv_residual(go, s->hidden, st));
+      else IFX_HIP(fused ? launch_mfma_residual_merge(go, a, s->hidden, st, s->merge_bound) : gemv_residual(go, s->hidden, st));
       return IFX_OK;
     }
     case 4: {
@@ -307,21 +309,28 @@ uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->
 
 // The attention merge goes into the O launch's prologue while the attended
 // rows make at most merge_o_first_chunks() chunk records (every workgroup
-// reads them all; past that the separate merge launch is faster).  `rows`
-// bounds the rows the step attends (the cache rows before it + 1).
-// IFX_MERGE_O=0 / 1 takes the separate / the fused merge at any length.
+// reads them all; past that the separate merge launch is faster), with the
+// step's chunk count rounded up to a multiple of merge_o_bound_step() as the
+// records its prologue loads.  `rows` bounds the rows the step attends (the
+// cache rows before it + 1).  IFX_MERGE_O=0 / 1 takes the separate / the
+// fused merge at any length.
 void choose_merge(ifx_session* s, uint64_t rows) {
+  const uint64_t nch = (rows + s->attn_chunk - 1) / s->attn_chunk, step = merge_o_bound_step();
+  const uint32_t most = merge_o_first_chunks();
+  const uint32_t bound = (uint32_t)std::max<uint64_t>(step, (nch + step - 1) / step * step);
   const char* f = getenv("IFX_MERGE_O");
-  if (f && (f[0] == '0' || f[0] == '1') && f[1] == 0) s->merge_o = f[0] == '1';
-  else s->merge_o = (rows + s->attn_chunk - 1) / s->attn_chunk <= merge_o_first_chunks();
+  if (f && (f[0] == '0' || f[0] == '1') && f[1] == 0) s->merge_bound = f[0] == '1' ? std::min(bound, most) : 0;
+  else s->merge_bound = nch <= most ? bound : 0;
 }
 
 // Replay the captured step (capturing it on first use); direct launches if the
 // runtime refuses capture.
 int run_step(ifx_session* s, uint64_t rows) {
   choose_merge(s, rows);
-  hipGraphExec_t& exec = s->exec[s->sampling][s->merge_o];
-  bool& tried = s->graph_tried[s->sampling][s->merge_o];
+  const int gi = (int)(s->merge_bound / merge_o_bound_step());
+  if (gi >= ifx_session::kMergeGraphs) return set_error(IFX_E_INVALID_ARG, "merge bound %u", s->merge_bound);
+  hipGraphExec_t& exec = s->exec[s->sampling][gi];
+  bool& tried = s->graph_tried[s->sampling][gi];
   if (!tried) {
     tried = true;
     // IFX_NO_GRAPH=1: launch the step's kernels directly (used under profilers

@@ -556,6 +556,7 @@ struct KsArgs {
   const float* partial;
   const DevState* state;
   uint32_t max_chunks, chunk;
+  uint32_t first;  // the prologue loads chunks [0, first) (a bound the host keeps above the step's count)
 };
 
 // The wave's units: tiles t0, t0 + tstride, ... x the slice's nbs blocks.
@@ -694,6 +695,7 @@ __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
 // sums chunks sp, sp + NS, ...; the first kMergeFirst chunks' loads are
 // issued with the prologue, later chunks (long contexts) are read in a loop.
 constexpr uint32_t kMergeFirst = 48;
+constexpr uint32_t kMergeBoundStep = 8;  // the host's bounds are multiples of this
 
 template <int T, int D, int G>
 __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
@@ -714,14 +716,16 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   const float* base = a.partial + (uint64_t)(blockIdx.x % kKs) * a.max_chunks * rec;
   const float* ml = base + SD;  // chunk c: max at ml[c rec + g], sum at ml[c rec + G + g]
   const uint32_t sp = (uint32_t)tid / NC4, col = (uint32_t)tid % NC4, g = col / (HD / 4);
-  // The first loads take chunks up to kMergeFirst - 1 clamped to the buffer,
-  // not to nch: their addresses do not wait for the state, and what lies past
-  // nch (records of earlier steps, or never written) is masked out by selects.
-  const uint32_t cl = a.max_chunks - 1;
+  // The first loads do not wait for the state: the max and sum of chunks
+  // lane < 64 are clamped to the buffer, the records' o of chunks < fe (the
+  // host's bound, a multiple of NS, or the buffer) to fe - 1 (repeats: cache
+  // hits); what lies past nch (records of earlier steps, or never written)
+  // is masked out by selects.
+  const uint32_t fe = min(min(a.first, kMergeFirst), a.max_chunks), cl = fe - 1;
   // wave g < G: the max and sum of head g over chunks lane, lane + 64, ... (issued first)
   float m0 = -INFINITY, l0 = 0.f;
   if (wave < (uint32_t)G) {
-    const uint64_t at = (uint64_t)min((uint32_t)lane, cl) * rec;
+    const uint64_t at = (uint64_t)min((uint32_t)lane, a.max_chunks - 1) * rec;
     m0 = ml[at + wave];
     l0 = ml[at + G + wave];
   }
@@ -753,10 +757,11 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   __syncthreads();
   const float M = sm[g];
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const uint32_t nb = min(nch, fe);
 #pragma unroll
   for (int k = 0; k < KB; k++)
-    if (sp + (uint32_t)(NS * k) < nch) acc = fma4(expf(mk[k] - M), ov[k], acc);
-  for (uint32_t c = sp + kMergeFirst; c < nch; c += NS) {
+    if (sp + (uint32_t)(NS * k) < nb) acc = fma4(expf(mk[k] - M), ov[k], acc);
+  for (uint32_t c = sp + fe; c < nch; c += NS) {
     const uint64_t at = (uint64_t)c * rec;
     acc = fma4(expf(ml[at + g] - M), ((const float4*)(base + at))[col], acc);
   }
@@ -947,6 +952,7 @@ hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st
 }
 
 uint32_t merge_o_first_chunks() { return kMergeFirst; }
+uint32_t merge_o_bound_step() { return kMergeBoundStep; }
 
 bool merge_o_supported(const GemvLaunch& L, const AttnArgs& at) {
   KsArgs a;
@@ -959,8 +965,9 @@ bool merge_o_supported(const GemvLaunch& L, const AttnArgs& at) {
          a.nbs * 256 == G * 128 && at.max_chunks > 0 && at.chunk > 0;
 }
 
-hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, float* h, hipStream_t st) {
-  if (!merge_o_supported(L, at)) return hipErrorInvalidValue;
+hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, float* h, hipStream_t st,
+                                      uint32_t first) {
+  if (!merge_o_supported(L, at) || first == 0) return hipErrorInvalidValue;
   KsArgs a;
   uint32_t blocks;
   size_t lds;
@@ -971,6 +978,9 @@ hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, f
   a.state = at.state;
   a.max_chunks = at.max_chunks;
   a.chunk = at.chunk;
+  // a multiple of the splits of a workgroup's chunks (2 or 4): the batch and
+  // the loop after it then cover each chunk once
+  a.first = std::min((first + kMergeBoundStep - 1) / kMergeBoundStep * kMergeBoundStep, kMergeFirst);
   // a ring of at most 4: the first merge batch holds up to 120 registers
   const bool g8 = at.n_heads / at.n_kv_heads == 8, q6 = L.seg[0].type == T_Q6K;
   auto go = [&](auto kern) {

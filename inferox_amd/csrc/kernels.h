@@ -194,11 +194,15 @@ hipError_t launch_attn_partials(const AttnArgs& a, hipStream_t st);
 // (kern_gemv_mfma.hip): x is formed from a.partial, the chunk records that
 // launch_attn_partials left, for the rows a.state attends.  Needs 8 kv heads,
 // head dim 128, 4 or 8 query heads per kv head and a K-split launch of
-// W_o (merge_o_supported); any chunk count, the first merge_o_first_chunks()
-// of them loaded with the prologue.
+// W_o (merge_o_supported).  Any chunk count: the first min(first,
+// merge_o_first_chunks()) records are loaded with the prologue (without
+// waiting for the state), the rest in a loop; `first` is best a bound a
+// little above the steps' chunk count (a multiple of merge_o_bound_step()).
 bool merge_o_supported(const GemvLaunch& L, const AttnArgs& a);
-hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& a, float* h, hipStream_t st);
+hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& a, float* h, hipStream_t st,
+                                      uint32_t first);
 uint32_t merge_o_first_chunks();
+uint32_t merge_o_bound_step();
 // head dims the decode attention takes: multiples of 4 (f32 cache) or 8 (f16) up to 256
 bool attn_decode_head_dim(uint32_t head_dim, bool kv_f16);
 // floats of one partial record (per kv head and chunk): o[group][head_dim],
