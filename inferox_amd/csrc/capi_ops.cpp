@@ -47,7 +47,10 @@ static hipStream_t stream_of(void* s) { return s ? (hipStream_t)s : g_stream; }
 hipStream_t library_stream() { return g_stream; }
 
 DevW devw(const ifx_tensor* t) {
-  return DevW{t->L.type, t->L.cols, t->L.body, t->L.scal, t->L.q6_signed};
+  DevW w{t->L.type, t->L.cols, t->L.body, t->L.scal, t->L.q6_signed, 0, 0};
+  if (t->L.type == T_Q4K || t->L.type == T_Q6K)
+    tile_strides(t->L.type, t->L.rows, &w.tstride, &w.bstride);
+  return w;
 }
 
 // Runs fn(i0, i1) over [0, n) in contiguous ranges, one worker per core share.
@@ -304,7 +307,7 @@ int ifx_gemv(const ifx_tensor* w, const float* x, float* y, void* stream) {
   IFX_TRY(device_init());
   if (!w || !x || !y) return set_error(IFX_E_INVALID_ARG, "null argument");
   GemvLaunch L;
-  L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.q6_signed};
+  L.seg[0] = gemv_seg(w->L);
   L.nseg = 1;
   L.cols = (uint32_t)w->L.cols;
   L.x = x;
@@ -331,7 +334,7 @@ int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, voi
                     part_bytes};
     hipError_t e = launch_prep_rows(a, (uint32_t)m, (uint32_t)k, (uint32_t)k, nullptr, 0.f, in, st);
     if (e == hipSuccess) {
-      const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols, w->L.q6_signed};
+      const GemmW gw = gemm_w(w->L);
       e = gemm_store(in, gw, c, (uint32_t)w->L.rows, st);
     }
     const hipError_t ef = hipFreeAsync(buf, st);
@@ -341,7 +344,7 @@ int ifx_matmul_qt(const float* a, uint64_t m, const ifx_tensor* w, float* c, voi
   }
   for (uint64_t i = 0; i < m; i++) {
     GemvLaunch L;
-    L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.q6_signed};
+    L.seg[0] = gemv_seg(w->L);
     L.nseg = 1;
     L.cols = (uint32_t)w->L.cols;
     L.x = a + i * w->L.cols;

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ifx_common.h"
+
 namespace ifx {
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
@@ -90,7 +92,8 @@ struct DevW {
   uint64_t cols;
   const uint8_t* body;
   const uint8_t* scal;
-  uint32_t q6_signed = 0;  // Q6_K: int8 scale bytes (ggml's), else u8 (the reference's)
+  uint32_t q6_signed;  // Q6_K: int8 scale bytes (ggml's), else u8 (the reference's)
+  uint64_t tstride, bstride;  // Q4_K / Q6_K: unit (t, b) at body + t tstride + b bstride (tile_strides)
 };
 
 // Element e (row-major flat index) of a matrix in the device layout; same
@@ -114,7 +117,7 @@ __device__ __forceinline__ float dev_elem(const DevW& w, uint64_t e) {
     }
     case 12: {  // tiled Q4_K (ifx_common.h): same arithmetic as raw_elem
       const uint64_t row = e / w.cols, col = e % w.cols;
-      const uint8_t* u = w.body + ((row >> 4) * (w.cols >> 8) + (col >> 8)) * 2304;
+      const uint8_t* u = w.body + (row >> 4) * w.tstride + (col >> 8) * w.bstride;
       const int n = (int)(row & 15), j = (int)(col & 255), g = j / 32, l = j % 32;
       const uint8_t* h = u + 16 * n;
       float d = h2f(ld_u16_unaligned(h)), dmin = h2f(ld_u16_unaligned(h + 2));
@@ -128,7 +131,7 @@ __device__ __forceinline__ float dev_elem(const DevW& w, uint64_t e) {
     }
     case 14: {  // tiled Q6_K
       const uint64_t row = e / w.cols, col = e % w.cols;
-      const uint8_t* u = w.body + ((row >> 4) * (w.cols >> 8) + (col >> 8)) * 3360;
+      const uint8_t* u = w.body + (row >> 4) * w.tstride + (col >> 8) * w.bstride;
       const int n = (int)(row & 15), j = (int)(col & 255), s = j / 32, k = j & 15;
       const int lane = n + 16 * (s & 3), c = 2 * (s >> 2) + ((j >> 4) & 1);
       uint32_t qlb = u[(s >> 2) * 1024 + lane * 16 + ((j >> 1) & 15)];

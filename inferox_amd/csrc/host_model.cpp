@@ -171,7 +171,7 @@ int check_dims(const ifx_model* m) {
 }
 
 GemvSeg seg_of(const ifx_tensor* t) {
-  return GemvSeg{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.q6_signed};
+  return gemv_seg(t->L);
 }
 
 // The batched prefill GEMM takes the quantized matrices whose operands it can
@@ -191,7 +191,7 @@ bool gemm_eligible(const ifx_model* m) {
   return true;
 }
 GemmW gw(const ifx_tensor* t) {
-  return GemmW{t->L.body, t->L.scal, t->L.type, (uint32_t)t->L.rows, t->L.cols, t->L.q6_signed};
+  return gemm_w(t->L);
 }
 
 // Kernel classes of one step (ifx_session_profile): 0 embed, 1 qkv + rope +

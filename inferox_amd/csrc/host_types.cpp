@@ -199,7 +199,7 @@ void ggml_kquant_to_reference(uint32_t type, const uint8_t* in, uint64_t n_block
 
 void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t cols, uint64_t t0, uint64_t t1,
                   uint8_t* body) {
-  const uint64_t nbr = cols / 256, bb = type == T_Q4K ? 144 : 210;
+  const uint64_t nbr = cols / 256, bb = type == T_Q4K ? 144 : 210, tiles = row_tiles(rows);
   const uint64_t unit = type == T_Q4K ? kUnitQ4K : kUnitQ6K;
   const uint8_t* blk[kTileRows];
   for (uint64_t t = t0; t < t1; t++)
@@ -208,7 +208,7 @@ void repack_tiles(uint32_t type, const uint8_t* src, uint64_t rows, uint64_t col
         const uint64_t r = t * kTileRows + n;
         blk[n] = r < rows ? src + (r * nbr + b) * bb : nullptr;
       }
-      pack_unit(type, blk, body + (t * nbr + b) * unit);
+      pack_unit(type, blk, body + tile_unit(t, b, tiles) * unit);
     }
 }
 

@@ -58,7 +58,13 @@ const char* type_name(uint32_t t);
 //   Q8_K     : body[nb][288] = sc[32] | qs[256]  and  dd[nb] = {d, dmin} (f16 x 2).
 //   Q4_K, Q6_K (tiled, for the int8-MFMA GEMV): rows are grouped in tiles of
 //     16 (the last tile padded with zero blocks); unit (t, b) holds block b of
-//     rows 16t..16t+15 at ((t * cols/256) + b) * unit bytes.  Lane L = n + 16g
+//     rows 16t..16t+15 at unit tile_unit(t, b, tiles), block-major: the
+//     units of block b of all tiles are consecutive (the kernels take the
+//     byte strides of tile_strides).  The GEMV, K-split GEMV and GEMM
+//     launches read a block of many tiles at a time, so the whole GPU streams
+//     one contiguous region (a 48 MB Q6_K stream with nontemporal loads:
+//     7.3 us, against 9.2 us when each wave streams the units of its own tile
+//     in a tile-major order).  Lane L = n + 16g
 //     (row n, group g = 0..3) owns sub-blocks g and g + 4 (32 elements each)
 //     of row n; its bytes sit where one 16-byte load per lane fetches them.
 //     Q4_K unit (2304 B = 16 x 144):
@@ -74,6 +80,16 @@ const char* type_name(uint32_t t);
 // ---------------------------------------------------------------------------
 constexpr uint64_t kTileRows = 16;
 constexpr uint64_t kUnitQ4K = 16 * 144, kUnitQ6K = 16 * 210;
+__host__ __device__ inline uint64_t row_tiles(uint64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
+// unit index of (tile t, 256-column block b) in a matrix of `tiles` row tiles
+__host__ __device__ inline uint64_t tile_unit(uint64_t t, uint64_t b, uint64_t tiles) { return b * tiles + t; }
+// byte strides of a tile and of a block of a tiled Q4_K / Q6_K matrix: unit
+// (t, b) at body + t tstride + b bstride
+__host__ __device__ inline void tile_strides(uint32_t type, uint64_t rows, uint64_t* tstride, uint64_t* bstride) {
+  const uint64_t unit = type == 12 ? kUnitQ4K : kUnitQ6K;
+  *tstride = unit;
+  *bstride = row_tiles(rows) * unit;
+}
 
 struct DevLayout {
   uint32_t type = 0;

@@ -117,7 +117,7 @@ struct WQ<T_Q4K> {  // tiled Q4_K (src/gguf/dequant.rs:133-161)
   uint2 qs;
   // g: the step's group within its super-block (a constant of the unrolled loop)
   __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t g, int h, bool sb0) {
-    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (ks >> 3)) * kUnitQ4K;
+    const uint8_t* u = w.body + (uint64_t)(row >> 4) * w.tstride + (uint64_t)(ks >> 3) * w.bstride;
     const uint32_t nt = row & 15u;
     if (sb0) hdr = *(const uint4*)(u + 16u * nt);
     qs = *(const uint2*)(u + 256u + (g >> 2) * 1024u + (nt + 16u * (g & 3u)) * 16u + 8u * (uint32_t)h);
@@ -174,7 +174,7 @@ struct WQ<T_Q6K> {  // tiled Q6_K (src/gguf/dequant.rs:182-197)
   int32_t sc;  // u8, or int8 for a tensor read in ggml's layout
   __device__ void load(const GemmW& w, uint32_t row, uint32_t ks, uint32_t g, int h, bool sb0) {
     const uint32_t nt = row & 15u;
-    const uint8_t* u = w.body + ((uint64_t)(row >> 4) * (w.cols >> 8) + (ks >> 3)) * kUnitQ6K;
+    const uint8_t* u = w.body + (uint64_t)(row >> 4) * w.tstride + (uint64_t)(ks >> 3) * w.bstride;
     const uint32_t lane = nt + 16u * (g & 3u), c = 2u * (g >> 2) + (uint32_t)h;
     ql = *(const uint2*)(u + (g >> 2) * 1024u + lane * 16u + 8u * (uint32_t)h);
     hw = *(const uint32_t*)(u + 2048u + lane * 16u + 4u * c);

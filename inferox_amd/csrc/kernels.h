@@ -50,8 +50,14 @@ struct GemvSeg {
   const uint8_t* scal;
   uint32_t type;
   uint32_t rows;
-  uint32_t q6_signed = 0;  // Q6_K with int8 scale bytes (ggml's layout)
+  uint32_t q6_signed;  // Q6_K with int8 scale bytes (ggml's layout)
+  uint64_t tstride, bstride;  // Q4_K / Q6_K: unit (t, b) at body + t tstride + b bstride (tile_strides)
 };
+inline GemvSeg gemv_seg(const DevLayout& L) {
+  GemvSeg s{L.body, L.scal, L.type, (uint32_t)L.rows, L.q6_signed, 0, 0};
+  if (L.type == T_Q4K || L.type == T_Q6K) tile_strides(L.type, L.rows, &s.tstride, &s.bstride);
+  return s;
+}
 
 struct GemvLaunch {
   GemvSeg seg[3];
@@ -92,8 +98,14 @@ struct GemmW {
   uint32_t type;
   uint32_t rows;
   uint64_t cols;
-  uint32_t q6_signed = 0;  // Q6_K with int8 scale bytes (ggml's layout)
+  uint32_t q6_signed;  // Q6_K with int8 scale bytes (ggml's layout)
+  uint64_t tstride, bstride;  // Q4_K / Q6_K: unit (t, b) at body + t tstride + b bstride (tile_strides)
 };
+inline GemmW gemm_w(const DevLayout& L) {
+  GemmW w{L.body, L.scal, L.type, (uint32_t)L.rows, L.cols, L.q6_signed, 0, 0};
+  if (L.type == T_Q4K || L.type == T_Q6K) tile_strides(L.type, L.rows, &w.tstride, &w.bstride);
+  return w;
+}
 // The activation operand as k_prep_rows leaves it (launch_prep_rows): m rows
 // of k columns scaled per row into the fp16 range and split into hi + lo fp16
 // planes, the 32-element group sums, and each row's scale exponent.

@@ -89,7 +89,7 @@ int ifx_matmul_qt_noalloc(const float* a, uint64_t m, const ifx_tensor* w, float
                     (const int*)(s + 2 * bh + bg), (uint32_t)m, (uint32_t)k, (float*)(s + used),
                     kScratchBytes - used};
     IFX_HIP(launch_prep_rows(a, (uint32_t)m, (uint32_t)k, (uint32_t)k, nullptr, 0.f, in, st));
-    const GemmW gw{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.cols, w->L.q6_signed};
+    const GemmW gw = gemm_w(w->L);
     IFX_HIP(gemm_store(in, gw, c, (uint32_t)w->L.rows, st));
     return IFX_OK;
   }
@@ -97,7 +97,7 @@ int ifx_matmul_qt_noalloc(const float* a, uint64_t m, const ifx_tensor* w, float
   // uses no scratch (as ifx_matmul_qt does)
   for (uint64_t i = 0; i < m; i++) {
     GemvLaunch L;
-    L.seg[0] = GemvSeg{w->L.body, w->L.scal, w->L.type, (uint32_t)w->L.rows, w->L.q6_signed};
+    L.seg[0] = gemv_seg(w->L);
     L.nseg = 1;
     L.cols = (uint32_t)k;
     L.x = a + i * k;
