@@ -572,6 +572,13 @@ constexpr uint32_t kKs = 8;
 // destinations the compiler waits on, and a conditional prefetch makes its
 // waits assume the shorter path.)
 constexpr uint32_t kKsMaxBlocks = kThreads * 8 / 256;
+// Units in flight per wave.  Two: the ring is issued in well under a
+// microsecond, so the prologue and the first units' arithmetic overlap the
+// stream.  With all of a wave's units in flight (8 for the 8B down
+// projection) issuing them stalled until the data drained (per-wave
+// timestamps: loads issued at a median 5.2 us, the arithmetic of every unit
+// after 7 us): 13.5 us per launch against 10.7 with 2, 11.6 with 4.
+constexpr int kKsRing = 2;
 
 struct KsArgs {
   GemvSeg seg;
@@ -931,7 +938,7 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
 // tile per wave of the grid; hipErrorNotSupported otherwise (the caller takes
 // launch_mfma).
 namespace {
-hipError_t ks_plan(const GemvLaunch& L, float* h, KsArgs& a, uint32_t& blocks, size_t& lds, int& D) {
+hipError_t ks_plan(const GemvLaunch& L, float* h, KsArgs& a, uint32_t& blocks, size_t& lds) {
   if (L.nseg != 1 || L.norm_w || L.paired || !mfma_type(L.seg[0].type) || L.cols == 0 || L.cols % 256)
     return hipErrorNotSupported;
   const uint32_t nbr = L.cols / 256;
@@ -949,20 +956,7 @@ hipError_t ks_plan(const GemvLaunch& L, float* h, KsArgs& a, uint32_t& blocks, s
   a.xs_off = 768u * a.nbs;              // digit planes: 48 bytes per 16 elements
   a.zero_off = a.xs_off + 128u * a.nbs;  // group sums: 16 bytes per 32 elements
   lds = a.zero_off + kZeroBytes;
-  // units per wave: a ring as deep as the work, up to 8
-  const uint32_t w = ((ntiles - 1) / (blocks / kKs * kWaves) + 1) * a.nbs;
-  D = w <= 2 ? 2 : w <= 4 ? 4 : 8;
   return hipSuccess;
-}
-
-template <class F>
-hipError_t ks_go(bool q6, int D, F&& go) {
-  if (D == 2) return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 2>{})
-                        : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 2>{});
-  if (D == 4) return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 4>{})
-                        : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 4>{});
-  return q6 ? go(std::integral_constant<int, T_Q6K>{}, std::integral_constant<int, 8>{})
-            : go(std::integral_constant<int, T_Q4K>{}, std::integral_constant<int, 8>{});
 }
 }  // namespace
 
@@ -970,13 +964,11 @@ hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st
   KsArgs a;
   uint32_t blocks;
   size_t lds;
-  int D;
-  const hipError_t e = ks_plan(L, h, a, blocks, lds, D);
+  const hipError_t e = ks_plan(L, h, a, blocks, lds);
   if (e != hipSuccess) return e;
-  return ks_go(L.seg[0].type == T_Q6K, D, [&](auto t, auto d) {
-    hipLaunchKernelGGL((k_gemv_ks<decltype(t)::value, decltype(d)::value>), dim3(blocks), dim3(kThreads), lds, st, a);
-    return hipGetLastError();
-  });
+  if (L.seg[0].type == T_Q6K) hipLaunchKernelGGL((k_gemv_ks<T_Q6K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
+  else hipLaunchKernelGGL((k_gemv_ks<T_Q4K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
+  return hipGetLastError();
 }
 
 uint32_t merge_o_first_chunks() { return kMergeFirst; }
@@ -986,8 +978,7 @@ bool merge_o_supported(const GemvLaunch& L, const AttnArgs& at) {
   KsArgs a;
   uint32_t blocks;
   size_t lds;
-  int D;
-  if (ks_plan(L, nullptr, a, blocks, lds, D) != hipSuccess) return false;
+  if (ks_plan(L, nullptr, a, blocks, lds) != hipSuccess) return false;
   const uint32_t G = at.n_kv_heads ? at.n_heads / at.n_kv_heads : 0;
   return at.n_kv_heads == kKs && at.n_heads == G * kKs && at.head_dim == 128 && (G == 4 || G == 8) &&
          a.nbs * 256 == G * 128 && at.max_chunks > 0 && at.chunk > 0;
@@ -999,8 +990,7 @@ hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, f
   KsArgs a;
   uint32_t blocks;
   size_t lds;
-  int D;
-  (void)ks_plan(L, h, a, blocks, lds, D);
+  (void)ks_plan(L, h, a, blocks, lds);
   a.x = nullptr;
   a.partial = at.partial;
   a.state = at.state;
@@ -1009,18 +999,13 @@ hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, f
   // a multiple of the splits of a workgroup's chunks (2 or 4): the batch and
   // the loop after it then cover each chunk once
   a.first = std::min((first + kMergeBoundStep - 1) / kMergeBoundStep * kMergeBoundStep, kMergeFirst);
-  // a ring of at most 4: the first merge batch holds up to 120 registers
   const bool g8 = at.n_heads / at.n_kv_heads == 8, q6 = L.seg[0].type == T_Q6K;
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a);
     return hipGetLastError();
   };
-  if (D == 2) {
-    if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, 2, 8>) : go(k_gemv_ks_merge<T_Q4K, 2, 8>);
-    return q6 ? go(k_gemv_ks_merge<T_Q6K, 2, 4>) : go(k_gemv_ks_merge<T_Q4K, 2, 4>);
-  }
-  if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, 4, 8>) : go(k_gemv_ks_merge<T_Q4K, 4, 8>);
-  return q6 ? go(k_gemv_ks_merge<T_Q6K, 4, 4>) : go(k_gemv_ks_merge<T_Q4K, 4, 4>);
+  if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 8>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 8>);
+  return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 4>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 4>);
 }
 
 template hipError_t launch_mfma<EpiStore>(const GemvLaunch&, const EpiStore&, hipStream_t);
