@@ -252,9 +252,12 @@ __device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool 
 // The prologue in two halves, so that a workgroup issues its x (and norm
 // weight) loads before the weight prefetch: loads return in issue order, and
 // staging must not wait for the prefetched weights.
-template <bool NORM>
+// KB: chunks of 8 elements per thread per batch (the launch takes 1 up to
+// 4096 columns: with more, the clamped surplus loads queued ahead of the
+// weight ring and delayed its issue)
+template <bool NORM, int KB>
 struct XStage {
-  static constexpr int kB = NORM ? 2 : 4;  // chunks of 8 elements per thread per batch
+  static constexpr int kB = KB;
   float4 xv[kB][2], wv[kB][2];
 
   __device__ __forceinline__ void load(const MArgs& a, uint32_t base, int tid) {
@@ -476,11 +479,11 @@ __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D
 // the wave's first D blocks (issued after x, so x is not queued behind them),
 // staging, then the segment.  With the whole ring in flight during staging the
 // 9.4 MB attn_output launch takes 5.4 us instead of 5.8 us.
-template <bool NORM, int T, int NT, int D, class Epi>
+template <bool NORM, int KB, int T, int NT, int D, class Epi>
 __device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename Epi::Wave& ws, int s0, uint32_t first,
                                      uint32_t TG, uint32_t iters, uint32_t j, uint8_t* lds, float* red,
                                      uint32_t a_base, uint32_t a_step, float* part, int tid, int lane, int wave) {
-  XStage<NORM> xs;
+  XStage<NORM, KB> xs;
   xs.load(a, 0, tid);
   // every wave's x loads enter the CU's memory queues before any weight load
   // (a bare barrier: nothing waits for the loads here)
@@ -494,7 +497,7 @@ __device__ __forceinline__ float lead(const MArgs& a, const Epi& epi, typename E
   return nscale;
 }
 
-template <class Epi, int TA, int TB, int D, bool NORM>
+template <class Epi, int TA, int TB, int D, bool NORM, int KB>
 __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, Epi epi) {
   constexpr int NT = Epi::kPaired ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -526,9 +529,9 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
   if (s0 < a.nseg) {
     const uint32_t first = (tg + TG - a.rot[s0]) % TG, iters = block_iters(s0);
     if (TA != TB && ((a.use_b >> s0) & 1u))
-      nscale = lead<NORM, TB, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
+      nscale = lead<NORM, KB, TB, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
     else
-      nscale = lead<NORM, TA, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
+      nscale = lead<NORM, KB, TA, NT, D>(a, epi, ws, s0, first, TG, iters, j, lds, red, a_base, a_step, part, tid, lane, wave);
   }
   // paired launches have one logical segment: no later segments to run
   for (int s = s0 + 1; !Epi::kPaired && s < a.nseg; s++) {
@@ -835,23 +838,26 @@ int cu_count() {
   return n;
 }
 
-template <class Epi, int TA, int TB, int D, bool NORM>
+template <class Epi, int TA, int TB, int D, bool NORM, int KB>
 hipError_t go_one(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
   static bool opted = false;
   if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns (the 70B down projection: 28672)
-    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM, KB>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
     if (e != hipSuccess) return e;
     opted = true;
   }
-  hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D, NORM>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
+  hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D, NORM, KB>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
   return hipGetLastError();
 }
 
 template <class Epi, int TA, int TB, int D>
 hipError_t go(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
-  if (a.norm_w) return go_one<Epi, TA, TB, D, true>(a, epi, blocks, lds, st);
-  return go_one<Epi, TA, TB, D, false>(a, epi, blocks, lds, st);
+  const bool one = a.cols <= 8u * kThreads;  // one chunk of 8 per thread stages all of x
+  if (a.norm_w) return one ? go_one<Epi, TA, TB, D, true, 1>(a, epi, blocks, lds, st)
+                           : go_one<Epi, TA, TB, D, true, 2>(a, epi, blocks, lds, st);
+  return one ? go_one<Epi, TA, TB, D, false, 1>(a, epi, blocks, lds, st)
+             : go_one<Epi, TA, TB, D, false, 4>(a, epi, blocks, lds, st);
 }
 
 template <class Epi, int D>
