@@ -924,6 +924,27 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     a.rot[s] = acc % TG;
     acc += a.ntiles[s];
   }
+  // One tile per workgroup on more workgroups than CUs (the mixed QKV launch:
+  // 384 on 256): workgroup i shares a CU with workgroup i + CUs, and those
+  // pairs end last (per-workgroup stamps: the second ones at 8.3-9.2 us,
+  // against 5.9-6.5 us for workgroups that run alone).  The Q6_K tiles
+  // (3360-byte units against Q4_K's 2304) go to the workgroups that run
+  // alone, [blocks - CUs, CUs), so that no pair carries one: the busiest CU
+  // streams 73.7 KB instead of 90.6 (8B), and the launch takes 8.41-8.44 us
+  // against 8.49-8.63 (graph-order traces).  IFX_QKV_PLACE=0 keeps the plain
+  // rotation.
+  const uint32_t cus = (uint32_t)cu_count();
+  const char* pf = getenv("IFX_QKV_PLACE");
+  const bool place = !(pf && pf[0] == '0' && pf[1] == 0);
+  if (place && mixed && split == (uint32_t)kWaves && acc == TG && blocks > cus && blocks <= 2 * cus) {
+    uint32_t pos = blocks - cus;  // the first workgroup that runs alone
+    for (int heavy = 1; heavy >= 0; heavy--)
+      for (int s = 0; s < a.nseg; s++)
+        if ((L.seg[s].type == T_Q6K) == (heavy == 1)) {
+          a.rot[s] = pos % TG;
+          pos += a.ntiles[s];
+        }
+  }
   const uint32_t ta = L.seg[0].type;
   uint32_t tb = ta;
   for (int s = 1; s < a.nseg; s++)
