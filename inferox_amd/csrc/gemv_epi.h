@@ -151,8 +151,6 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st);
 
 bool mfma_type(uint32_t t);  // Q4_K and Q6_K: tiled device layout, MFMA GEMV
 
-// h += W x with K split over workgroups (kern_gemv_mfma.hip); returns
-// hipErrorNotSupported for launches it does not take
-hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st);
+
 
 }  // namespace ifx

@@ -59,6 +59,8 @@ struct ifx_session {
   uint32_t kv_es = 4;                    // 4: f32 (IFX_KV_F32), 2: binary16 (IFX_KV_F16)
   float *hidden = nullptr, *q = nullptr, *attn = nullptr, *mid = nullptr, *logits = nullptr;
   float* partial = nullptr;
+  int qkv_ks = -1;  // K-split q/k/v in every layer: 1 / 0, -1 not yet decided (qkv_split)
+  float* qkv_q = nullptr;  // K-split q/k/v: each layer's q ([n_layers][hidden])
   float2* rope_cs = nullptr;
   DevState* state = nullptr;
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
@@ -201,6 +203,93 @@ GemmW gw(const ifx_tensor* t) {
 constexpr int kClasses = 8;
 bool per_layer_class(int k) { return k >= 1 && k <= 5; }
 
+// q/k/v + RoPE + KV append of a layer (rms-normed hidden in)
+GemvLaunch qkv_launch(const ifx_session* s, const LayerDev& L) {
+  GemvLaunch g;
+  g.seg[0] = seg_of(L.q);
+  g.seg[1] = seg_of(L.k);
+  g.seg[2] = seg_of(L.v);
+  g.nseg = 3;
+  g.cols = (uint32_t)s->m->cfg.hidden_size;
+  g.x = s->hidden;
+  g.norm_w = L.attn_norm;
+  g.eps = s->m->cfg.norm_eps;
+  return g;
+}
+
+// ffn_down + residual of a layer (mid in)
+GemvLaunch down_launch(const ifx_session* s, const LayerDev& L) {
+  GemvLaunch gd;
+  gd.seg[0] = seg_of(L.down);
+  gd.nseg = 1;
+  gd.cols = (uint32_t)s->m->cfg.intermediate_size;
+  gd.x = s->mid;
+  return gd;
+}
+
+// attn_output + residual of a layer (attention output in)
+GemvLaunch o_launch(const ifx_session* s, const LayerDev& L) {
+  GemvLaunch go;
+  go.seg[0] = seg_of(L.o);
+  go.nseg = 1;
+  go.cols = (uint32_t)s->m->cfg.hidden_size;
+  go.x = s->attn;
+  return go;
+}
+
+float* layer_cache(const ifx_session* s, uint8_t* base, size_t l) {
+  const uint64_t kvd = s->m->cfg.n_kv_heads * s->m->cfg.head_dim;
+  return (float*)(base + l * s->max_seq * kvd * s->kv_es);
+}
+
+// layer l's q under the K-split q/k/v launch
+float* layer_q(const ifx_session* s, size_t l) { return s->qkv_q + l * s->m->cfg.hidden_size; }
+
+// the K-split q/k/v launch's targets for layer l
+QkvDst qkv_dst(const ifx_session* s, size_t l) {
+  const ifx_config& c = s->m->cfg;
+  return QkvDst{layer_q(s, l), layer_cache(s, s->kc, l), layer_cache(s, s->vc, l), s->rope_cs, s->state,
+                (uint32_t)c.head_dim, (uint32_t)c.rope_dim, (uint32_t)s->max_seq};
+}
+
+// the rows every layer's K-split q/k/v launch adds into (its q, and cache row
+// len of its K and V), cleared by the step's embedding gather
+QkvClear qkv_clear_rows(const ifx_session* s) {
+  const ifx_config& c = s->m->cfg;
+  QkvClear r;
+  r.q = s->qkv_q;
+  r.k_cache = layer_cache(s, s->kc, 0);
+  r.v_cache = layer_cache(s, s->vc, 0);
+  r.state = s->state;
+  r.nq = (uint32_t)(c.n_heads * c.head_dim);
+  r.n_kv = (uint32_t)c.n_kv_heads;
+  r.head_dim = (uint32_t)c.head_dim;
+  r.max_seq = (uint32_t)s->max_seq;
+  r.n_layers = (uint32_t)s->m->layers.size();
+  r.q_stride = c.hidden_size;
+  r.kv_stride = (uint64_t)s->max_seq * c.n_kv_heads * c.head_dim;
+  return r;
+}
+
+// q/k/v as one K-split launch in every layer (kern_gemv_mfma.hip) where each
+// layer's launch applies and the cache is f32 (the atomic adds accumulate in
+// the cache's own type).  Each layer adds into its own q buffer and its cache
+// rows, all cleared at once by the step's embedding gather: a clear in each
+// layer's O or down launch cost it 0.3-0.6 us.  The tiled
+// launch with the q/k/v epilogue otherwise.  IFX_QKV_KS=0 keeps the tiled
+// launch.  Decided once per session.
+bool qkv_split(ifx_session* s) {
+  if (s->qkv_ks >= 0) return s->qkv_ks == 1;
+  const char* f = getenv("IFX_QKV_KS");
+  bool ok = !(f && f[0] == '0' && f[1] == 0) && s->kv_es == 4 && !s->m->layers.empty();
+  for (size_t l = 0; ok && l < s->m->layers.size(); l++) {
+    const LayerDev& L = s->m->layers[l];
+    ok = qkv_ks_supported(qkv_launch(s, L), qkv_dst(s, l));
+  }
+  s->qkv_ks = ok ? 1 : 0;
+  return ok;
+}
+
 // Launches the kernel(s) of class k (for layer l where it applies).  Every
 // kernel reads positions from s->state.
 int enqueue_class(ifx_session* s, int k, size_t l) {
@@ -211,7 +300,8 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
   const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim);
   switch (k) {
     case 0:
-      IFX_HIP(launch_embed_state(devw(m->embd), s->state, s->hidden, st));
+      IFX_HIP(launch_embed_state(devw(m->embd), s->state, s->hidden, st,
+                                 qkv_split(s) ? qkv_clear_rows(s) : QkvClear{}));
       return IFX_OK;
     case 6: {
       GemvLaunch gh;
@@ -237,15 +327,11 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
   const uint32_t kv16 = s->kv_es == 2;
   switch (k) {
     case 1: {
-      GemvLaunch g;
-      g.seg[0] = seg_of(L.q);
-      g.seg[1] = seg_of(L.k);
-      g.seg[2] = seg_of(L.v);
-      g.nseg = 3;
-      g.cols = D;
-      g.x = s->hidden;
-      g.norm_w = L.attn_norm;
-      g.eps = c.norm_eps;
+      const GemvLaunch g = qkv_launch(s, L);
+      if (qkv_split(s)) {
+        IFX_HIP(launch_qkv_ks(g, qkv_dst(s, l), st));
+        return IFX_OK;
+      }
       QkvEpi e{s->q, kc, vc, s->rope_cs, s->state, (uint32_t)c.head_dim, (uint32_t)c.rope_dim, kvd,
                (uint32_t)s->max_seq, kv16};
       IFX_HIP(gemv_qkv(g, e, st));
@@ -253,14 +339,11 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
     }
     case 2:
     case 3: {
-      AttnArgs a{s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
+      // q as the layer's q/k/v launch left it
+      AttnArgs a{qkv_split(s) ? layer_q(s, l) : s->q, kc, vc, s->attn, s->partial, s->state, (uint32_t)c.n_heads,
                  (uint32_t)c.n_kv_heads, (uint32_t)c.head_dim, s->max_chunks, s->attn_chunk,
                  (uint32_t)s->max_seq, kv16};
-      GemvLaunch go;
-      go.seg[0] = seg_of(L.o);
-      go.nseg = 1;
-      go.cols = D;
-      go.x = s->attn;
+      const GemvLaunch go = o_launch(s, L);
       // the merge of the chunk records moves into the O launch's prologue
       const bool fused = s->merge_bound && merge_o_supported(go, a);
       if (k == 2) IFX_HIP(fused ? launch_attn_partials(a, st) : launch_attn_decode(a, st));
@@ -280,15 +363,9 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       IFX_HIP(gemv_swiglu(gf, s->mid, st));
       return IFX_OK;
     }
-    case 5: {
-      GemvLaunch gd;
-      gd.seg[0] = seg_of(L.down);
-      gd.nseg = 1;
-      gd.cols = F;
-      gd.x = s->mid;
-      IFX_HIP(gemv_residual(gd, s->hidden, st));
+    case 5:
+      IFX_HIP(gemv_residual(down_launch(s, L), s->hidden, st));
       return IFX_OK;
-    }
     default:
       return set_error(IFX_E_INVALID_ARG, "kernel class %d", k);
   }
@@ -692,6 +769,7 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
   A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
   A((void**)&s->probs, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
   A((void**)&s->partial, (uint64_t)c.n_kv_heads * s->max_chunks * attn_partial_floats(G, c.head_dim) * 4);
+  A((void**)&s->qkv_q, (uint64_t)std::max<size_t>(m->layers.size(), 1) * D * 4);
   A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
   A((void**)&s->state, sizeof(DevState));
   A((void**)&s->out_tokens, max_seq_len * 4);

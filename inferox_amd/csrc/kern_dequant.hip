@@ -1,5 +1,7 @@
 // kern_dequant.hip — bit-exact dequantization kernels and the embedding gather.
 // Compiled with -ffp-contract=off (see inferox_amd/build.py).
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace ifx {
@@ -31,9 +33,12 @@ __global__ void __launch_bounds__(256) k_embed_rows(DevW w, const uint32_t* __re
 }
 
 // hidden = row cur_token (Model::decode_step, src/model/forward.rs:556-558).
+// It also clears the rows of the step's first K-split q/k/v launch (clr).
 __global__ void __launch_bounds__(256) k_embed_state(DevW w, const DevState* __restrict__ s,
-                                                     float* __restrict__ hidden) {
+                                                     float* __restrict__ hidden, QkvClear clr) {
   uint64_t row = s->cur_token;
+  const uint32_t len = s->len;
+  qkv_clear(clr, len, blockIdx.x, gridDim.x, threadIdx.x, blockDim.x);
   for (uint64_t c = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; c < w.cols;
        c += (uint64_t)gridDim.x * blockDim.x)
     hidden[c] = dev_elem(w, row * w.cols + c);
@@ -63,10 +68,10 @@ hipError_t launch_embed_rows(const DevW& w, const uint32_t* ids, uint64_t n_ids,
   return hipGetLastError();
 }
 
-hipError_t launch_embed_state(const DevW& w, const DevState* state, float* hidden,
-                              hipStream_t st) {
-  unsigned gx = (unsigned)((w.cols + 255) / 256);
-  hipLaunchKernelGGL(k_embed_state, dim3(gx), dim3(256), 0, st, w, state, hidden);
+hipError_t launch_embed_state(const DevW& w, const DevState* state, float* hidden, hipStream_t st,
+                              const QkvClear& clr) {
+  const unsigned gx = (unsigned)std::max<uint64_t>((w.cols + 255) / 256, (clr.floats() + 1023) / 1024);
+  hipLaunchKernelGGL(k_embed_state, dim3(gx), dim3(256), 0, st, w, state, hidden, clr);
   return hipGetLastError();
 }
 

@@ -600,6 +600,8 @@ struct KsArgs {
 // The wave's units: tiles t0, t0 + tstride, ... x the slice's nbs blocks.
 struct KsWave {
   uint32_t t0, tstride, b0, W;
+  __device__ __forceinline__ KsWave(uint32_t t0_, uint32_t tstride_, uint32_t b0_, uint32_t ntiles, uint32_t nbs)
+      : t0(t0_), tstride(tstride_), b0(b0_), W(t0_ < ntiles ? ((ntiles - 1 - t0_) / tstride_ + 1) * nbs : 0u) {}
   __device__ __forceinline__ KsWave(const KsArgs& a, uint32_t wave) {
     b0 = (blockIdx.x % kKs) * a.nbs;
     t0 = (blockIdx.x / kKs) * kWaves + wave;
@@ -608,38 +610,56 @@ struct KsWave {
   }
 };
 
+// Where a K-split wave's tiles live and where their row sums go.
+// One segment, the sums added into h (the O and down projections).
+template <int T>
+struct KsToH {
+  const KsArgs& a;
+  __device__ __forceinline__ const uint8_t* unit(uint32_t tile, uint32_t b) const {
+    return unit_ptr<T>(a.seg, a.nbr, tile, b);
+  }
+  __device__ __forceinline__ uint32_t q6(uint32_t) const { return a.seg.q6_signed; }
+  struct Pre {};
+  __device__ __forceinline__ Pre pre(uint32_t, int) const { return Pre{}; }
+  __device__ __forceinline__ void emit(uint32_t tile, float r, int lane, Pre) const {
+    const uint32_t row = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
+    if (lane < 16 && row < a.seg.rows) atomicAdd(a.h + row, r);
+  }
+};
+
 // Ring: slot i holds unit u = i (mod D); unit u is block b0 + u mod nbs of
 // tile t0 + (u / nbs) tstride.  Loads past the wave's last unit (and all of a
 // wave without tiles) read the slice's first unit (tile 0): in bounds, unused,
 // shared (an L2 hit), and unconditional, so that the compiler's waits count
 // one path.
-template <int T, int D>
-__device__ __forceinline__ void ks_prefetch(const KsArgs& a, const KsWave& w, KBuf<T> (&buf)[D], int lane) {
+template <int T, int D, class M>
+__device__ __forceinline__ void ks_prefetch(uint32_t nbs, const KsWave& w, const M& m, KBuf<T> (&buf)[D],
+                                            int lane) {
 #pragma unroll
   for (int i = 0; i < D; i++) {
     const bool past = (uint32_t)i >= w.W;
-    const uint32_t u = past ? 0u : (uint32_t)i, tl = past ? 0u : w.t0 + (u / a.nbs) * w.tstride;
-    buf[i].load(unit_ptr<T>(a.seg, a.nbr, tl, w.b0 + u % a.nbs), (uint32_t)lane, a.seg.q6_signed);
+    const uint32_t u = past ? 0u : (uint32_t)i, tl = past ? 0u : w.t0 + (u / nbs) * w.tstride;
+    buf[i].load(m.unit(tl, w.b0 + u % nbs), (uint32_t)lane, m.q6(tl));
     __builtin_amdgcn_sched_barrier(0);  // slots in ring order
   }
 }
 
-// The wave's units against the slice of x staged in LDS; each finished tile's
-// 16 row sums are added into h.
-template <int T, int D>
-__device__ __forceinline__ void ks_run(const KsArgs& a, const KsWave& w, KBuf<T> (&buf)[D], const uint8_t* lds,
-                                       int lane) {
+// The wave's units against the slice of x staged in LDS (digit planes at 0,
+// group sums at xs_off); each finished tile's 16 row sums go to m.emit.
+template <int T, int D, class M>
+__device__ __forceinline__ void ks_run(uint32_t nbs, uint32_t xs_off, uint32_t zero_off, const KsWave& w, const M& m,
+                                       KBuf<T> (&buf)[D], const uint8_t* lds, int lane) {
   if (w.W == 0) return;
-  const uint32_t nbs = a.nbs;
   const int ai = lane & 15, ag = lane >> 4;
   const bool active = (ai >> 2) == ag && (ai & 3) < 3;
-  const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : a.zero_off;
+  const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : zero_off;
   const uint32_t a_step = active ? kBlockA : 0u;
-  const float4* xs4 = (const float4*)(lds + a.xs_off) + ag;
+  const float4* xs4 = (const float4*)(lds + xs_off) + ag;
   const uint32_t Wp = (w.W + D - 1) / D * D;
   float acc = 0.f;
   uint32_t bl = 0, tile = w.t0;                                            // unit u: local block, tile
   uint32_t rb = (uint32_t)D % nbs, rt = w.t0 + ((uint32_t)D / nbs) * w.tstride;  // unit u + D
+  typename M::Pre pre = m.pre(tile, lane);  // the epilogue's reads, in flight during the tile
   for (uint32_t u0 = 0; u0 < Wp; u0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
@@ -654,8 +674,7 @@ __device__ __forceinline__ void ks_run(const KsArgs& a, const KsWave& w, KBuf<T>
       // refill shares (an L2 hit; the wave's own first unit is gone from L2
       // under the stream)
       const bool past = u + D >= w.W;
-      buf[i].load(unit_ptr<T>(a.seg, a.nbr, past ? 0u : rt, w.b0 + (past ? 0u : rb)), (uint32_t)lane,
-                  a.seg.q6_signed);
+      buf[i].load(m.unit(past ? 0u : rt, w.b0 + (past ? 0u : rb)), (uint32_t)lane, m.q6(past ? 0u : rt));
       // keep the ring order (see run_seg)
       __builtin_amdgcn_sched_barrier(0);
       if (++rb == nbs) {
@@ -667,12 +686,12 @@ __device__ __forceinline__ void ks_run(const KsArgs& a, const KsWave& w, KBuf<T>
           float r = acc;
           r += __shfl_xor(r, 16, 64);
           r += __shfl_xor(r, 32, 64);
-          const uint32_t row = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
-          if (lane < 16 && row < a.seg.rows) atomicAdd(a.h + row, r);
+          m.emit(tile, r, lane, pre);
         }
         acc = 0.f;
         bl = 0;
         tile += w.tstride;
+        pre = m.pre(tile, lane);
       }
     }
   }
@@ -700,14 +719,163 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
   const float4 xv0 = x4[0], xv1 = x4[1];
   loads_first();
   KBuf<T> buf[D];
-  ks_prefetch<T, D>(a, w, buf, lane);
+  const KsToH<T> m{a};
+  ks_prefetch<T, D>(a.nbs, w, m, buf, lane);
   {  // whole 32-element groups are in or out of the slice (nch % 32 == 0)
     float v[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
     quantize_chunk(v, c, c < nch, lds, (float4*)(lds + a.xs_off));
   }
   ks_zero(a, lds, tid);
   __syncthreads();
-  ks_run<T, D>(a, w, buf, lds, lane);
+  ks_run<T, D>(a.nbs, a.xs_off, a.zero_off, w, m, buf, lds, lane);
+}
+
+// ---------------------------------------------------------------------------
+// K-split q/k/v: the three projections of rms_norm(h) in one K-split launch
+// (what k_gemv_mfma<EpiQkv> computes with whole rows per workgroup).  The
+// tiled launch takes 384 workgroups for the 8B shape (384 tiles), two on half
+// of the CUs, and those CUs take twice the units: per-wave timestamps showed
+// the second workgroups ending at 8.3-9.2 us against 5.9-6.5 us.  Here every
+// CU takes the same share.  Each workgroup stages its slice of x * w (w: the
+// norm weight; the norm's scale, one scalar, is applied to the row sums as in
+// the tiled launch), reading all of h for the sum of squares.
+// RoPE rotates each (even, odd) pair of a q or k row, a linear map, so each
+// slice rotates its own partial sums (the pair's partner row sits in the
+// neighbouring lane) and adds them, as the O and down launches add into h,
+// straight into q and into the f32 cache's new row (cache row state->len):
+// the attention reads both as the tiled launch leaves them.  Those rows are
+// cleared beforehand (QkvClear: the layer before's O launch, or the step's
+// embedding gather for layer 0).
+// The waves of a slice are shared out over q, k and v in proportion to their
+// tiles, and each wave runs tiles of one segment (one buffer type, and its
+// segment's fields at fixed kernel-argument offsets: a segment looked up per
+// unit went through scratch).  Wave slot (wave, workgroup r of the slice) =
+// wave * R + r spreads the waves with two tiles and those with one over the
+// workgroups.
+// ---------------------------------------------------------------------------
+struct KsQkvArgs {
+  GemvSeg seg[3];      // q, k, v
+  uint32_t ntiles[3];
+  uint32_t nbr, nbs, cols;
+  uint32_t wq, wk;     // waves per slice on q and on k tiles (v takes the rest)
+  const float* x;      // h
+  const float* norm_w;
+  float eps;
+  QkvDst dst;          // where q, k and v go
+  uint32_t xs_off, zero_off;
+};
+
+// One segment's tiles (KIND 0: q, 1: k, 2: v); each row sum, times the norm
+// scale, with RoPE for q and k (src/ops.rs:281-296, as EpiQkv applies it), is
+// added into q or into its cache row.
+template <int T, int KIND>
+struct KsToQkv {
+  const GemvSeg& seg;
+  const QkvDst& d;
+  float scale;
+  uint32_t len, pos;  // cache row of the new key/value, RoPE position
+  __device__ __forceinline__ const uint8_t* unit(uint32_t tile, uint32_t b) const {
+    return unit_ptr<T>(seg, 0u, tile, b);
+  }
+  __device__ __forceinline__ uint32_t q6(uint32_t) const { return seg.q6_signed; }
+  struct Pre {
+    float2 cs;
+  };
+  // the (cos, sin) of the row's RoPE pair (clamped rows past the segment's end
+  // read an in-bounds pair and are not stored)
+  __device__ __forceinline__ Pre pre(uint32_t tile, int lane) const {
+    Pre p{make_float2(1.f, 0.f)};
+    if (KIND < 2 && d.rope_dim) {
+      const uint32_t row = min(tile * (uint32_t)kTileRows + (uint32_t)(lane & 15), seg.rows - 1);
+      const uint32_t i = min(row % d.head_dim, d.rope_dim - 1);
+      p.cs = d.rope_cs[(uint64_t)pos * (d.rope_dim / 2) + i / 2];
+    }
+    return p;
+  }
+  __device__ __forceinline__ void emit(uint32_t tile, float r, int lane, const Pre& p) const {
+    const uint32_t row = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
+    float v = r * scale;
+    if (KIND < 2) {
+      const float other = __shfl_xor(v, 1, 64);
+      const uint32_t i = row % d.head_dim;
+      if (i < d.rope_dim) v = (i & 1) ? (other * p.cs.y + v * p.cs.x) : (v * p.cs.x - other * p.cs.y);
+    }
+    if (lane < 16 && row < seg.rows) {
+      if (KIND == 0) {
+        atomicAdd(d.q + row, v);
+      } else {
+        float* c = KIND == 1 ? d.k_cache : d.v_cache;
+        atomicAdd(c + ((uint64_t)(row / d.head_dim) * d.max_seq + len) * d.head_dim + row % d.head_dim, v);
+      }
+    }
+  }
+};
+
+// KX: chunks of 8 elements of h per thread for the sum of squares (1 up to
+// 4096 columns, 2 up to 8192).
+template <int TA, int TB, int D, int KX>
+__global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_qkv(KsQkvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ float red[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t sl = blockIdx.x % kKs, R = gridDim.x / kKs, slot = wave * R + blockIdx.x / kKs;
+  const uint32_t b0 = sl * a.nbs, ws = R * kWaves;
+  // the wave's segment (uniform) and its place among that segment's waves
+  const uint32_t sg = slot < a.wq ? 0u : slot < a.wq + a.wk ? 1u : 2u;
+  const uint32_t w0 = sg == 0 ? 0u : sg == 1 ? a.wq : a.wq + a.wk;
+  const uint32_t nw = sg == 0 ? a.wq : sg == 1 ? a.wk : ws - a.wq - a.wk;
+  const KsWave w(slot - w0, max(nw, 1u), b0, a.ntiles[sg], a.nbs);
+  // all of h (the sum of squares), then the slice's chunk tid of h and of w
+  const uint32_t nchx = a.cols / 8, nch = a.nbs * 32;
+  const float4* x4 = (const float4*)a.x;
+  const float4* w4 = (const float4*)a.norm_w;
+  float4 hv[KX][2];
+#pragma unroll
+  for (int i = 0; i < KX; i++) {
+    const uint32_t c = min((uint32_t)tid + kThreads * i, nchx - 1);  // clamped: unconditional
+    hv[i][0] = x4[2 * c];
+    hv[i][1] = x4[2 * c + 1];
+  }
+  const uint32_t cs = b0 * 32 + min((uint32_t)tid, nch - 1);
+  const float4 xv0 = x4[2 * cs], xv1 = x4[2 * cs + 1], wv0 = w4[2 * cs], wv1 = w4[2 * cs + 1];
+  loads_first();
+  KBuf<TA> bufa[D];
+  KBuf<TB> bufb[D];
+  const uint32_t len = a.dst.state->len, pos = a.dst.state->rope_pos;
+  if (sg == 0) ks_prefetch<TA, D>(a.nbs, w, KsToQkv<TA, 0>{a.seg[0], a.dst, 0.f, len, pos}, bufa, lane);
+  else if (sg == 1) ks_prefetch<TA, D>(a.nbs, w, KsToQkv<TA, 1>{a.seg[1], a.dst, 0.f, len, pos}, bufa, lane);
+  else ks_prefetch<TB, D>(a.nbs, w, KsToQkv<TB, 2>{a.seg[2], a.dst, 0.f, len, pos}, bufb, lane);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < KX; i++) {
+    if ((uint32_t)tid + kThreads * i < nchx) {
+#pragma unroll
+      for (int hlf = 0; hlf < 2; hlf++) {
+        const float4 u = hv[i][hlf];
+        ss = fmaf(u.x, u.x, ss); ss = fmaf(u.y, u.y, ss); ss = fmaf(u.z, u.z, ss); ss = fmaf(u.w, u.w, ss);
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  {  // whole 32-element groups are in or out of the slice (nch % 32 == 0)
+    float v[8] = {xv0.x * wv0.x, xv0.y * wv0.y, xv0.z * wv0.z, xv0.w * wv0.w,
+                  xv1.x * wv1.x, xv1.y * wv1.y, xv1.z * wv1.z, xv1.w * wv1.w};
+    quantize_chunk(v, (uint32_t)tid, (uint32_t)tid < nch, lds, (float4*)(lds + a.xs_off));
+  }
+  if (tid < (int)(kZeroBytes / 16)) *(uint4*)(lds + a.zero_off + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int q = 0; q < kWaves; q++) tot += red[q];
+  const float nscale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+  if (sg == 0)
+    ks_run<TA, D>(a.nbs, a.xs_off, a.zero_off, w, KsToQkv<TA, 0>{a.seg[0], a.dst, nscale, len, pos}, bufa, lds, lane);
+  else if (sg == 1)
+    ks_run<TA, D>(a.nbs, a.xs_off, a.zero_off, w, KsToQkv<TA, 1>{a.seg[1], a.dst, nscale, len, pos}, bufa, lds, lane);
+  else
+    ks_run<TB, D>(a.nbs, a.xs_off, a.zero_off, w, KsToQkv<TB, 2>{a.seg[2], a.dst, nscale, len, pos}, bufb, lds, lane);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -777,7 +945,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   }
   loads_first();
   KBuf<T> buf[D];
-  ks_prefetch<T, D>(a, w, buf, lane);
+  const KsToH<T> m{a};
+  ks_prefetch<T, D>(a.nbs, w, m, buf, lane);
 
   if (wave < (uint32_t)G) {
     float M = (uint32_t)lane < nch ? m0 : -INFINITY;
@@ -824,7 +993,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   }
   ks_zero(a, lds, tid);
   __syncthreads();
-  ks_run<T, D>(a, w, buf, lds, lane);
+  ks_run<T, D>(a.nbs, a.xs_off, a.zero_off, w, m, buf, lds, lane);
 }
 
 int cu_count() {
@@ -996,6 +1165,73 @@ hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st
   if (L.seg[0].type == T_Q6K) hipLaunchKernelGGL((k_gemv_ks<T_Q6K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
   else hipLaunchKernelGGL((k_gemv_ks<T_Q4K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
   return hipGetLastError();
+}
+
+// The K-split q/k/v launch where it applies: three Q4_K / Q6_K segments with
+// the norm, q and k of one type, K in whole slices of at most 16 blocks and
+// at most 8192 columns.
+namespace {
+bool qkv_ks_plan(const GemvLaunch& L, const QkvDst& d, KsQkvArgs& a, uint32_t& blocks, size_t& lds) {
+  // whole heads per segment, RoPE pairs inside a head
+  if (d.head_dim == 0 || d.head_dim % 2 || d.rope_dim > d.head_dim || d.rope_dim % 2 || d.max_seq == 0) return false;
+  if (L.nseg != 3 || !L.norm_w || L.paired || L.cols == 0 || L.cols % 256 || L.cols > 2 * 8 * kThreads) return false;
+  for (int s = 0; s < 3; s++)
+    if (!mfma_type(L.seg[s].type) || L.seg[s].rows == 0) return false;
+  if (L.seg[0].type != L.seg[1].type) return false;
+  const uint32_t nbr = L.cols / 256;
+  blocks = (uint32_t)cu_count();
+  if (nbr % kKs || nbr / kKs > kKsMaxBlocks || blocks % kKs) return false;
+  a = KsQkvArgs{};
+  for (int s = 0; s < 3; s++) {
+    if (L.seg[s].rows % d.head_dim) return false;
+    a.seg[s] = L.seg[s];
+    a.ntiles[s] = (uint32_t)((L.seg[s].rows + kTileRows - 1) / kTileRows);
+  }
+  a.nbr = nbr;
+  a.nbs = nbr / kKs;
+  a.cols = L.cols;
+  a.x = L.x;
+  a.norm_w = L.norm_w;
+  a.eps = L.eps;
+  a.dst = d;
+  // waves per slice for each segment, in proportion to its tiles (at least one each)
+  const uint32_t ws = blocks / kKs * kWaves, nt = a.ntiles[0] + a.ntiles[1] + a.ntiles[2];
+  if (ws < 3) return false;
+  auto share = [&](uint32_t n) { return std::max(1u, (uint32_t)(((uint64_t)ws * n + nt / 2) / nt)); };
+  a.wk = std::min(share(a.ntiles[1]), ws - 2);
+  const uint32_t wv = std::min(share(a.ntiles[2]), ws - a.wk - 1);
+  a.wq = ws - a.wk - wv;
+  a.xs_off = 768u * a.nbs;               // digit planes: 48 bytes per 16 elements
+  a.zero_off = a.xs_off + 128u * a.nbs;  // group sums: 16 bytes per 32 elements
+  lds = a.zero_off + kZeroBytes;
+  return true;
+}
+
+template <int TA, int TB>
+hipError_t go_qkv(const KsQkvArgs& a, uint32_t blocks, size_t lds, hipStream_t st) {
+  if (a.cols <= 8u * kThreads)
+    hipLaunchKernelGGL((k_gemv_ks_qkv<TA, TB, kKsRing, 1>), dim3(blocks), dim3(kThreads), lds, st, a);
+  else
+    hipLaunchKernelGGL((k_gemv_ks_qkv<TA, TB, kKsRing, 2>), dim3(blocks), dim3(kThreads), lds, st, a);
+  return hipGetLastError();
+}
+}  // namespace
+
+bool qkv_ks_supported(const GemvLaunch& L, const QkvDst& d) {
+  KsQkvArgs a;
+  uint32_t blocks;
+  size_t lds;
+  return qkv_ks_plan(L, d, a, blocks, lds);
+}
+
+hipError_t launch_qkv_ks(const GemvLaunch& L, const QkvDst& d, hipStream_t st) {
+  KsQkvArgs a;
+  uint32_t blocks;
+  size_t lds;
+  if (!d.q || !d.k_cache || !d.v_cache || !d.state || !qkv_ks_plan(L, d, a, blocks, lds)) return hipErrorInvalidValue;
+  const uint32_t ta = a.seg[0].type, tb = a.seg[2].type;
+  if (ta == T_Q4K) return tb == T_Q4K ? go_qkv<T_Q4K, T_Q4K>(a, blocks, lds, st) : go_qkv<T_Q4K, T_Q6K>(a, blocks, lds, st);
+  return tb == T_Q6K ? go_qkv<T_Q6K, T_Q6K>(a, blocks, lds, st) : go_qkv<T_Q6K, T_Q4K>(a, blocks, lds, st);
 }
 
 uint32_t merge_o_first_chunks() { return kMergeFirst; }

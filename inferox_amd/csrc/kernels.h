@@ -35,6 +35,58 @@ struct DevState {
   unsigned long long seed;
 };
 
+// Where the K-split q/k/v launch adds its rows (launch_qkv_ks): q, and row
+// state->len of the layer's f32 K and V caches ([n_kv][max_seq][head_dim]),
+// all cleared beforehand (QkvClear); RoPE at state->rope_pos from rope_cs.
+struct QkvDst {
+  float* q;
+  float* k_cache;
+  float* v_cache;
+  const float2* rope_cs;
+  const DevState* state;
+  uint32_t head_dim, rope_dim, max_seq;
+};
+// Rows a launch clears for K-split q/k/v launches, for each of n_layers
+// layers: q[0, nq) (layer l's at q + l q_stride) and, for each of n_kv kv
+// heads, row state->len (head_dim floats) of the K and V caches (layer l's at
+// k_cache / v_cache + l kv_stride).  A null q clears nothing.
+struct QkvClear {
+  float* q = nullptr;
+  float* k_cache = nullptr;
+  float* v_cache = nullptr;
+  const DevState* state = nullptr;
+  uint32_t nq = 0, n_kv = 0, head_dim = 0, max_seq = 0;
+  uint32_t n_layers = 1;
+  uint64_t q_stride = 0, kv_stride = 0;  // floats
+  __host__ __device__ uint64_t floats() const { return q ? (uint64_t)n_layers * (nq + 2ull * n_kv * head_dim) : 0; }
+};
+// workgroup wg of nwg clears its share, with threads tid of nthreads; len is
+// c.state->len, read by the caller early (a read here would put its round trip
+// where the clear is placed)
+__device__ inline void qkv_clear(const QkvClear& c, uint32_t len, uint32_t wg, uint32_t nwg, uint32_t tid,
+                                 uint32_t nthreads) {
+  if (!c.q) return;
+  const uint32_t nkv = c.n_kv * c.head_dim, layer_n = c.nq + 2 * nkv, total = (uint32_t)c.floats();
+  const uint32_t per = (total + nwg - 1) / nwg, base = wg * per;
+  for (uint32_t i = tid; i < per; i += nthreads) {
+    const uint32_t e0 = base + i;
+    if (e0 >= total) break;
+    const uint32_t layer = e0 / layer_n, e = e0 % layer_n;
+    // agent-scope stores, as the atomic adds that follow: they leave no dirty
+    // line in this XCD's L2 (plain stores cost the launch ~0.5 us, the L2
+    // write-back at its end)
+    float* p;
+    if (e < c.nq) {
+      p = c.q + layer * c.q_stride + e;
+    } else {
+      const uint32_t f = e - c.nq, r = f % nkv;
+      float* cache = (f >= nkv ? c.v_cache : c.k_cache) + layer * c.kv_stride;
+      p = cache + ((uint64_t)(r / c.head_dim) * c.max_seq + len) * c.head_dim + r % c.head_dim;
+    }
+    __hip_atomic_store(p, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ---- dequantization (kern_dequant.hip) ----
 hipError_t launch_dequant_raw(uint32_t type, const uint8_t* bytes, uint64_t n, float* out,
                               hipStream_t st);
@@ -42,7 +94,10 @@ hipError_t launch_dequant_dev(const DevW& w, uint64_t n, float* out, hipStream_t
 hipError_t launch_embed_rows(const DevW& w, const uint32_t* ids, uint64_t n_ids, float* out,
                              hipStream_t st);
 // hidden[cols] = row state->cur_token of the table
-hipError_t launch_embed_state(const DevW& w, const DevState* state, float* hidden, hipStream_t st);
+// clr: rows cleared for the step's K-split q/k/v launches (extra workgroups
+// take them, 1024 floats each)
+hipError_t launch_embed_state(const DevW& w, const DevState* state, float* hidden, hipStream_t st,
+                              const QkvClear& clr = QkvClear{});
 
 // ---- fused GEMV (kern_gemv.hip) ----
 struct GemvSeg {
@@ -213,6 +268,14 @@ hipError_t launch_attn_partials(const AttnArgs& a, hipStream_t st);
 bool merge_o_supported(const GemvLaunch& L, const AttnArgs& a);
 hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& a, float* h, hipStream_t st,
                                       uint32_t first);
+// h += W x with K split over workgroups (kern_gemv_mfma.hip); returns
+// hipErrorNotSupported for launches it does not take
+hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st);
+// q/k/v of rms_norm(x) as one K-split launch (kern_gemv_mfma.hip): segments
+// q, k, v of L (Q4_K / Q6_K, q and k of one type, with the norm, whole heads),
+// added into d's targets.
+bool qkv_ks_supported(const GemvLaunch& L, const QkvDst& d);
+hipError_t launch_qkv_ks(const GemvLaunch& L, const QkvDst& d, hipStream_t st);
 uint32_t merge_o_first_chunks();
 uint32_t merge_o_bound_step();
 // head dims the decode attention takes: multiples of 4 (f32 cache) or 8 (f16) up to 256
