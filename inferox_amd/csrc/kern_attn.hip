@@ -103,6 +103,41 @@ __device__ __forceinline__ float quad_sum(float v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
   return v;
 }
+// Quad reduce-scatter: lane q of each quad holds partial sums v[0..N); on
+// return v[j] (j < N / 4) holds the quad's total of element q + 4j.  Round 1
+// (lane ^ 1) keeps the elements h with h % 2 == q % 2 and sends the others,
+// round 2 (lane ^ 2) likewise on h / 2.  Lane q adds (v_q + v_q^1) + (v_q^2 +
+// v_q^3) exactly as quad_sum does, so the totals are bit-identical to it.
+template <int N>
+__device__ __forceinline__ void quad_reduce_scatter(float (&v)[N], uint32_t q) {
+  static_assert(N % 4 == 0, "whole quads");
+  float t[N / 2];  // t[p]: element 2p + q % 2 over lanes q, q ^ 1
+  const bool b0 = q & 1, b1 = q & 2;
+#pragma unroll
+  for (int p = 0; p < N / 2; p++) {
+    const float keep = b0 ? v[2 * p + 1] : v[2 * p], send = b0 ? v[2 * p] : v[2 * p + 1];
+    t[p] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xb1, 0xf, 0xf, false));
+  }
+#pragma unroll
+  for (int j = 0; j < N / 4; j++) {
+    const float keep = b1 ? t[2 * j + 1] : t[2 * j], send = b1 ? t[2 * j] : t[2 * j + 1];
+    v[j] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x4e, 0xf, 0xf, false));
+  }
+}
+// max / sum over the 16 lanes of a wave that share lane % 4, in every lane:
+// row_ror:4 and row_ror:8 (0x124, 0x128) inside each 16-lane row, then the
+// gfx950 swaps of rows 0<->1, 2<->3 and of the two halves (each returns the
+// pair as {own, partner} in some order: the pair's max / sum either way).
+__device__ __forceinline__ float pair16(float a, float b, bool mx) { return mx ? fmaxf(a, b) : a + b; }
+template <bool MAX>
+__device__ __forceinline__ float class4_reduce(float v) {
+  v = pair16(v, dpp_f<0x124, 0xf, 0xf>(v, v), MAX);
+  v = pair16(v, dpp_f<0x128, 0xf, 0xf>(v, v), MAX);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = pair16(__uint_as_float(r16[0]), __uint_as_float(r16[1]), MAX);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return pair16(__uint_as_float(r32[0]), __uint_as_float(r32[1]), MAX);
+}
 
 constexpr int kRowsPerWave = kChunk / (kThreads / 64);  // 16
 
@@ -202,8 +237,6 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
   // (softmax_rows, src/ops.rs:223-239) ----
   const bool row_ok = kr_row < n;
   const float rs = sqrtf((float)HD);
-  float e_row[GM];  // exp(s - m_wave) of this lane's row, per query head
-  float m_w[GM], l_w[GM];
   // the query heads' dot products advance together: each LDS round trip for q
   // feeds GM independent FMA chains (one chain per head would wait for every read)
   float sg[GM];
@@ -232,27 +265,57 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
       }
     }
   }
+  // The row weights e go to LDS (es, read back as broadcasts by the whole
+  // wave in p . V: LDS keeps a wave's accesses in order), the wave's max and
+  // sum per head to wst for the combine.
+  if constexpr (GT > 0 && GT % 4 == 0) {
+    // Whole quads of heads: the quad's reduce-scatter leaves lane (row l / 4,
+    // q = l % 4) the row's scores of heads q + 4j, so each lane takes one
+    // division, exp and pair of class reductions per four heads.
+    quad_reduce_scatter(sg, (uint32_t)kq);
 #pragma unroll
-  for (int g = 0; g < GM; g++) {
-    e_row[g] = 0.f;
-    m_w[g] = -INFINITY;
-    l_w[g] = 0.f;
-    if (g < (int)G) {
-      const float sv = quad_sum(sg[g]) / rs;
-      m_w[g] = wave_max_dpp(row_ok ? sv : -INFINITY);
-      e_row[g] = row_ok ? expf(sv - m_w[g]) : 0.f;
-      l_w[g] = wave_sum_dpp(kq == 0 ? e_row[g] : 0.f);
+    for (int j = 0; j < GM / 4; j++) {
+      const uint32_t g = (uint32_t)kq + 4 * j;
+      const float sv = sg[j] / rs;
+      const float m = class4_reduce<true>(row_ok ? sv : -INFINITY);
+      const float e = row_ok ? expf(sv - m) : 0.f;
+      const float l = class4_reduce<false>(e);
+      es[wave][lane >> 2][g] = e;
+      if (lane < 4) {
+        wst[wave][0][g] = m;
+        wst[wave][1][g] = l;
+      }
+    }
+  } else {
+    float e_row[GM];  // exp(s - m_wave) of this lane's row, per query head
+    float m_w[GM], l_w[GM];
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+      e_row[g] = 0.f;
+      m_w[g] = -INFINITY;
+      l_w[g] = 0.f;
+      if (g < (int)G) {
+        const float sv = quad_sum(sg[g]) / rs;
+        m_w[g] = wave_max_dpp(row_ok ? sv : -INFINITY);
+        e_row[g] = row_ok ? expf(sv - m_w[g]) : 0.f;
+        l_w[g] = wave_sum_dpp(kq == 0 ? e_row[g] : 0.f);
+      }
+    }
+    if (kq == 0) {
+#pragma unroll
+      for (int g = 0; g < GM; g++)
+        if (g < (int)G) es[wave][lane >> 2][g] = e_row[g];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < GM; g++) {
+        wst[wave][0][g] = m_w[g];
+        wst[wave][1][g] = l_w[g];
+      }
     }
   }
 
   // ---- o = sum_t e_t v_t over the wave's rows (src/model/forward.rs:401-409) ----
-  // The row weights go through LDS (written by each row's first lane, read
-  // back as broadcasts by the whole wave; LDS keeps a wave's accesses in order).
-  if (kq == 0) {
-#pragma unroll
-    for (int g = 0; g < GM; g++)
-      if (g < (int)G) es[wave][lane >> 2][g] = e_row[g];
-  }
   float2 o[GM][VJ];
 #pragma unroll
   for (int g = 0; g < GM; g++)
@@ -279,13 +342,6 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
   }
 
   // ---- combine the four waves into the chunk's record ----
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < GM; g++) {
-      wst[wave][0][g] = m_w[g];
-      wst[wave][1][g] = l_w[g];
-    }
-  }
 #pragma unroll
   for (int g = 0; g < GM; g++)
 #pragma unroll
