@@ -158,10 +158,12 @@ __device__ __forceinline__ void attended_rows(const DevState* st, uint32_t& lo, 
 // Each wave owns 16 cache rows of the chunk end to end:
 //   scores  lane = (row l/4, quarter l%4): the quarter's 16-byte K chunks
 //           ch = l%4 + 4i, q from LDS, a quad reduction on the DPP network;
-//   softmax max / sum over the wave's rows on the DPP network;
+//   softmax the wave's max on the DPP network, the chunk's max M over the
+//           four waves through LDS, then exp(s - M) and the wave's sums;
 //   p . V   lane = columns 2l, 2l+1 (+128 j) of all 16 rows, the row weights
-//           broadcast with readlane: no cross-lane reduction.
-// The four waves are combined once through LDS into the chunk's record.
+//           broadcast from LDS: no cross-lane reduction.
+// The four waves' o and sums (all relative to M) add up through LDS into the
+// chunk's record.
 // At least 3 waves per SIMD: the 70B shape (group 8) otherwise takes 172
 // registers, 2 waves per SIMD, and its ~1040 workgroups at ctx 8192 run in 3
 // rounds instead of 2.
@@ -265,52 +267,58 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
       }
     }
   }
-  // The row weights e go to LDS (es, read back as broadcasts by the whole
-  // wave in p . V: LDS keeps a wave's accesses in order), the wave's max and
-  // sum per head to wst for the combine.
-  if constexpr (GT > 0 && GT % 4 == 0) {
+  // The softmax runs against the chunk's max M over all four waves (one
+  // barrier after the scores), so the waves' o and sums add up in the
+  // combine without rescaling.  The row weights e go to LDS (es, read back as
+  // broadcasts by the whole wave in p . V: LDS keeps a wave's accesses in
+  // order), the wave's max and sum per head to wst.
+  constexpr bool kSpread = GT > 0 && GT % 4 == 0;
+  float sv[GM];
+  if constexpr (kSpread) {
     // Whole quads of heads: the quad's reduce-scatter leaves lane (row l / 4,
     // q = l % 4) the row's scores of heads q + 4j, so each lane takes one
     // division, exp and pair of class reductions per four heads.
     quad_reduce_scatter(sg, (uint32_t)kq);
 #pragma unroll
     for (int j = 0; j < GM / 4; j++) {
-      const uint32_t g = (uint32_t)kq + 4 * j;
-      const float sv = sg[j] / rs;
-      const float m = class4_reduce<true>(row_ok ? sv : -INFINITY);
-      const float e = row_ok ? expf(sv - m) : 0.f;
-      const float l = class4_reduce<false>(e);
-      es[wave][lane >> 2][g] = e;
-      if (lane < 4) {
-        wst[wave][0][g] = m;
-        wst[wave][1][g] = l;
-      }
+      sv[j] = sg[j] / rs;
+      const float m = class4_reduce<true>(row_ok ? sv[j] : -INFINITY);
+      if (lane < 4) wst[wave][0][kq + 4 * j] = m;
     }
   } else {
-    float e_row[GM];  // exp(s - m_wave) of this lane's row, per query head
-    float m_w[GM], l_w[GM];
 #pragma unroll
     for (int g = 0; g < GM; g++) {
-      e_row[g] = 0.f;
-      m_w[g] = -INFINITY;
-      l_w[g] = 0.f;
       if (g < (int)G) {
-        const float sv = quad_sum(sg[g]) / rs;
-        m_w[g] = wave_max_dpp(row_ok ? sv : -INFINITY);
-        e_row[g] = row_ok ? expf(sv - m_w[g]) : 0.f;
-        l_w[g] = wave_sum_dpp(kq == 0 ? e_row[g] : 0.f);
+        sv[g] = quad_sum(sg[g]) / rs;
+        const float m = wave_max_dpp(row_ok ? sv[g] : -INFINITY);
+        if (lane == 0) wst[wave][0][g] = m;
       }
     }
-    if (kq == 0) {
+  }
+  __syncthreads();
+  auto chunk_max = [&](uint32_t g) {
+    float M = wst[0][0][g];
 #pragma unroll
-      for (int g = 0; g < GM; g++)
-        if (g < (int)G) es[wave][lane >> 2][g] = e_row[g];
+    for (int w = 1; w < kThreads / 64; w++) M = fmaxf(M, wst[w][0][g]);
+    return M;
+  };
+  if constexpr (kSpread) {
+#pragma unroll
+    for (int j = 0; j < GM / 4; j++) {
+      const uint32_t g = (uint32_t)kq + 4 * j;
+      const float e = row_ok ? expf(sv[j] - chunk_max(g)) : 0.f;
+      const float l = class4_reduce<false>(e);
+      es[wave][lane >> 2][g] = e;
+      if (lane < 4) wst[wave][1][g] = l;
     }
-    if (lane == 0) {
+  } else {
 #pragma unroll
-      for (int g = 0; g < GM; g++) {
-        wst[wave][0][g] = m_w[g];
-        wst[wave][1][g] = l_w[g];
+    for (int g = 0; g < GM; g++) {
+      if (g < (int)G) {
+        const float e = row_ok ? expf(sv[g] - chunk_max(g)) : 0.f;
+        const float l = wave_sum_dpp(kq == 0 ? e : 0.f);
+        if (kq == 0) es[wave][lane >> 2][g] = e;
+        if (lane == 0) wst[wave][1][g] = l;
       }
     }
   }
@@ -352,30 +360,20 @@ __global__ void __launch_bounds__(kThreads, GT == 8 ? 3 : 1) k_attn_decode(AttnA
   float* part = a.partial + ((uint64_t)hk * a.max_chunks + c) * rec;
   for (uint32_t item = tid; item < G * HD / 2; item += kThreads) {
     const uint32_t g = item / (HD / 2), cp = item % (HD / 2);
-    float M = -INFINITY;
+    float2 acc = wo[0][g][cp];
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; w++) M = fmaxf(M, wst[w][0][g]);
-    float2 acc = make_float2(0.f, 0.f);
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; w++) {
-      // waves whose rows are all past the chunk end have max -inf: weight 0
-      const float mw = wst[w][0][g];
-      const float sc = mw == -INFINITY ? 0.f : expf(mw - M);
-      acc.x = fmaf(sc, wo[w][g][cp].x, acc.x);
-      acc.y = fmaf(sc, wo[w][g][cp].y, acc.y);
+    for (int w = 1; w < kThreads / 64; w++) {
+      // waves whose rows are all past the chunk end hold zeros
+      acc.x += wo[w][g][cp].x;
+      acc.y += wo[w][g][cp].y;
     }
     *(float2*)(part + g * HD + 2 * cp) = acc;
   }
   if (tid < (int)G) {
-    float M = -INFINITY, L = 0.f;
+    float L = wst[0][1][tid];
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; w++) M = fmaxf(M, wst[w][0][tid]);
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; w++) {
-      const float mw = wst[w][0][tid];
-      L = fmaf(mw == -INFINITY ? 0.f : expf(mw - M), wst[w][1][tid], L);
-    }
-    part[G * HD + tid] = M;
+    for (int w = 1; w < kThreads / 64; w++) L += wst[w][1][tid];
+    part[G * HD + tid] = chunk_max((uint32_t)tid);
     part[G * HD + G + tid] = L;
   }
 
