@@ -907,10 +907,12 @@ template <int T, int D, int G>
 __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   constexpr int HD = 128, SD = G * HD, NC4 = SD / 4, NS = kThreads / NC4, KB = (int)kMergeFirst / NS;
   static_assert(kThreads % NC4 == 0 && SD / 8 <= kThreads, "slice shape");
+  static_assert(kMergeFirst <= 64, "the first loads' weights come from one lane each");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float4 red[kThreads];
   __shared__ __attribute__((aligned(16))) float xsl[SD];
   __shared__ float sm[G], sd[G];
+  __shared__ float wts[G][64];  // exp(m_c - M) of head g for chunks c < 64 (weights of the first loads)
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
   const KsWave w(a, wave);
@@ -936,12 +938,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
     l0 = ml[at + G + wave];
   }
   float4 ov[KB];
-  float mk[KB];
 #pragma unroll
   for (int k = 0; k < KB; k++) {
     const uint64_t at = (uint64_t)min(sp + (uint32_t)(NS * k), cl) * rec;  // clamped: unconditional
     ov[k] = ((const float4*)(base + at))[col];
-    mk[k] = ml[at + g];
   }
   loads_first();
   KBuf<T> buf[D];
@@ -952,7 +952,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
     float M = (uint32_t)lane < nch ? m0 : -INFINITY;
     for (uint32_t c = lane + 64; c < nch; c += 64) M = fmaxf(M, ml[(uint64_t)c * rec + wave]);
     M = wave_max(M);
-    float den = (uint32_t)lane < nch ? l0 * expf(m0 - M) : 0.f;
+    // each weight once, for every thread that sums chunk `lane` of head g
+    const float w0 = (uint32_t)lane < nch ? expf(m0 - M) : 0.f;
+    wts[wave][lane] = w0;
+    float den = (uint32_t)lane < nch ? l0 * w0 : 0.f;
     for (uint32_t c = lane + 64; c < nch; c += 64)
       den = fmaf(ml[(uint64_t)c * rec + G + wave], expf(ml[(uint64_t)c * rec + wave] - M), den);
     den = wave_sum(den);
@@ -967,7 +970,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   const uint32_t nb = min(nch, fe);
 #pragma unroll
   for (int k = 0; k < KB; k++)
-    if (sp + (uint32_t)(NS * k) < nb) acc = fma4(expf(mk[k] - M), ov[k], acc);
+    if (sp + (uint32_t)(NS * k) < nb) acc = fma4(wts[g][sp + NS * k], ov[k], acc);
   for (uint32_t c = sp + fe; c < nch; c += NS) {
     const uint64_t at = (uint64_t)c * rec;
     acc = fma4(expf(ml[at + g] - M), ((const float4*)(base + at))[col], acc);
