@@ -83,11 +83,52 @@ struct MArgs {
   uint32_t xs_off, zero_off;  // LDS byte offsets (the digit planes start at 0)
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+// ---- lane exchanges without LDS round trips (whole wave active) ----
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_mov<0xb1>(v); }  // quad_perm [1,0,3,2]
+__device__ __forceinline__ float lane_xor2(float v) { return dpp_mov<0x4e>(v); }  // quad_perm [2,3,0,1]
+// One butterfly step: v op (v of lane ^ OFF) in every lane.  OFF 32 / 16: the
+// gfx950 swaps of the two halves / of rows 0<->1, 2<->3 return {own, partner}
+// in some order (the pair's op either way); 8: row_ror:8; 4: row_half_mirror
+// then quad_perm [3,2,1,0]; 2, 1: quad_perm.  The operands are those of a
+// __shfl_xor butterfly, so sums come out bit for bit the same.
+template <int OFF, bool MAX>
+__device__ __forceinline__ float bfly(float v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane offset");
+  float a = v, b;
+  if constexpr (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else if constexpr (OFF == 8) {
+    b = dpp_mov<0x128>(v);
+  } else if constexpr (OFF == 4) {
+    b = dpp_mov<0x1b>(dpp_mov<0x141>(v));
+  } else if constexpr (OFF == 2) {
+    b = lane_xor2(v);
+  } else {
+    b = lane_xor1(v);
+  }
+  return MAX ? fmaxf(a, b) : a + b;
+}
+// sum / max over the 64 lanes, in every lane (the xor butterfly 32, 16, ..., 1)
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  v = bfly<32, MAX>(v);
+  v = bfly<16, MAX>(v);
+  v = bfly<8, MAX>(v);
+  v = bfly<4, MAX>(v);
+  v = bfly<2, MAX>(v);
+  return bfly<1, MAX>(v);
+}
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce<false>(v); }
 
 __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -221,8 +262,8 @@ __device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool 
   float m = 0.f;
 #pragma unroll
   for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  m = bfly<1, true>(m);
+  m = bfly<2, true>(m);
   int e;
   (void)frexpf(m, &e);  // m < 2^e
   e = e < -100 ? -100 : e;
@@ -238,8 +279,8 @@ __device__ __forceinline__ void quantize_chunk(const float* v, uint32_t c, bool 
     p2[w] |= (uint32_t)(X2 & 255) << sh;
   }
   const float s8 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-  const float s16 = s8 + __shfl_xor(s8, 1, 64);
-  const float s16o = __shfl_xor(s16, 2, 64);
+  const float s16 = bfly<1, false>(s8);
+  const float s16o = lane_xor2(s16);
   if (ok) {
     uint8_t* dst = lds + (c >> 1) * kPartBytes + 8 * (c & 1);
     *(uint2*)dst = make_uint2(p0[0], p0[1]);
@@ -359,7 +400,7 @@ __device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, con
   const float v = acc[0];
   float partner = 0.f;
   if (Epi::kPaired) partner = acc[NT - 1];
-  else if (Epi::kNeighbor) partner = __shfl_xor(v, 1, 64);
+  else if (Epi::kNeighbor) partner = lane_xor1(v);
   const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
   if (lane < 16 && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner, pre);
 }
@@ -427,8 +468,8 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      acc[t] += __shfl_xor(acc[t], 16, 64);
-      acc[t] += __shfl_xor(acc[t], 32, 64);
+      acc[t] = bfly<16, false>(acc[t]);
+      acc[t] = bfly<32, false>(acc[t]);
     }
     if (S > 1) {
       // partial sums of the group's waves through LDS (double-buffered: one barrier per item)
@@ -684,8 +725,8 @@ __device__ __forceinline__ void ks_run(uint32_t nbs, uint32_t xs_off, uint32_t z
       if (++bl == nbs) {  // the tile's slice is done (uniform over the wave)
         if (u < w.W) {
           float r = acc;
-          r += __shfl_xor(r, 16, 64);
-          r += __shfl_xor(r, 32, 64);
+          r = bfly<16, false>(r);
+          r = bfly<32, false>(r);
           m.emit(tile, r, lane, pre);
         }
         acc = 0.f;
@@ -796,7 +837,7 @@ struct KsToQkv {
     const uint32_t row = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
     float v = r * scale;
     if (KIND < 2) {
-      const float other = __shfl_xor(v, 1, 64);
+      const float other = lane_xor1(v);
       const uint32_t i = row % d.head_dim;
       if (i < d.rope_dim) v = (i & 1) ? (other * p.cs.y + v * p.cs.x) : (v * p.cs.x - other * p.cs.y);
     }
@@ -878,11 +919,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_qkv(KsQkvArgs a) {
     ks_run<TB, D>(a.nbs, a.xs_off, a.zero_off, w, KsToQkv<TB, 2>{a.seg[2], a.dst, nscale, len, pos}, bufb, lds, lane);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave_reduce<true>(v); }
 __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
   acc.x = fmaf(w, v.x, acc.x);
   acc.y = fmaf(w, v.y, acc.y);
