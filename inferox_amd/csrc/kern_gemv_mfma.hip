@@ -1121,14 +1121,20 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   const uint32_t resident = per_cu * cu_count() * kWaves;
   uint32_t split = 1;
   while (split < (uint32_t)kWaves && split < a.nbr && total * split < resident) split *= 2;
-  if constexpr (NT == 2) {
-    // Paired launches (gate and up): of the splits from that one up to
-    // kWaves, the one whose busiest wave streams the fewest blocks, the
-    // larger on a tie, which leaves fewer waves idle at the end.  8B (896
-    // tile pairs, 16 blocks): split 4 gives 128 of 512 wave groups one item
-    // against two, split 8 gives 128 of 256 workgroups three against four,
-    // 8 blocks on the busiest wave either way: gate/up 14.30 -> 14.07 us.
-    // 70B (1792 pairs, 32 blocks): 32 blocks at split 2, 28 at split 8.
+  if (a.nseg == 1) {
+    // One segment (gate and up paired, the output head, ...): of the splits
+    // from that one up to kWaves, the one whose busiest wave streams the
+    // fewest blocks, the larger on a tie.  The waves that share an item meet
+    // at its reduction, so a larger split keeps a CU's waves in step and
+    // fewer of them idle at the end:
+    //   8B gate/up (896 tile pairs, 16 blocks): split 4 gives 128 of 512
+    //   wave groups one item against two, split 8 gives 128 of 256
+    //   workgroups three against four, 8 blocks on the busiest wave either
+    //   way: 14.30 -> 14.07 us.  70B (1792 pairs, 32 blocks): 32 blocks at
+    //   split 2, 28 at split 8.
+    //   8B head (8016 tiles): 64 blocks on the busiest wave at every split;
+    //   one wave per tile ended anywhere from 36 to 77 us (the waves of a CU
+    //   stream at unequal rates), 80 us per launch against 69 at split 8.
     auto busiest = [&](uint32_t sp) {
       const uint32_t nb = std::min<uint32_t>((total * sp + kWaves - 1) / kWaves, per_cu * cu_count());
       const uint32_t tg = nb * ((uint32_t)kWaves / sp);
