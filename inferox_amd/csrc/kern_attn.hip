@@ -139,6 +139,34 @@ __device__ __forceinline__ float class4_reduce(float v) {
   return pair16(__uint_as_float(r32[0]), __uint_as_float(r32[1]), MAX);
 }
 
+// v + (v of lane ^ OFF), OFF a power of two from 4 to 32, whole wave active:
+// row_half_mirror then quad_perm [3,2,1,0] (4), row_ror:8 (8), the gfx950
+// swaps of rows 0<->1, 2<->3 (16) and of the two halves (32).
+template <int OFF>
+__device__ __forceinline__ float xor_add(float v) {
+  static_assert(OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane offset");
+  if constexpr (OFF == 32 || OFF == 16) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                             : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (OFF == 8) {
+    return v + dpp_f<0x128, 0xf, 0xf>(v, v);
+  } else {
+    return v + dpp_f<0x1b, 0xf, 0xf>(0.f, dpp_f<0x141, 0xf, 0xf>(v, v));
+  }
+}
+// the sum over the lanes l, l ^ OFF, l ^ 2 OFF, ... (l < OFF), in each of them
+template <int OFF>
+__device__ __forceinline__ float4 lanes_sum4(float4 v) {
+  if constexpr (OFF < 64) {
+    v = make_float4(xor_add<OFF>(v.x), xor_add<OFF>(v.y), xor_add<OFF>(v.z), xor_add<OFF>(v.w));
+    return lanes_sum4<2 * OFF>(v);
+  } else {
+    return v;
+  }
+}
+
 constexpr int kRowsPerWave = kChunk / (kThreads / 64);  // 16
 
 // Cache rows [lo, hi) the current token attends to.  The three fields are read
@@ -459,11 +487,31 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
       }
     }
   }
-  red[tid] = acc;
-  __syncthreads();
+  // the splits' partial sums: with a power-of-two column count up to 32 the
+  // wave's splits (lane = nc4 (sp mod 64 / nc4) + col) meet through xor
+  // butterflies and the waves' sums through LDS; otherwise one thread per
+  // column adds them up through LDS
+  constexpr int NC4 = HDT > 0 ? HDT / 4 / CS : 0;
+  constexpr bool kTree = NC4 >= 4 && NC4 <= 32 && (NC4 & (NC4 - 1)) == 0;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (kTree) {
+    acc = lanes_sum4<NC4>(acc);
+    if (lane < NC4) red[wave * NC4 + lane] = acc;
+    __syncthreads();
+    if (tid < NC4) {
+      o = red[tid];
+#pragma unroll
+      for (int w = 1; w < kThreads / 64; w++) o = add4(o, red[w * NC4 + tid]);
+    }
+  } else {
+    red[tid] = acc;
+    __syncthreads();
+    if ((uint32_t)tid < nc4) {
+      o = red[tid];
+      for (uint32_t q = 1; q < nsplit; q++) o = add4(o, red[q * nc4 + tid]);
+    }
+  }
   if ((uint32_t)tid < nc4) {
-    float4 o = red[tid];
-    for (uint32_t q = 1; q < nsplit; q++) o = add4(o, red[q * nc4 + tid]);
     float dsum = 0.f;
 #pragma unroll
     for (int w = 0; w < kThreads / 64; w++) dsum += wred[1][w];
