@@ -785,8 +785,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
 // neighbouring lane) and adds them, as the O and down launches add into h,
 // straight into q and into the f32 cache's new row (cache row state->len):
 // the attention reads both as the tiled launch leaves them.  Those rows are
-// cleared beforehand (QkvClear: the layer before's O launch, or the step's
-// embedding gather for layer 0).
+// cleared beforehand, every layer's at once by the step's embedding gather
+// (QkvClear; each layer has its own q buffer).
 // The waves of a slice are shared out over q, k and v in proportion to their
 // tiles, and each wave runs tiles of one segment (one buffer type, and its
 // segment's fields at fixed kernel-argument offsets: a segment looked up per
