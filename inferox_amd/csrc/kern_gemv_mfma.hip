@@ -687,16 +687,19 @@ __device__ __forceinline__ void ks_prefetch(uint32_t nbs, const KsWave& w, const
 
 // The wave's units against the slice of x staged in LDS (digit planes at 0,
 // group sums at xs_off); each finished tile's 16 row sums go to m.emit.
-template <int T, int D, class M>
+// LOCK: every wave of the workgroup runs Wu units (the workgroup's largest
+// count; units past its own W are the ring's unused loads) and the waves meet
+// at a barrier after each round of D units.
+template <int T, int D, class M, bool LOCK = false>
 __device__ __forceinline__ void ks_run(uint32_t nbs, uint32_t xs_off, uint32_t zero_off, const KsWave& w, const M& m,
-                                       KBuf<T> (&buf)[D], const uint8_t* lds, int lane) {
-  if (w.W == 0) return;
+                                       KBuf<T> (&buf)[D], const uint8_t* lds, int lane, uint32_t Wu = 0) {
+  if ((LOCK ? Wu : w.W) == 0) return;
   const int ai = lane & 15, ag = lane >> 4;
   const bool active = (ai >> 2) == ag && (ai & 3) < 3;
   const uint32_t a_base = active ? (uint32_t)(2 * kPartBytes * ag + 16 * (ai & 3)) : zero_off;
   const uint32_t a_step = active ? kBlockA : 0u;
   const float4* xs4 = (const float4*)(lds + xs_off) + ag;
-  const uint32_t Wp = (w.W + D - 1) / D * D;
+  const uint32_t Wp = ((LOCK ? Wu : w.W) + D - 1) / D * D;
   float acc = 0.f;
   uint32_t bl = 0, tile = w.t0;                                            // unit u: local block, tile
   uint32_t rb = (uint32_t)D % nbs, rt = w.t0 + ((uint32_t)D / nbs) * w.tstride;  // unit u + D
@@ -735,6 +738,7 @@ __device__ __forceinline__ void ks_run(uint32_t nbs, uint32_t xs_off, uint32_t z
         pre = m.pre(tile, lane);
       }
     }
+    if constexpr (LOCK) __builtin_amdgcn_s_barrier();
   }
 }
 
@@ -749,7 +753,7 @@ __device__ __forceinline__ void loads_first() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int T, int D>
+template <int T, int D, bool LOCK>
 __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -768,7 +772,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks(KsArgs a) {
   }
   ks_zero(a, lds, tid);
   __syncthreads();
-  ks_run<T, D>(a.nbs, a.xs_off, a.zero_off, w, m, buf, lds, lane);
+  // wave 0 has the workgroup's first tile, so the most units
+  ks_run<T, D, KsToH<T>, LOCK>(a.nbs, a.xs_off, a.zero_off, w, m, buf, lds, lane, KsWave(a, 0u).W);
 }
 
 // ---------------------------------------------------------------------------
@@ -1224,8 +1229,18 @@ hipError_t launch_mfma_residual_ks(const GemvLaunch& L, float* h, hipStream_t st
   size_t lds;
   const hipError_t e = ks_plan(L, h, a, blocks, lds);
   if (e != hipSuccess) return e;
-  if (L.seg[0].type == T_Q6K) hipLaunchKernelGGL((k_gemv_ks<T_Q6K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
-  else hipLaunchKernelGGL((k_gemv_ks<T_Q4K, kKsRing>), dim3(blocks), dim3(kThreads), lds, st, a);
+  // The waves of a workgroup in lockstep (a barrier per ring round): 70B
+  // down 30.45 -> 29.55 us (28 units per wave), O 7.91 -> 7.80; no change at
+  // 8B (7 units per wave).  IFX_KS_LOCK=0 runs each wave on its own.
+  const char* lk = getenv("IFX_KS_LOCK");
+  const bool lock = !(lk && lk[0] == '0' && lk[1] == 0);
+  if (L.seg[0].type == T_Q6K) {
+    if (lock) hipLaunchKernelGGL((k_gemv_ks<T_Q6K, kKsRing, true>), dim3(blocks), dim3(kThreads), lds, st, a);
+    else hipLaunchKernelGGL((k_gemv_ks<T_Q6K, kKsRing, false>), dim3(blocks), dim3(kThreads), lds, st, a);
+  } else {
+    if (lock) hipLaunchKernelGGL((k_gemv_ks<T_Q4K, kKsRing, true>), dim3(blocks), dim3(kThreads), lds, st, a);
+    else hipLaunchKernelGGL((k_gemv_ks<T_Q4K, kKsRing, false>), dim3(blocks), dim3(kThreads), lds, st, a);
+  }
   return hipGetLastError();
 }
 
