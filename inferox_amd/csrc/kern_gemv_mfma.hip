@@ -945,11 +945,15 @@ __device__ __forceinline__ float4 fma4(float w, float4 v, float4 acc) {
 constexpr uint32_t kMergeFirst = 48;
 constexpr uint32_t kMergeBoundStep = 8;  // the host's bounds are multiples of this
 
-template <int T, int D, int G>
+// FB: the host's bound on the step's chunk count (a multiple of
+// kMergeBoundStep up to kMergeFirst), the chunks whose records the prologue
+// loads: each of those loads costs the CU's address path 1 KB per wave, hit
+// or miss, so the launch loads no more of them than the bound.
+template <int T, int D, int G, int FB>
 __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
-  constexpr int HD = 128, SD = G * HD, NC4 = SD / 4, NS = kThreads / NC4, KB = (int)kMergeFirst / NS;
-  static_assert(kThreads % NC4 == 0 && SD / 8 <= kThreads, "slice shape");
-  static_assert(kMergeFirst <= 64, "the first loads' weights come from one lane each");
+  constexpr int HD = 128, SD = G * HD, NC4 = SD / 4, NS = kThreads / NC4, KB = FB / NS;
+  static_assert(kThreads % NC4 == 0 && SD / 8 <= kThreads && FB % NS == 0, "slice shape");
+  static_assert(FB <= (int)kMergeFirst && kMergeFirst <= 64, "the first loads' weights come from one lane each");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float4 red[kThreads];
   __shared__ __attribute__((aligned(16))) float xsl[SD];
@@ -971,7 +975,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
   // host's bound, a multiple of NS, or the buffer) to fe - 1 (repeats: cache
   // hits); what lies past nch (records of earlier steps, or never written)
   // is masked out by selects.
-  const uint32_t fe = min(min(a.first, kMergeFirst), a.max_chunks), cl = fe - 1;
+  const uint32_t fe = min(min(a.first, (uint32_t)FB), a.max_chunks), cl = fe - 1;
   // wave g < G: the max and sum of head g over chunks lane, lane + 64, ... (issued first)
   float m0 = -INFINITY, l0 = 0.f;
   if (wave < (uint32_t)G) {
@@ -1344,8 +1348,20 @@ hipError_t launch_mfma_residual_merge(const GemvLaunch& L, const AttnArgs& at, f
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a);
     return hipGetLastError();
   };
-  if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 8>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 8>);
-  return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 4>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 4>);
+  auto types = [&](auto fb) {
+    constexpr int FB = decltype(fb)::value;
+    if (g8) return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 8, FB>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 8, FB>);
+    return q6 ? go(k_gemv_ks_merge<T_Q6K, kKsRing, 4, FB>) : go(k_gemv_ks_merge<T_Q4K, kKsRing, 4, FB>);
+  };
+  static_assert(kMergeFirst == 48 && kMergeBoundStep == 8, "one kernel per bound below");
+  switch (a.first) {
+    case 8: return types(std::integral_constant<int, 8>{});
+    case 16: return types(std::integral_constant<int, 16>{});
+    case 24: return types(std::integral_constant<int, 24>{});
+    case 32: return types(std::integral_constant<int, 32>{});
+    case 40: return types(std::integral_constant<int, 40>{});
+    default: return types(std::integral_constant<int, 48>{});
+  }
 }
 
 template hipError_t launch_mfma<EpiStore>(const GemvLaunch&, const EpiStore&, hipStream_t);
