@@ -9,8 +9,8 @@
 * 70B shape: decode over an 8192-row cache (two layers; 129 chunk records per
   kv head to merge).
 * The attention merge in the O projection's prologue (the default up to 48
-  chunk records) forced at 63 and 129 records, and the separate merge launch
-  forced at 33.
+  chunk records) at a length in each of its chunk bounds (8 to 48 records),
+  forced at 63 and 129 records, and the separate merge launch forced at 33.
 * Long caches past one merge batch (256 chunks of 64 rows): 4200 and 20000
   rows at query-group sizes 1, 4 and 8, with the f32 and the f16 cache.
 * Tiny model prefill chunks of 129, 300 and 512 ids (several 128-query
@@ -117,6 +117,21 @@ def test_merge_in_o_projection_long(tmpdir_session, monkeypatch, shape, rows):
     p = _model(tmpdir_session, name, spec, seed)
     g, o = GpuModel(p), orc.Model(p)
     _decode_from_import(g, o, rows, rows + 8, 2, 321, seed=rows + 7)
+    g.close()
+    o.close()
+
+
+@pytest.mark.parametrize("shape,rows", [("8b", r) for r in (100, 900, 1400, 1900, 2400, 2900)]
+                         + [("70b", 900), ("70b", 2900)])
+def test_merge_in_o_projection_each_bound(tmpdir_session, shape, rows):
+    """The merged O launch at every chunk bound it has an instance for: 2, 15,
+    22, 30, 38 and 46 chunk records per kv head (the host's bounds 8, 16, 24,
+    32, 40 and 48; the launch loads that many records per kv head)."""
+    base, name, seed = (synth.LLAMA3_8B, "l8b_2l.gguf", 8) if shape == "8b" else (synth.LLAMA3_70B, "l70b_2l.gguf", 70)
+    spec = synth.reduced(base, n_layers=2, ctx=512)
+    p = _model(tmpdir_session, name, spec, seed)
+    g, o = GpuModel(p), orc.Model(p)
+    _decode_from_import(g, o, rows, rows + 8, 1, 555, seed=rows + 3)
     g.close()
     o.close()
 
