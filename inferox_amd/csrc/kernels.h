@@ -253,6 +253,7 @@ struct AttnArgs {
   const DevState* state;
   uint32_t n_heads, n_kv_heads, head_dim, max_chunks, chunk, max_seq;
   uint32_t kv_f16;
+  uint32_t hk_fast = 0;  // chunk grid ordered kv head fastest (set by the launcher)
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
 // the chunk records only (their merge is left to launch_mfma_residual_merge)
