@@ -536,11 +536,13 @@ int attn_cu_count() {
 template <typename E>
 void launch_typed(const AttnArgs& a0, hipStream_t st, bool merge) {
   // Chunk grid order: kv head fastest while the grid holds at most two
-  // workgroups per CU, so that the workgroups that double up on a CU are the
-  // light last chunks (8B at ctx 2048: 296 workgroups on 256 CUs, decode
-  // 679.5 -> 684.8 tok/s on one box); chunk fastest for larger grids (70B at
-  // ctx 8192, 1048 workgroups: attention 20.17 against 20.74 us kv head
-  // fastest).  IFX_ATTN_HKF=0 / 1 forces either.
+  // workgroups per CU, so that every chunk of kv head hk runs on XCD hk
+  // (workgroup g runs on XCD g mod 8) with that head's contiguous K/V rows,
+  // and its records stay in the L2 the merged O launch's slice hk reads (8B
+  // at ctx 2048, 296 workgroups: decode 679.5 -> 684.8 tok/s on one box; an
+  // order that only put the light last chunks last gained nothing).  Chunk
+  // fastest for larger grids (70B at ctx 8192, 1048 workgroups: attention
+  // 20.17 against 20.74 us kv head fastest).  IFX_ATTN_HKF=0 / 1 forces either.
   AttnArgs a = a0;
   const char* hf = getenv("IFX_ATTN_HKF");
   const bool forced = hf && (hf[0] == '0' || hf[0] == '1') && hf[1] == 0;
