@@ -318,6 +318,75 @@ int ifx_ops_embedding_lookup(const ifx_tensor* table, const uint32_t* ids, uint6
  * (device int) becomes IFX_E_NAN_LOGIT if a NaN is present. out: device u32. */
 int ifx_ops_argmax(const float* x, uint64_t n, uint32_t* out, int* status_out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * The decode step's attention, q/k/v and residual launches as operators, on
+ * caller buffers (device pointers).  A device KV cache here is head-major,
+ * [n_kv_heads][max_seq][head_dim] of kv_type (IFX_KV_F32 or IFX_KV_F16), the
+ * layout a session keeps.  Each call allocates its small device state, runs
+ * on `stream` (NULL = the library's) and returns when its work is complete.
+ * ------------------------------------------------------------------------- */
+/* The decode attention of Layer::decode_step (src/model/forward.rs:383-414,
+ * softmax_rows src/ops.rs:223-239): query head h (kv head h / (n_heads /
+ * n_kv_heads)) of q [n_heads*head_dim] attends to cache rows 0 .. n_rows-1:
+ * out[h] = sum_t softmax_t(q_h . k_t / sqrt(head_dim)) v_t, through the
+ * step's launches (records of 64-row chunks, then their merge).  head_dim a
+ * multiple of 4 (f32 cache) or 8 (f16) up to 256; at most 8 query heads per
+ * kv head. */
+int ifx_ops_attention_decode(const float* q, const void* k_cache, const void* v_cache, int kv_type, uint64_t max_seq,
+                             uint64_t n_rows, uint64_t n_heads, uint64_t n_kv_heads, uint64_t head_dim, float* out,
+                             void* stream);
+/* ifx_ops_attention_decode, then h += W_o . attn: the attn_output projection
+ * and residual add of Layer::decode_step (src/model/forward.rs:415-419), h of
+ * W_o's rows.  merge_bound > 0: the step's fused form, the chunk records
+ * merged inside the O projection's prologue, which loads merge_bound records
+ * per kv head up front (rounded up to a multiple of 8, at most 48) and any
+ * further ones in a loop; needs 8 kv heads, head dim 128, 4 or 8 query heads
+ * per kv head and a Q4_K/Q6_K W_o of n_heads*head_dim = 1024*group columns
+ * (IFX_E_INVALID_ARG otherwise).  merge_bound 0: the separate merge launch,
+ * then the O launch the step takes.  attn_out: NULL, or a device buffer of
+ * n_heads*head_dim floats for the attention output (separate form only). */
+int ifx_ops_attention_decode_o(const float* q, const void* k_cache, const void* v_cache, int kv_type,
+                               uint64_t max_seq, uint64_t n_rows, uint64_t n_heads, uint64_t n_kv_heads,
+                               uint64_t head_dim, const ifx_tensor* w_o, float* h, uint32_t merge_bound,
+                               float* attn_out, void* stream);
+/* The attention of a prefill chunk (Layer::prefill, src/model/forward.rs:
+ * 255-303; causal) or of Layer::forward (src/model/forward.rs:104-156;
+ * causal = 0) over its own cache rows: query row t of q [n][n_heads*head_dim]
+ * attends to cache rows row0 .. row0+t (causal) or row0 .. row0+n-1; out
+ * [n][n_heads*head_dim].  The batched prefill's kernels; head_dim 48, 64, 96
+ * or 128. */
+int ifx_ops_attention_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_type,
+                              uint64_t max_seq, uint64_t row0, uint64_t n, uint64_t n_heads, uint64_t n_kv_heads,
+                              uint64_t head_dim, int causal, float* out, void* stream);
+/* h[rows] += W . x[cols]: matmul_t + add_in_place of the attn_output and
+ * ffn_down projections (src/model/forward.rs:415-419,432-437).  mode 0: the
+ * decode step's launch (for Q4_K/Q6_K matrices it takes, K split over 8
+ * workgroup slices whose partial sums are added with atomics); mode 1: the
+ * tiled launch, each row summed in one fixed order.  *path_out (optional):
+ * 1 if the K-split launch ran, else 0. */
+int ifx_ops_gemv_residual(const ifx_tensor* w, const float* x, float* h, int mode, int* path_out, void* stream);
+/* q/k/v of one decode token (src/model/forward.rs:357-378): x_n =
+ * rms_norm(x, norm_w, eps); q = Wq x_n, k = Wk x_n, v = Wv x_n; RoPE of q and
+ * k at position pos (base rope_base over the first rope_dim dims of each
+ * head, src/ops.rs:265-287); q -> q_out; k, v -> row `row` of the caches.
+ * pos < 131072.  mode 0: the decode step's launch (for Q4_K/Q6_K matrices
+ * and an f32 cache, K split over 8 slices whose RoPE-rotated partial sums are
+ * added into q and the cache rows with atomics); mode 1: the tiled launch.
+ * *path_out (optional): 1 if the K-split launch ran. */
+int ifx_ops_qkv(const ifx_tensor* wq, const ifx_tensor* wk, const ifx_tensor* wv, const float* x, const float* norm_w,
+                float eps, uint64_t head_dim, uint64_t rope_dim, float rope_base, uint64_t pos, float* q_out,
+                void* k_cache, void* v_cache, int kv_type, uint64_t max_seq, uint64_t row, int mode, int* path_out,
+                void* stream);
+
+/* Fixed summation order for a session (no reference counterpart; the
+ * reference adds in one order, src/ops.rs:212-217, src/model/forward.rs:
+ * 419,437).  on = 1: q/k/v, attn_output and ffn_down take the tiled launches
+ * and the attention merge its own launch, so two runs of the same calls give
+ * bit-identical logits, tokens and draws.  on = 0 (default): the faster
+ * K-split launches, whose atomic adds of partial sums can differ in the last
+ * bits between runs.  Takes effect from the next step. */
+int ifx_session_set_deterministic(ifx_session* s, int on);
+
 #ifdef __cplusplus
 }
 #endif

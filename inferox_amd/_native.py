@@ -91,6 +91,12 @@ SIGNATURES = {
     "ifx_ops_rope": (i32, [vp, u64, u64, u64, u64, f32, u64, vp]),
     "ifx_ops_embedding_lookup": (i32, [vp, vp, u64, vp, vp]),
     "ifx_ops_argmax": (i32, [vp, u64, vp, vp, vp]),
+    "ifx_ops_attention_decode": (i32, [vp, vp, vp, i32, u64, u64, u64, u64, u64, vp, vp]),
+    "ifx_ops_attention_decode_o": (i32, [vp, vp, vp, i32, u64, u64, u64, u64, u64, vp, vp, u32, vp, vp]),
+    "ifx_ops_attention_prefill": (i32, [vp, vp, vp, i32, u64, u64, u64, u64, u64, u64, i32, vp, vp]),
+    "ifx_ops_gemv_residual": (i32, [vp, vp, vp, i32, P(i32), vp]),
+    "ifx_ops_qkv": (i32, [vp, vp, vp, vp, vp, f32, u64, u64, f32, u64, vp, vp, vp, i32, u64, u64, i32, P(i32), vp]),
+    "ifx_session_set_deterministic": (i32, [vp, i32]),
 }
 
 
@@ -118,6 +124,8 @@ def synth() -> C.CDLL:
         L = C.CDLL(SYNTH_LIB)
         L.ifx_synth_fill.restype = i32
         L.ifx_synth_fill.argtypes = [vp, u32, u64, u64, C.c_double, C.c_double, C.c_double, C.c_double]
+        L.ifx_synth_fill_centred.restype = i32
+        L.ifx_synth_fill_centred.argtypes = [vp, u32, u64, u64, C.c_double, C.c_double, C.c_double]
         L.ifx_synth_token_ids.restype = None
         L.ifx_synth_token_ids.argtypes = [vp, u64, u32, u64]
         L.ifx_synth_normal_f32.restype = None

@@ -45,6 +45,7 @@ int device_init() {
 
 static hipStream_t stream_of(void* s) { return s ? (hipStream_t)s : g_stream; }
 hipStream_t library_stream() { return g_stream; }
+hipStream_t ops_stream(void* s) { return stream_of(s); }
 
 DevW devw(const ifx_tensor* t) {
   DevW w{t->L.type, t->L.cols, t->L.body, t->L.scal, t->L.q6_signed, 0, 0};

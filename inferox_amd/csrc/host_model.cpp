@@ -73,6 +73,9 @@ struct ifx_session {
   hipGraphExec_t exec[2][kMergeGraphs] = {};
   bool graph_tried[2][kMergeGraphs] = {};
   bool sampling = false;                 // set for the duration of ifx_generate_sampled
+  // fixed summation order (ifx_session_set_deterministic): q/k/v, O and down
+  // through the tiled launches, the attention merge in its own launch
+  bool deterministic = false;
   uint32_t merge_bound = 0;              // of the step being enqueued: 0, or a multiple of 8 up to 48
   float* probs = nullptr;                // k_sample scratch [vocab]
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -93,6 +96,23 @@ struct ifx_session {
     void* kv_split = nullptr;  // the attention's fp16 K/V pairs (attn_prefill_ws_bytes)
   } ws;
 };
+
+namespace ifx {
+// RoPE table in the reference arithmetic (src/ops.rs:278-280), glibc
+// powf/sinf/cosf: inv = 1/powf(base, i/rope_dim); angle = pos*inv; row pos of
+// out holds (cos, sin) of pair i at [pos * rope_dim/2 + i], for pos < n_pos.
+void rope_table_host(float base, uint64_t rope_dim, uint64_t n_pos, std::vector<float2>& out) {
+  const uint64_t half = rope_dim / 2;
+  out.assign(n_pos * std::max<uint64_t>(half, 1), make_float2(1.f, 0.f));
+  std::vector<float> inv(half);
+  for (uint64_t i = 0; i < half; i++) inv[i] = 1.0f / powf(base, (float)(2 * i) / (float)rope_dim);
+  for (uint64_t p = 0; p < n_pos; p++)
+    for (uint64_t i = 0; i < half; i++) {
+      const float ang = (float)p * inv[i];
+      out[p * half + i] = make_float2(cosf(ang), sinf(ang));
+    }
+}
+}  // namespace ifx
 
 namespace {
 
@@ -279,6 +299,7 @@ QkvClear qkv_clear_rows(const ifx_session* s) {
 // launch with the q/k/v epilogue otherwise.  IFX_QKV_KS=0 keeps the tiled
 // launch.  Decided once per session.
 bool qkv_split(ifx_session* s) {
+  if (s->deterministic) return false;
   if (s->qkv_ks >= 0) return s->qkv_ks == 1;
   const char* f = getenv("IFX_QKV_KS");
   bool ok = !(f && f[0] == '0' && f[1] == 0) && s->kv_es == 4 && !s->m->layers.empty();
@@ -347,7 +368,8 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       // the merge of the chunk records moves into the O launch's prologue
       const bool fused = s->merge_bound && merge_o_supported(go, a);
       if (k == 2) IFX_HIP(fused ? launch_attn_partials(a, st) : launch_attn_decode(a, st));
-      else IFX_HIP(fused ? launch_mfma_residual_merge(go, a, s->hidden, st, s->merge_bound) : gemv_residual(go, s->hidden, st));
+      else if (fused) IFX_HIP(launch_mfma_residual_merge(go, a, s->hidden, st, s->merge_bound));
+      else IFX_HIP(s->deterministic ? gemv_residual_fixed(go, s->hidden, st) : gemv_residual(go, s->hidden, st));
       return IFX_OK;
     }
     case 4: {
@@ -364,7 +386,8 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       return IFX_OK;
     }
     case 5:
-      IFX_HIP(gemv_residual(down_launch(s, L), s->hidden, st));
+      IFX_HIP(s->deterministic ? gemv_residual_fixed(down_launch(s, L), s->hidden, st)
+                               : gemv_residual(down_launch(s, L), s->hidden, st));
       return IFX_OK;
     default:
       return set_error(IFX_E_INVALID_ARG, "kernel class %d", k);
@@ -392,6 +415,10 @@ uint64_t tensor_stream_bytes(const ifx_tensor* t) { return t->L.body_bytes + t->
 // cache rows before it + 1).  IFX_MERGE_O=0 / 1 takes the separate / the
 // fused merge at any length.
 void choose_merge(ifx_session* s, uint64_t rows) {
+  if (s->deterministic) {
+    s->merge_bound = 0;
+    return;
+  }
   const uint64_t nch = (rows + s->attn_chunk - 1) / s->attn_chunk, step = merge_o_bound_step();
   const uint32_t most = merge_o_first_chunks();
   const uint32_t bound = (uint32_t)std::max<uint64_t>(step, (nch + step - 1) / step * step);
@@ -780,18 +807,8 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
     session_free(s);
     return set_error(IFX_E_HIP, "stream/event creation failed");
   }
-  // RoPE table in the reference arithmetic (src/ops.rs:278-280), glibc powf/sinf/cosf:
-  // inv = 1/powf(base, i/rope_dim); angle = pos*inv.
-  const uint64_t half = c.rope_dim / 2;
-  std::vector<float2> cs(max_seq_len * std::max<uint64_t>(half, 1));
-  std::vector<float> inv(half);
-  for (uint64_t i = 0; i < half; i++)
-    inv[i] = 1.0f / powf(c.rope_base, (float)(2 * i) / (float)c.rope_dim);
-  for (uint64_t p = 0; p < max_seq_len; p++)
-    for (uint64_t i = 0; i < half; i++) {
-      const float ang = (float)p * inv[i];
-      cs[p * half + i] = make_float2(cosf(ang), sinf(ang));
-    }
+  std::vector<float2> cs;
+  rope_table_host(c.rope_base, c.rope_dim, max_seq_len, cs);
   DevState init{};
   init.rope_mode = IFX_ROPE_REFERENCE;
   init.feed_ids = s->feed_ids;
@@ -835,6 +852,22 @@ int ifx_session_set_prefill_batch(ifx_session* s, uint64_t min_rows) {
 int ifx_model_batched_prefill(const ifx_model* m, int* eligible) {
   if (!m || !eligible) return set_error(IFX_E_INVALID_ARG, "null argument");
   *eligible = m->gemm_ok ? 1 : 0;
+  return IFX_OK;
+}
+
+int ifx_session_set_deterministic(ifx_session* s, int on) {
+  if (!s || (on != 0 && on != 1)) return set_error(IFX_E_INVALID_ARG, "bad argument");
+  if (s->deterministic == (on == 1)) return IFX_OK;
+  // the captured steps hold the other launches: capture again on next use
+  IFX_HIP(hipStreamSynchronize(s->stream));
+  for (int i = 0; i < 2; i++)
+    for (int j = 0; j < ifx_session::kMergeGraphs; j++) {
+      if (s->exec[i][j]) IFX_HIP(hipGraphExecDestroy(s->exec[i][j]));
+      s->exec[i][j] = nullptr;
+      s->graph_tried[i][j] = false;
+    }
+  s->deterministic = on == 1;
+  s->qkv_ks = -1;
   return IFX_OK;
 }
 

@@ -669,6 +669,11 @@ hipError_t gemv_residual(const GemvLaunch& L, float* hidden, hipStream_t st) {
   return launch(L, EpiResidual{hidden}, st);
 }
 
+hipError_t gemv_residual_fixed(const GemvLaunch& L, float* hidden, hipStream_t st) {
+  if (L.nseg != 1) return hipErrorInvalidValue;
+  return launch(L, EpiResidual{hidden}, st);
+}
+
 hipError_t gemv_qkv(const GemvLaunch& L, const QkvEpi& e, hipStream_t st) {
   if (L.nseg != 3 || (e.head_dim & 1) || (e.rope_dim & 1)) return hipErrorInvalidValue;
   return launch(L, EpiQkv{e}, st);

@@ -139,7 +139,12 @@ struct QkvEpi {
 };
 
 hipError_t gemv_store(const GemvLaunch& L, float* y, hipStream_t st);
+// h += W x: the K-split launch where it applies (its slices' partial sums are
+// added with atomics, so the last bits may differ between runs), else the
+// tiled launch
 hipError_t gemv_residual(const GemvLaunch& L, float* hidden, hipStream_t st);
+// h += W x by the tiled launch only: each row's sum formed in one fixed order
+hipError_t gemv_residual_fixed(const GemvLaunch& L, float* hidden, hipStream_t st);
 hipError_t gemv_qkv(const GemvLaunch& L, const QkvEpi& e, hipStream_t st);
 hipError_t gemv_swiglu(const GemvLaunch& L, float* mid, hipStream_t st);
 hipError_t gemv_logits(const GemvLaunch& L, float* logits, DevState* state, hipStream_t st);

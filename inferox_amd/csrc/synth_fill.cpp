@@ -134,6 +134,50 @@ int ifx_synth_fill(uint8_t* dst, uint32_t type, uint64_t n_elements, uint64_t se
   return 0;
 }
 
+// Zero-mean K-quant blocks (test models whose attention carries weight in
+// the logits; the benchmark models keep the uniform bytes above).
+//   Q4_K : d f16 ~ U[p0,p1]; per 32-element group a 6-bit scale sc ~ U{0..63}
+//          and min mn = sc, dmin = f16(7.5 d): w = (d sc) q - (dmin sc),
+//          about d sc (q - 7.5), q uniform nibbles.  The 12 scale bytes are
+//          packed as the reference unpacks them (src/gguf/dequant.rs:139-152).
+//   Q6_K : d f16 ~ U[p0,p1] at byte 0, u8 scales ~ U{1..p2} (p2 <= 127),
+//          uniform ql/qh: w = (d sc)(q - 32), mean -d sc / 2.
+// Other types as ifx_synth_fill.  Returns 0, or -1 as ifx_synth_fill.
+int ifx_synth_fill_centred(uint8_t* dst, uint32_t type, uint64_t n_elements, uint64_t seed, double p0, double p1,
+                           double p2) {
+  if (type != 12 && type != 14) return ifx_synth_fill(dst, type, n_elements, seed, p0, p1, p2, 0.0);
+  if (n_elements % 256) return -1;
+  const uint64_t nb = n_elements / 256, bb = type == 12 ? 144 : 210;
+  const int sc_hi = p2 < 1.0 ? 1 : (p2 > 127.0 ? 127 : (int)p2);
+#pragma omp parallel for schedule(static, 4096)
+  for (uint64_t b = 0; b < nb; b++) {
+    Rng r(seed, b);
+    uint8_t* blk = dst + b * bb;
+    const uint16_t dh = f32_to_f16((float)(p0 + (p1 - p0) * r.uniform()));
+    blk[0] = (uint8_t)(dh & 0xff);
+    blk[1] = (uint8_t)(dh >> 8);
+    if (type == 12) {
+      // the f16 value of d, widened (normal range: p0 >= 6.2e-5)
+      uint32_t e = (dh >> 10) & 31u, m = dh & 1023u;
+      float d = e ? ldexpf((float)(1024u + m), (int)e - 25) : ldexpf((float)m, -24);
+      put_f16(blk + 2, 7.5 * (double)d);
+      uint8_t sc[8];
+      for (int g = 0; g < 8; g++) sc[g] = (uint8_t)(r.next() % 64u);
+      uint8_t* s = blk + 4;
+      for (int g = 0; g < 4; g++) {
+        s[g] = (uint8_t)((sc[g] & 63u) | ((sc[g + 4] >> 4) << 6));      // sc_g, top bits of sc_{g+4}
+        s[g + 4] = (uint8_t)((sc[g] & 63u) | ((sc[g + 4] >> 4) << 6));  // mn_g = sc_g, top bits of mn_{g+4}
+        s[g + 8] = (uint8_t)((sc[g + 4] & 15u) | ((sc[g + 4] & 15u) << 4));
+      }
+      r.bytes(blk + 16, 128);
+    } else {
+      for (int j = 0; j < 16; j++) blk[2 + j] = (uint8_t)(1 + r.next() % (uint64_t)sc_hi);
+      r.bytes(blk + 18, 192);
+    }
+  }
+  return 0;
+}
+
 // Seeded uniform token ids in [0, vocab).
 void ifx_synth_token_ids(uint32_t* out, uint64_t n, uint32_t vocab, uint64_t seed) {
   Rng r(seed, 0x70ull);

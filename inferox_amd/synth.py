@@ -14,6 +14,14 @@ layout, d first): d ~ U[1e-4, 1e-3], scales i8 ~ U[-32, 31], uniform ql/qh.
 
 Payloads come from ``libifx_synth.so`` (counter-based per-block streams), so a
 (spec, seed) pair names exactly one file regardless of thread count.
+
+A spec with ``centred=True`` is a parity-test model instead: its Q4_K and
+Q6_K matrices are zero-mean (``ifx_synth_fill_centred``) and scaled so that a
+matrix-vector product with a unit-RMS input has output std ``CENTRED_GAIN``
+of its role.  With the uniform bytes above every Q4_K element has mean ~1.2,
+so a token's own key dominates the attention scores and the greedy pick
+hardly moves; in a centred model q.k / sqrt(head_dim) has std ~1.5, the
+softmax spreads over many cache rows and the logits follow the attention.
 """
 from __future__ import annotations
 
@@ -53,6 +61,10 @@ class LlamaSpec:
     eps: float = 1e-5
     types: Dict[str, int] = field(default_factory=dict)
     tied_output: bool = False
+    centred: bool = False
+    # per-layer type overrides: {layer: {role: type}} (real Q4_K_M files give
+    # attn_v / ffn_down Q6_K in some layers only)
+    layer_types: Dict[int, Dict[str, int]] = field(default_factory=dict)
 
     @property
     def head_dim(self) -> int:
@@ -62,7 +74,9 @@ class LlamaSpec:
     def kv_dim(self) -> int:
         return self.n_kv_heads * self.head_dim
 
-    def t(self, role: str) -> int:
+    def t(self, role: str, layer: Optional[int] = None) -> int:
+        if layer is not None and role in self.layer_types.get(layer, {}):
+            return self.layer_types[layer][role]
         return self.types[role]
 
     def shapes(self):
@@ -73,11 +87,12 @@ class LlamaSpec:
             out.append(("output.weight", self.t("output"), V, D))
         for i in range(self.n_layers):
             p = f"blk.{i}."
-            out += [(p + "attn_norm.weight", F32, 1, D), (p + "attn_q.weight", self.t("q"), D, D),
-                    (p + "attn_k.weight", self.t("k"), KV, D), (p + "attn_v.weight", self.t("v"), KV, D),
-                    (p + "attn_output.weight", self.t("o"), D, D), (p + "ffn_norm.weight", F32, 1, D),
-                    (p + "ffn_gate.weight", self.t("gate"), Fd, D), (p + "ffn_up.weight", self.t("up"), Fd, D),
-                    (p + "ffn_down.weight", self.t("down"), D, Fd)]
+            t = lambda role: self.t(role, i)  # noqa: E731
+            out += [(p + "attn_norm.weight", F32, 1, D), (p + "attn_q.weight", t("q"), D, D),
+                    (p + "attn_k.weight", t("k"), KV, D), (p + "attn_v.weight", t("v"), KV, D),
+                    (p + "attn_output.weight", t("o"), D, D), (p + "ffn_norm.weight", F32, 1, D),
+                    (p + "ffn_gate.weight", t("gate"), Fd, D), (p + "ffn_up.weight", t("up"), Fd, D),
+                    (p + "ffn_down.weight", t("down"), D, Fd)]
         return [(n, ([c] if r == 1 else [c, r]), t, r, c) for (n, t, r, c) in out]
 
     def gguf_bytes(self) -> int:
@@ -92,6 +107,31 @@ TINY = LlamaSpec("tiny", 288, 768, 6, 6, 6, 32000, 10000.0, 256, types=_ALL_Q8)
 LLAMA3_8B = LlamaSpec("llama3-8b", 4096, 14336, 32, 32, 8, 128256, 500000.0, 2560, types=_Q4KM)
 LLAMA3_70B = LlamaSpec("llama3-70b", 8192, 28672, 80, 64, 8, 128256, 500000.0, 8448, types=_Q4KM)
 SPECS = {s.name: s for s in (TINY, LLAMA3_8B, LLAMA3_70B)}
+
+
+# centred models: output std of each role's matrix-vector product for a
+# unit-RMS input (the embedding: std of its elements)
+CENTRED_GAIN = {"embd": 1.0, "q": 1.25, "k": 1.25, "v": 1.0, "o": 1.0, "gate": 1.0, "up": 1.0, "down": 1.0,
+                "output": 2.0}
+CENTRED_Q6_SC_MAX = 3  # Q6_K scale bytes 1..3: d stays in f16's normal range at 28672 columns
+_ELEM_STD_PER_D = {Q4_K: 168.5, Q6_K: 40.0}  # element std / d of the centred blocks
+
+
+def role_of(name: str) -> str:
+    if name == "token_embd.weight":
+        return "embd"
+    if name == "output.weight":
+        return "output"
+    base = name.split(".")[-2]  # blk.{i}.<base>.weight
+    return {"attn_q": "q", "attn_k": "k", "attn_v": "v", "attn_output": "o", "ffn_gate": "gate",
+            "ffn_up": "up", "ffn_down": "down"}.get(base, base)
+
+
+def centred_params(ggml_type: int, cols: int, role: str):
+    """(d_lo, d_hi, q6_scale_max) of a centred matrix of `cols` columns."""
+    std = CENTRED_GAIN[role] if role == "embd" else CENTRED_GAIN[role] / float(np.sqrt(cols))
+    d = std / _ELEM_STD_PER_D[ggml_type]
+    return (0.75 * d, 1.25 * d, float(CENTRED_Q6_SC_MAX))
 
 
 def fnv1a64(s: str) -> int:
@@ -116,6 +156,14 @@ def _filler(ggml_type: int, n: int, seed: int, params=None):
     return fill
 
 
+def _centred_filler(ggml_type: int, n: int, seed: int, params):
+    def fill(view: np.ndarray) -> None:
+        rc = _native.synth().ifx_synth_fill_centred(view.ctypes.data_as(C.c_void_p), ggml_type, n, seed, *params)
+        if rc != 0:
+            raise ValueError(f"synth centred fill failed for type {ggml_type}")
+    return fill
+
+
 def write_llama(path: str, spec: LlamaSpec, seed: int = 1234, norm_mean: float = 1.0,
                 norm_std: float = 0.02) -> int:
     """Write `spec` as a GGUF file at `path`; returns the file size."""
@@ -129,10 +177,16 @@ def write_llama(path: str, spec: LlamaSpec, seed: int = 1234, norm_mean: float =
     w.add_f32("llama.rope.freq_base", spec.rope_theta)
     w.add_u32("llama.context_length", spec.ctx)
     w.add_u64("inferox.synth.seed", seed)
+    if spec.centred:
+        w.add_u32("inferox.synth.centred", 1)
     for name, shape, t, r, c in spec.shapes():
         n = r * c
-        params = (norm_mean, norm_std, 0.0, 0.0) if t == F32 and name.endswith("norm.weight") else None
-        w.add_tensor(name, shape, t, fill=_filler(t, n, tensor_seed(seed, name), params))
+        if spec.centred and t in (Q4_K, Q6_K):
+            fill = _centred_filler(t, n, tensor_seed(seed, name), centred_params(t, c, role_of(name)))
+        else:
+            params = (norm_mean, norm_std, 0.0, 0.0) if t == F32 and name.endswith("norm.weight") else None
+            fill = _filler(t, n, tensor_seed(seed, name), params)
+        w.add_tensor(name, shape, t, fill=fill)
     return w.write(path)
 
 
@@ -152,6 +206,14 @@ def random_blocks(ggml_type: int, n_elements: int, seed: int, params=None) -> np
     """Seeded raw block bytes of one tensor (same generator as the model files)."""
     buf = np.zeros(byte_size(ggml_type, n_elements), dtype=np.uint8)
     _filler(ggml_type, n_elements, seed, params)(buf)
+    return buf
+
+
+def random_centred_blocks(ggml_type: int, n_elements: int, cols: int, role: str, seed: int) -> np.ndarray:
+    """Seeded zero-mean Q4_K / Q6_K block bytes of a [n_elements / cols x cols]
+    matrix of `role`, as a centred model's (same generator)."""
+    buf = np.zeros(byte_size(ggml_type, n_elements), dtype=np.uint8)
+    _centred_filler(ggml_type, n_elements, seed, centred_params(ggml_type, cols, role))(buf)
     return buf
 
 

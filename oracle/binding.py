@@ -44,6 +44,8 @@ _SIGS = {
     "orc_embedding_lookup": (i32, [vp, u64, vp, u64, u64, vp]),
     "orc_rope": (None, [vp, u64, u64, u64, u64, f32, u64]),
     "orc_argmax": (i32, [vp, u64, P(u32)]),
+    "orc_attention_decode": (i32, [vp, vp, vp, u64, u64, u64, u64, vp]),
+    "orc_attention_batch": (i32, [vp, vp, vp, u64, u64, u64, u64, i32, vp, i32]),
     "orc_model_open": (i32, [cp, P(vp)]),
     "orc_model_close": (None, [vp]),
     "orc_model_config": (i32, [vp, P(OrcConfig)]),
@@ -113,6 +115,33 @@ def matmul_t(a: np.ndarray, b: np.ndarray, m: int, n: int, k: int, scalar: bool 
     fn = lib().orc_matmul_t_scalar if scalar else lib().orc_matmul_t
     fn(_ptr(a), _ptr(b), _ptr(c), m, n, k)
     return c
+
+
+def attention_decode(q, k, v, n_rows, n_heads, n_kv_heads, head_dim):
+    """The decode step's attention (src/model/forward.rs:383-414): q [n_heads*hd]
+    over rows 0..n_rows-1 of k, v [t][n_kv_heads*hd]; returns out [n_heads*hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(n_heads * head_dim, dtype=np.float32)
+    rc = lib().orc_attention_decode(_ptr(q), _ptr(k), _ptr(v), n_rows, n_heads, n_kv_heads, head_dim, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"orc_attention_decode: status {rc}")
+    return out
+
+
+def attention_batch(q, k, v, seq, n_heads, n_kv_heads, head_dim, causal=True, mode=MODE_FAST):
+    """A prefill (causal) or forward chunk's attention (src/model/forward.rs:
+    255-303, 104-156): q [seq][n_heads*hd], k, v [seq][n_kv*hd] -> [seq][n_heads*hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(seq * n_heads * head_dim, dtype=np.float32)
+    rc = lib().orc_attention_batch(_ptr(q), _ptr(k), _ptr(v), seq, n_heads, n_kv_heads, head_dim, int(causal),
+                                   _ptr(out), mode)
+    if rc != 0:
+        raise ValueError(f"orc_attention_batch: status {rc}")
+    return out
 
 
 def rms_norm_rows(x, w, eps, rows=None):

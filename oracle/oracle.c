@@ -1269,13 +1269,89 @@ static void batch_attention_fast(const float* q, const float* k, const float* v,
   }
 }
 
+/* The chunk attention of Layer::prefill (src/model/forward.rs:255-303, causal)
+ * and Layer::forward (src/model/forward.rs:104-156, no mask), one query head
+ * after another: s_pt = (sum_d q_d k_td) / sqrt(hd) in sequence (masked keys
+ * -inf), softmax_rows over the whole row, o_pd = sum_{t <= p} p_pt v_td.
+ * q, attn: [seq][H] (head h at h*hd); k, v: [seq][nkv*hd].  scores: seq*seq
+ * floats of scratch, head_out: seq*hd. */
+static void batch_attention_ref(const float* q, const float* k, const float* v, float* attn, uint64_t seq,
+                                uint64_t nh, uint64_t nkv, uint64_t hd, uint64_t H, int causal, float* scores,
+                                float* head_out) {
+  const uint64_t grp = nh / nkv;
+  float rs = sqrtf((float)hd);
+  for (uint64_t h = 0; h < nh; h++) {
+    uint64_t hk = h / grp;
+    for (uint64_t p = 0; p < seq; p++) {
+      const float* qh = q + (p * nh + h) * hd;
+      for (uint64_t t = 0; t < seq; t++) {
+        if (causal && t > p) { scores[p * seq + t] = -INFINITY; continue; }
+        const float* kh = k + (t * nkv + hk) * hd;
+        float s = 0.0f;
+        for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
+        scores[p * seq + t] = s / rs;
+      }
+    }
+    orc_softmax_rows(scores, seq, seq);
+    for (uint64_t p = 0; p < seq; p++) {
+      float* ho = head_out + p * hd;
+      for (uint64_t d = 0; d < hd; d++) ho[d] = 0.0f;
+      uint64_t tend = causal ? p + 1 : seq;
+      for (uint64_t t = 0; t < tend; t++) {
+        float sc = scores[p * seq + t];
+        const float* vh = v + (t * nkv + hk) * hd;
+        for (uint64_t d = 0; d < hd; d++) ho[d] = ho[d] + sc * vh[d];
+      }
+      memcpy(attn + p * H + h * hd, ho, hd * 4);
+    }
+  }
+}
+
+/* The decode attention of Layer::decode_step (src/model/forward.rs:383-414)
+ * on its own: every query head of q [n_heads*hd] over cache rows 0..nl-1 of k,
+ * v in the KvCache layout [t][n_kv_heads*hd] (src/model/cache.rs:8-24); out
+ * [n_heads*hd].  The same decode_head the decode step runs. */
+int orc_attention_decode(const float* q, const float* k, const float* v, uint64_t nl, uint64_t n_heads,
+                         uint64_t n_kv_heads, uint64_t hd, float* out) {
+  if (!q || !k || !v || !out || nl == 0 || hd == 0 || n_kv_heads == 0 || n_heads % n_kv_heads)
+    return ORC_E_INVALID_ARG;
+  const uint64_t grp = n_heads / n_kv_heads, kvd = n_kv_heads * hd;
+  float *scores = malloc(nl * 4), *head_out = malloc(hd * 4);
+  if (!scores || !head_out) { free(scores); free(head_out); return ORC_E_OOM; }
+  for (uint64_t h = 0; h < n_heads; h++) decode_head(q, k, v, nl, h, grp, hd, kvd, scores, head_out, out);
+  free(scores);
+  free(head_out);
+  return ORC_OK;
+}
+
+/* The chunk attention of Layer::prefill / Layer::forward on its own (the
+ * loops layer_batch runs): q, out [seq][n_heads*hd]; k, v [seq][n_kv_heads*hd]
+ * (the chunk's rows).  FAITHFUL: batch_attention_ref; FAST: the threaded form
+ * (the same bits). */
+int orc_attention_batch(const float* q, const float* k, const float* v, uint64_t seq, uint64_t n_heads,
+                        uint64_t n_kv_heads, uint64_t hd, int causal, float* out, int mode) {
+  if (!q || !k || !v || !out || seq == 0 || hd == 0 || n_kv_heads == 0 || n_heads % n_kv_heads)
+    return ORC_E_INVALID_ARG;
+  const uint64_t H = n_heads * hd;
+  if (mode == ORC_MODE_FAST) {
+    batch_attention_fast(q, k, v, out, seq, n_heads, n_kv_heads, hd, H, causal);
+    return ORC_OK;
+  }
+  float *scores = malloc(seq * seq * 4), *head_out = malloc(seq * hd * 4);
+  if (!scores || !head_out) { free(scores); free(head_out); return ORC_E_OOM; }
+  batch_attention_ref(q, k, v, out, seq, n_heads, n_kv_heads, hd, H, causal, scores, head_out);
+  free(scores);
+  free(head_out);
+  return ORC_OK;
+}
+
 /* Shared body of Layer::prefill (src/model/forward.rs:215-337, causal, writes
  * the cache) and Layer::forward (src/model/forward.rs:62-207, no mask, no cache). */
 static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_t seq, float* kc,
                        float* vc, uint64_t cache_start, int causal, int mode, int rope_mode, int kv16) {
   const orc_config* c = &m->cfg;
   uint64_t H = c->hidden_size, hd = c->head_dim, kvd = c->n_kv_heads * hd, F = c->intermediate_size;
-  uint64_t grp = c->n_heads / c->n_kv_heads, nh = c->n_heads;
+  uint64_t nh = c->n_heads;
   int rc = ORC_OK;
   float *residual = malloc(seq * H * 4), *q = malloc(seq * H * 4), *k = malloc(seq * kvd * 4);
   float *v = malloc(seq * kvd * 4), *scores = malloc(seq * seq * 4), *head_out = malloc(seq * hd * 4);
@@ -1303,32 +1379,7 @@ static int layer_batch(const orc_model* m, const orc_layer* L, float* x, uint64_
     }
   }
   if (mode == ORC_MODE_FAITHFUL) {
-    float rs = sqrtf((float)hd);
-    for (uint64_t h = 0; h < nh; h++) {
-      uint64_t hk = h / grp;
-      for (uint64_t p = 0; p < seq; p++) {
-        const float* qh = q + (p * nh + h) * hd;
-        for (uint64_t t = 0; t < seq; t++) {
-          if (causal && t > p) { scores[p * seq + t] = -INFINITY; continue; }
-          const float* kh = k + (t * c->n_kv_heads + hk) * hd;
-          float s = 0.0f;
-          for (uint64_t d = 0; d < hd; d++) s = s + qh[d] * kh[d];
-          scores[p * seq + t] = s / rs;
-        }
-      }
-      orc_softmax_rows(scores, seq, seq);
-      for (uint64_t p = 0; p < seq; p++) {
-        float* ho = head_out + p * hd;
-        for (uint64_t d = 0; d < hd; d++) ho[d] = 0.0f;
-        uint64_t tend = causal ? p + 1 : seq;
-        for (uint64_t t = 0; t < tend; t++) {
-          float sc = scores[p * seq + t];
-          const float* vh = v + (t * c->n_kv_heads + hk) * hd;
-          for (uint64_t d = 0; d < hd; d++) ho[d] = ho[d] + sc * vh[d];
-        }
-        memcpy(attn + p * H + h * hd, ho, hd * 4);
-      }
-    }
+    batch_attention_ref(q, k, v, attn, seq, nh, c->n_kv_heads, hd, H, causal, scores, head_out);
   } else {
     batch_attention_fast(q, k, v, attn, seq, nh, c->n_kv_heads, hd, H, causal);
   }

@@ -78,6 +78,14 @@ int orc_embedding_lookup(const float* emb, uint64_t vocab, const uint32_t* ids, 
 void orc_rope(float* x, uint64_t seq, uint64_t heads, uint64_t head_dim, uint64_t rope_dim,
               float base, uint64_t pos0);
 int orc_argmax(const float* x, uint64_t n, uint32_t* out);
+/* The attention loops of the decode step and of a prefill/forward chunk on
+ * their own.  Decode: q [n_heads*hd] over rows 0..nl-1 of k, v
+ * [t][n_kv_heads*hd]; batch: q, out [seq][n_heads*hd], k, v [seq][n_kv*hd],
+ * mode ORC_MODE_FAITHFUL or ORC_MODE_FAST (same bits). */
+int orc_attention_decode(const float* q, const float* k, const float* v, uint64_t nl, uint64_t n_heads,
+                         uint64_t n_kv_heads, uint64_t hd, float* out);
+int orc_attention_batch(const float* q, const float* k, const float* v, uint64_t seq, uint64_t n_heads,
+                        uint64_t n_kv_heads, uint64_t hd, int causal, float* out, int mode);
 
 /* ---- GGUF + model ---- */
 typedef struct orc_model orc_model;

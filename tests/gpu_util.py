@@ -118,6 +118,9 @@ class GpuSession:
     def set_rope_mode(self, mode: int):
         check(_native.lib().ifx_session_set_rope_mode(self.h, mode), "rope_mode")
 
+    def set_deterministic(self, on: bool):
+        check(_native.lib().ifx_session_set_deterministic(self.h, 1 if on else 0), "set_deterministic")
+
     def set_prefill_batch(self, min_rows: int):
         check(_native.lib().ifx_session_set_prefill_batch(self.h, min_rows), "prefill_batch")
 
