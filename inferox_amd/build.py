@@ -24,7 +24,7 @@ ARCH = os.environ.get("IFX_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["kern_dequant.hip", "kern_gemv.hip", "kern_gemv_mfma.hip", "kern_ops.hip", "kern_attn.hip",
                "kern_gemm.hip", "kern_attn_prefill.hip", "kern_sample.hip", "noalloc.hip",
-               "host_types.cpp", "host_gguf.cpp", "host_model.cpp", "capi_ops.cpp", "capi_attn.cpp", "host_tokenizer.cpp"]
+               "host_types.cpp", "host_gguf.cpp", "host_config.cpp", "host_model.cpp", "capi_ops.cpp", "capi_attn.cpp", "host_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",

@@ -16,6 +16,7 @@
 #include <thread>
 #include <vector>
 
+#include "host_config.h"
 #include "host_gguf.h"
 #include "ifx_common.h"
 #include "kernels.h"
@@ -116,8 +117,6 @@ void rope_table_host(float base, uint64_t rope_dim, uint64_t n_pos, std::vector<
 
 namespace {
 
-const char* kRoleNames[9] = {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
-                             "ffn_norm",  "ffn_gate", "ffn_up", "ffn_down"};
 
 int dev_alloc(std::vector<void*>& owner, void** p, size_t bytes) {
   if (bytes == 0) bytes = 4;
@@ -642,92 +641,43 @@ int model_open(const char* path, uint32_t flags, ifx_model** out) {
   m->flags = flags;
   int rc = m->map.open(path);
   if (rc == IFX_OK) rc = gguf_parse(m->map.data, m->map.size, &m->gguf);
+  // Config::from_gguf and the name resolution (host_config.cpp): parse errors
+  // are reported without touching a device
+  ModelPlan plan;
+  if (rc == IFX_OK) rc = plan_model(m->gguf, &plan);
   if (rc != IFX_OK) { model_free(m); return rc; }
   const GgufFile& f = m->gguf;
   ifx_config& c = m->cfg;
-  std::string arch;
-  if (!f.get_string("general.architecture", &arch)) {
-    model_free(m);
-    return set_error(IFX_E_TENSOR_NOT_FOUND, "general.architecture");
-  }
-  if (arch != "llama") {
-    model_free(m);
-    return set_error(IFX_E_UNSUPPORTED_ARCH, "unsupported model architecture: %s", arch.c_str());
-  }
-  snprintf(c.architecture, sizeof c.architecture, "%s", arch.c_str());
-  const char* req[3] = {"llama.embedding_length", "llama.block_count", "llama.attention.head_count"};
-  uint64_t* dst[3] = {&c.hidden_size, &c.n_layers, &c.n_heads};
-  for (int i = 0; i < 3; i++)
-    if (!f.get_u64(req[i], dst[i])) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "%s", req[i]); }
-  uint32_t u;
-  c.n_kv_heads = f.get_u32("llama.attention.head_count_kv", &u) ? u : c.n_heads;
-  if (c.n_heads == 0) { model_free(m); return set_error(IFX_E_INVALID_ARG, "head_count is 0"); }
-  c.head_dim = f.get_u32("llama.attention.key_length", &u) ? u : c.hidden_size / c.n_heads;
-  if (!f.get_u64("llama.feed_forward_length", &c.intermediate_size)) {
-    model_free(m);
-    return set_error(IFX_E_TENSOR_NOT_FOUND, "llama.feed_forward_length");
-  }
-  if (!f.get_f32("llama.attention.layer_norm_rms_epsilon", &c.norm_eps)) c.norm_eps = 1e-5f;
-  if (!f.get_f32("llama.rope.freq_base", &c.rope_base)) c.rope_base = 10000.0f;
-  c.rope_dim = f.get_u32("llama.rope.dimension_count", &u) ? u : c.head_dim;
-  c.context_length = f.get_u32("llama.context_length", &u) ? u : 4096;
-  c.vocab_size = f.get_u32("llama.vocab_size", &u) ? u : 0;
+  c = plan.cfg;
 
-  // name resolution (src/model/mod.rs:34-48,64-92).  block_count comes from
-  // the file: the indices grow one layer at a time, so a count larger than the
-  // file's tensors can hold ends at the first missing blk.N tensor
-  // (TensorNotFound, as the reference reports it) without sizing anything by it.
-  std::vector<int64_t> idx;
-  for (uint64_t l = 0; l < c.n_layers; l++)
-    for (int r = 0; r < 9; r++) {
-      char nm[128];
-      snprintf(nm, sizeof nm, "blk.%llu.%s.weight", (unsigned long long)l, kRoleNames[r]);
-      const int64_t ti = f.tensor_index(nm);
-      if (ti < 0) {
-        model_free(m);
-        return set_error(IFX_E_TENSOR_NOT_FOUND, "blk.%llu.*", (unsigned long long)l);
-      }
-      idx.push_back(ti);
-    }
-  int64_t i_embd = f.tensor_index("token_embd.weight");
-  if (i_embd < 0) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "token_embd.weight"); }
-  int64_t i_onorm = f.tensor_index("output_norm.weight");
-  if (i_onorm < 0) { model_free(m); return set_error(IFX_E_TENSOR_NOT_FOUND, "output_norm.weight"); }
-  int64_t i_out = f.tensor_index("output.weight");
-
-  // upload once (parse errors above are reported without touching a device)
+  // upload once
   rc = device_init();
   if (rc != IFX_OK) { model_free(m); return rc; }
-  const uint64_t D = c.hidden_size, F = c.intermediate_size, KV = c.n_kv_heads * c.head_dim;
+  uint64_t shapes[R_COUNT][2];
+  rc = plan_shapes(f, &plan, shapes);
+  if (rc != IFX_OK) { model_free(m); return rc; }
+  const uint64_t D = c.hidden_size;
   m->dims_ok = check_dims(m) == IFX_OK;
   clear_error();
-  const uint64_t embd_n = f.tensors[i_embd].n_elements();
-  if (D == 0 || embd_n % D) {
-    model_free(m);
-    return set_error(IFX_E_INVALID_ARG, "token_embd.weight is not [*, %llu]", (unsigned long long)D);
-  }
-  rc = upload_weight(m, i_embd, embd_n / D, D, &m->embd);
-  if (rc == IFX_OK && i_out >= 0) {
-    const uint64_t n = f.tensors[i_out].n_elements();
-    rc = n % D ? set_error(IFX_E_INVALID_ARG, "output.weight is not [*, %llu]", (unsigned long long)D)
-               : upload_weight(m, i_out, n / D, D, &m->output);
-  } else if (rc == IFX_OK) {
-    m->output = m->embd;
-  }
+  const int64_t i_onorm = plan.out_norm;
+  rc = upload_weight(m, plan.embd.idx, plan.embd.rows, D, &m->embd);
+  if (rc == IFX_OK && plan.output.idx >= 0) rc = upload_weight(m, plan.output.idx, plan.output.rows, D, &m->output);
+  else if (rc == IFX_OK) m->output = m->embd;
   if (rc == IFX_OK) rc = upload_norm(m, i_onorm, D, &m->out_norm);
   m->layers.resize(c.n_layers);
   for (uint64_t l = 0; l < c.n_layers && rc == IFX_OK; l++) {
     LayerDev& L = m->layers[l];
-    const int64_t* x = &idx[l * 9];
-    if (rc == IFX_OK) rc = upload_norm(m, x[0], D, &L.attn_norm);
-    if (rc == IFX_OK) rc = upload_weight(m, x[1], D, D, &L.q);
-    if (rc == IFX_OK) rc = upload_weight(m, x[2], KV, D, &L.k);
-    if (rc == IFX_OK) rc = upload_weight(m, x[3], KV, D, &L.v);
-    if (rc == IFX_OK) rc = upload_weight(m, x[4], D, D, &L.o);
-    if (rc == IFX_OK) rc = upload_norm(m, x[5], D, &L.ffn_norm);
-    if (rc == IFX_OK) rc = upload_weight(m, x[6], F, D, &L.gate);
-    if (rc == IFX_OK) rc = upload_weight(m, x[7], F, D, &L.up);
-    if (rc == IFX_OK) rc = upload_weight(m, x[8], D, F, &L.down);
+    const int64_t* x = &plan.layers[l * R_COUNT];
+    auto mat = [&](int r, ifx_tensor** t) { return upload_weight(m, x[r], shapes[r][0], shapes[r][1], t); };
+    if (rc == IFX_OK) rc = upload_norm(m, x[R_ATTN_NORM], D, &L.attn_norm);
+    if (rc == IFX_OK) rc = mat(R_Q, &L.q);
+    if (rc == IFX_OK) rc = mat(R_K, &L.k);
+    if (rc == IFX_OK) rc = mat(R_V, &L.v);
+    if (rc == IFX_OK) rc = mat(R_O, &L.o);
+    if (rc == IFX_OK) rc = upload_norm(m, x[R_FFN_NORM], D, &L.ffn_norm);
+    if (rc == IFX_OK) rc = mat(R_GATE, &L.gate);
+    if (rc == IFX_OK) rc = mat(R_UP, &L.up);
+    if (rc == IFX_OK) rc = mat(R_DOWN, &L.down);
     if (rc == IFX_OK && (L.q->L.type != L.k->L.type || L.gate->L.type != L.up->L.type))
       rc = set_error(IFX_E_INVALID_ARG, "layer %llu: attn_q/attn_k or ffn_gate/ffn_up types differ",
                      (unsigned long long)l);

@@ -4,7 +4,9 @@
 // built with g++ -fsanitize=address by tests/test_asan_parsers.py.
 //
 // Arguments: g:<path> parses a GGUF file and walks its metadata and tensor
-// byte ranges; t:<path> loads a tokenizer.json and round-trips a sample text.
+// byte ranges; m:<path> parses it and runs the model loader's host half
+// (host_config.cpp: Config::from_gguf, the blk.N name walk, the weight shape
+// plan); t:<path> loads a tokenizer.json and round-trips a sample text.
 // Prints one status per argument, in order.
 #include <stdio.h>
 #include <string.h>
@@ -12,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "../../inferox_amd/csrc/host_config.h"
 #include "../../inferox_amd/csrc/host_gguf.h"
 #include "../../inferox_amd/csrc/ifx_common.h"
 
@@ -42,6 +45,29 @@ static int run_gguf(const char* path) {
   return sum == 0xffffffffffffffffull ? -1 : IFX_OK;
 }
 
+static int run_model_plan(const char* path) {
+  ifx::MappedFile m;
+  int rc = m.open(path);
+  if (rc != IFX_OK) return rc;
+  ifx::GgufFile f;
+  rc = ifx::gguf_parse(m.data, m.size, &f);
+  if (rc != IFX_OK) return rc;
+  ifx::ModelPlan plan;
+  rc = ifx::plan_model(f, &plan);
+  if (rc != IFX_OK) return rc;
+  uint64_t shapes[ifx::R_COUNT][2];
+  rc = ifx::plan_shapes(f, &plan, shapes);
+  if (rc != IFX_OK) return rc;
+  // every resolved tensor's bytes, as the upload reads them
+  unsigned long long sum = 0;
+  for (int64_t i : plan.layers) {
+    const uint8_t* data;
+    uint64_t n;
+    if (ifx::gguf_tensor_bytes(f, m, i, &data, &n) == IFX_OK && n) sum += data[0] + data[n - 1];
+  }
+  return sum == 0xffffffffffffffffull ? -1 : IFX_OK;
+}
+
 static int run_tokenizer(const char* path) {
   ifx_tokenizer* t = nullptr;
   int rc = ifx_tokenizer_from_file(path, &t);
@@ -65,6 +91,7 @@ int main(int argc, char** argv) {
     const char* a = argv[i];
     int rc = -1;
     if (!strncmp(a, "g:", 2)) rc = run_gguf(a + 2);
+    else if (!strncmp(a, "m:", 2)) rc = run_model_plan(a + 2);
     else if (!strncmp(a, "t:", 2)) rc = run_tokenizer(a + 2);
     printf("%d\n", rc);
   }

@@ -1,7 +1,10 @@
 """AddressSanitizer (+ UndefinedBehaviorSanitizer) run of the product's
 untrusted-input parsers on the CPU: the GGUF reader (host_gguf.cpp, with the
-type tables of host_types.cpp; counterpart of src/gguf/file.rs:57-116) and the
-tokenizer.json reader + BPE (host_tokenizer.cpp; src/tokenizer/mod.rs:61-226).
+type tables of host_types.cpp; counterpart of src/gguf/file.rs:57-116), the
+model loader's host half (host_config.cpp: Config::from_gguf,
+src/model/config.rs:34-84, and the weight resolution of Model::open,
+src/model/mod.rs:34-92) and the tokenizer.json reader + BPE
+(host_tokenizer.cpp; src/tokenizer/mod.rs:61-226).
 
 tests/asan/parse_driver.cpp is compiled with g++ -fsanitize=address,undefined
 together with those three sources and fed: the malformed GGUF files of the
@@ -42,6 +45,7 @@ def driver(tmp_path_factory):
     cmd = [gxx, "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
            "-fno-sanitize-recover=undefined", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
            os.path.join(ROOT, "tests", "asan", "parse_driver.cpp"), os.path.join(CSRC, "host_gguf.cpp"),
+           os.path.join(CSRC, "host_config.cpp"),
            os.path.join(CSRC, "host_types.cpp"), os.path.join(CSRC, "host_tokenizer.cpp"), "-o", out]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
@@ -150,3 +154,73 @@ def test_tokenizer_reader_under_asan(driver, tmp_path):
     want = [_python_status(t) for t in cases]
     assert got == want
     assert got[0] == 0 and got[1] == 0
+
+
+def _llama(path, *, block_count=1, dim=64, heads=4, kv_heads=None, ffn=128, key_length=None, skip=(),
+           shapes=None):
+    """A small llama GGUF with one block's tensors (F32 zeros) and chosen metadata."""
+    from inferox_amd.gguf_writer import GGUFWriter
+    w = GGUFWriter()
+    w.add_string("general.architecture", "llama")
+    w.add_u32("llama.vocab_size", 16).add_u64("llama.embedding_length", dim)
+    w.add_u64("llama.block_count", block_count).add_u64("llama.attention.head_count", heads)
+    if kv_heads is not None:
+        w.add_u32("llama.attention.head_count_kv", kv_heads)
+    if key_length is not None:
+        w.add_u32("llama.attention.key_length", key_length)
+    w.add_u64("llama.feed_forward_length", ffn)
+    d, f, kv = min(dim, 64), min(ffn, 128), min(dim, 64)  # the tensors stay small whatever the metadata says
+    base = {"token_embd.weight": [d, 16], "output_norm.weight": [d], "blk.0.attn_norm.weight": [d],
+            "blk.0.attn_q.weight": [d, d], "blk.0.attn_k.weight": [d, kv], "blk.0.attn_v.weight": [d, kv],
+            "blk.0.attn_output.weight": [d, d], "blk.0.ffn_norm.weight": [d],
+            "blk.0.ffn_gate.weight": [d, f], "blk.0.ffn_up.weight": [d, f], "blk.0.ffn_down.weight": [f, d]}
+    base.update(shapes or {})
+    for name, shape in base.items():
+        if name in skip:
+            continue
+        n = int(np.prod(shape))
+        w.tensor_f32(name, shape, [0.0] * n)
+    w.write(path)
+    return path
+
+
+def test_asan_model_loader(driver, tmp_path):
+    """The loader's host half on valid and hostile metadata: wrapping and huge
+    block counts end at the first missing blk.N tensor (TensorNotFound),
+    dimensions whose products overflow or do not match the tensors are
+    InvalidArg, missing tensors TensorNotFound; nothing is sized from a count."""
+    T = str(tmp_path)
+    cases = [
+        (_llama(T + "/ok.gguf"), 0),
+        (_llama(T + "/wrap.gguf", block_count=2049638230412172402), 9),
+        (_llama(T + "/huge_blocks.gguf", block_count=(1 << 64) - 1), 9),
+        (_llama(T + "/two_blocks.gguf", block_count=2), 9),
+        (_llama(T + "/heads0.gguf", heads=0), 20),
+        (_llama(T + "/huge_dim.gguf", dim=1 << 62), 20),
+        (_llama(T + "/huge_ffn.gguf", ffn=(1 << 63) + 64), 20),
+        (_llama(T + "/huge_kv.gguf", kv_heads=0xFFFFFFFF, key_length=0xFFFFFFFF), 20),
+        (_llama(T + "/no_v.gguf", skip=("blk.0.attn_v.weight",)), 9),
+        (_llama(T + "/no_onorm.gguf", skip=("output_norm.weight",)), 9),
+        (_llama(T + "/no_embd.gguf", skip=("token_embd.weight",)), 9),
+        (_llama(T + "/untied.gguf", shapes={"output.weight": [64, 16]}), 0),
+        (_llama(T + "/bad_output.gguf", shapes={"output.weight": [63, 16]}), 20),
+        (_llama(T + "/bad_q.gguf", shapes={"blk.0.attn_q.weight": [64, 63]}), 20),
+        (_llama(T + "/bad_embd.gguf", shapes={"token_embd.weight": [63, 16]}), 20),
+        (_llama(T + "/bad_norm.gguf", shapes={"blk.0.ffn_norm.weight": [65]}), 20),
+        (_llama(T + "/bad_down.gguf", shapes={"blk.0.ffn_down.weight": [128, 63]}), 20),
+    ]
+    got = _run(driver, ["m:" + p for p, _ in cases])
+    assert got == [e for _, e in cases], list(zip([os.path.basename(p) for p, _ in cases], got))
+    # the regular build reports the same statuses for what it decides before any device work
+    for (p, e), g in zip(cases, got):
+        if e == 9:
+            assert _native_open_status(p) == 9, p
+
+
+def _native_open_status(path):
+    import ctypes as C
+    h = C.c_void_p()
+    rc = _native.lib().ifx_model_open(path.encode(), C.byref(h))
+    if rc == 0:
+        _native.lib().ifx_model_close(h)
+    return rc

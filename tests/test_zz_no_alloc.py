@@ -6,7 +6,9 @@ compared with ifx_matmul_qt on the same operands: every element within
 1e-5 * sum_k |a||w| of it (the two may split K differently, so the partial
 sums can be added in another order; with the same split they are equal) and
 rows at 1e-5 relative L2; a shape past the fixed scratch is refused with
-IFX_E_INVALID_ARG; one-row calls take the GEMV as ifx_matmul_qt does.
+IFX_E_INVALID_ARG; one-row calls, and several rows against a matrix the GEMM
+does not take (F32, F16, Q8_K), take the GEMV row by row as ifx_matmul_qt
+does, with the same bits.
 """
 from __future__ import annotations
 
@@ -78,3 +80,33 @@ def test_noalloc_limits_and_gemv_rows():
     assert _native.lib().ifx_matmul_qt(dx.ptr, 1, w.h, y1.ptr, None) == 0
     assert _fn()(dx.ptr, 1, w.h, y2.ptr, None) == 0
     np.testing.assert_array_equal(y1.get(np.float32, 256), y2.get(np.float32, 256))
+
+
+@pytest.mark.parametrize("t", [0, 1, 15])  # F32, F16, Q8_K: no GEMM operand form
+def test_noalloc_gemv_rows_for_other_types(t):
+    """m = 3 against a matrix the GEMM does not take: the row-by-row GEMV of
+    both entry points, bit for bit."""
+    rows, cols, m = 160, 1024, 3
+    rng = np.random.default_rng(40 + t)
+    if t == 0:
+        raw = rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+    elif t == 1:
+        raw = (0.05 * rng.standard_normal(rows * cols)).astype("<f2").view(np.uint8)
+    else:
+        nb = rows * cols // 256
+        raw = rng.integers(0, 256, size=(nb, 292), dtype=np.uint8)
+        raw[:, :4] = rng.uniform(1e-3, 1e-2, (nb, 2)).astype("<f2").view(np.uint8).reshape(nb, 4)
+        raw = raw.reshape(-1)
+    w = Tensor(t, raw, rows, cols)
+    a = rng.standard_normal((m, cols)).astype(np.float32)
+    da, y1, y2 = Dev.of(a), Dev(4 * m * rows), Dev(4 * m * rows)
+    assert _native.lib().ifx_matmul_qt(da.ptr, m, w.h, y1.ptr, None) == 0
+    assert _fn()(da.ptr, m, w.h, y2.ptr, None) == 0
+    ref, got = y1.get(np.float32, m * rows), y2.get(np.float32, m * rows)
+    assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+    # and the rows are the product, to the GEMV bar
+    from oracle import numpy_ref
+    wf = numpy_ref.dequant(t, raw).reshape(rows, cols).astype(np.float64)
+    want = a.astype(np.float64) @ wf.T
+    bound = np.abs(a).astype(np.float64) @ np.abs(wf).T
+    assert np.all(np.abs(got.reshape(m, rows) - want) <= 1e-5 * bound)
