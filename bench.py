@@ -9,8 +9,9 @@ a 2048-token KV context filled by a GPU prefill of 2048 seeded token ids, then
 in HBM when timing starts).
 
 Prints ONE JSON line (metric, value, roofline of the dominant kernel measured
-with HIP events over back-to-back launches, cpu_baseline of the CPU oracle on a
-bounded sample).  `value` uses the f32 KV cache (the reference's; --kv f16
+with HIP events around back-to-back launches, with the same kernel timed by
+event pairs around each launch of directly launched steps carried beside it;
+cpu_baseline of the CPU oracle on a bounded sample).  `value` uses the f32 KV cache (the reference's; --kv f16
 switches); `other_kv_cache` times the same decode with the other cache type,
 reported apart from `value`.
 
@@ -76,6 +77,10 @@ def parse():
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
     ap.add_argument("--prefill-reps", type=int, default=3)
     ap.add_argument("--prefill-sizes", default="512,2048", help="prompt lengths of the prefill measurement")
+    ap.add_argument("--lite", action="store_true",
+                    help="decode, its profile and the CPU baseline only (no other-KV run, no prefill sizes)")
+    ap.add_argument("--no-70b", action="store_true",
+                    help="skip the 70B-shape run the default 8B line carries as model_70b")
     args = ap.parse_args()
     big = args.model == "70b"
     args.steps = args.steps if args.steps is not None else (128 if big else 256)
@@ -344,6 +349,37 @@ def cpu_baseline(model_path, kv_k, kv_v, ctx, token, n_steps):
     return med, toks
 
 
+def run_70b(args):
+    """The 70B-shape workload (8192-token context from a GPU prefill, then 128
+    greedy tokens, f32 KV, one faithful CPU step from the same state) in a
+    child process of this script, when the scratch space holds its 45 GB
+    model; its JSON line, or why it was skipped."""
+    import shutil
+    import subprocess
+    from inferox_amd import synth
+    spec = synth.LLAMA3_70B
+    path = os.path.join(args.model_dir, f"{spec.name}-seed1234.gguf")
+    have = os.path.exists(path) and os.path.getsize(path) >= spec.gguf_bytes()
+    free = shutil.disk_usage(args.model_dir).free
+    if not have and free < spec.gguf_bytes() + (4 << 30):
+        return {"skipped": f"the 70B model needs {spec.gguf_bytes() / 1e9:.1f} GB of scratch space; "
+                           f"{free / 1e9:.1f} GB free in {args.model_dir}"}
+    cmd = [sys.executable, os.path.abspath(__file__), "--model", "70b", "--steps", "128", "--warmup", "8",
+           "--cpu-steps", "1", "--no-micro", "--lite", "--model-dir", args.model_dir]
+    log("70B-shape run: " + " ".join(cmd[1:]))
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=1200)
+    except subprocess.TimeoutExpired:
+        return {"skipped": "the 70B-shape run did not finish in 1200 s"}
+    lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"skipped": f"the 70B-shape run failed (exit {r.returncode})"}
+    d = json.loads(lines[-1])
+    keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "dtype", "config", "roofline",
+            "roofline_tok", "device_tok_s", "prefill_tok_s", "cpu_baseline", "kernels")
+    return {k: d.get(k) for k in keep}
+
+
 def main():
     args = parse()
     if args.no_graph:
@@ -395,7 +431,7 @@ def main():
         return
 
     K, W = args.steps, args.warmup
-    max_seq = args.ctx + max(K, W) + args.profile_steps + 8
+    max_seq = args.ctx + max(K, W) + 2 * args.profile_steps + 8
     sess = C.c_void_p()
     check(L.ifx_session_create_kv(model, max_seq, 1 if args.kv == "f16" else 0, C.byref(sess)), "session_create")
     vocab = spec.vocab
@@ -445,14 +481,22 @@ def main():
     b_tok = w_bytes + kv_bytes
     frac_tok = tok_s * b_tok / HBM_PEAK
 
-    # ---- dominant kernel: HIP events around back-to-back launches of each kernel class ----
+    # ---- dominant kernel: HIP events around each launch of directly launched
+    # steps (step order: each kernel meets the cache state of a real step), and
+    # around back-to-back launches of each class (reported beside it) ----
     roofline = None
     prof = {}
     if not args.no_profile:
         avg = (C.c_float * 8)()
+        ordered = (C.c_float * 8)()
         launches = (C.c_uint64 * 8)()
         wbytes = (C.c_uint64 * 8)()
+        check(L.ifx_session_profile_ordered(sess, int(out[K - 1]), args.profile_steps, ordered), "profile_ordered")
         check(L.ifx_session_profile(sess, int(out[K - 1]), args.profile_steps, avg, launches, wbytes), "profile")
+        # avg: back-to-back launches of one class (kernel + the launch gap);
+        # ordered (step order): an event pair around each launch, which adds the
+        # events' own ~2 us per launch -- the two bracket the kernel's duration
+        # inside the replayed step graph (rocprofv3 trace in profiles/)
         per_step = {KCLASS[k]: avg[k] * launches[k] for k in range(8)}
         dom = max(range(8), key=lambda k: avg[k] * launches[k])
         # algorithmic bytes of one launch of the dominant kernel: its weight bytes
@@ -468,12 +512,17 @@ def main():
                                        "scaled by a copy of known size (profiles/traffic.json; counters cannot run "
                                        "inside this process)") if args.model == "8b" else None,
                     "kernel": KERNEL_NAMES.get(dom, KCLASS[dom]), "kernel_class": KCLASS[dom],
-                    "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2)}
-        prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "launches_per_step": int(launches[k]),
+                    "bytes_per_launch": int(alg), "avg_launch_us": round(avg[dom] * 1e3, 2),
+                    "avg_launch_us_timing": "HIP events around 32 x profile_steps back-to-back launches on the "
+                                            "session stream",
+                    "avg_launch_us_step_order": round(ordered[dom] * 1e3, 2),
+                    "frac_step_order": round(alg / (ordered[dom] * 1e-3) / HBM_PEAK, 4) if ordered[dom] else None}
+        prof = {KCLASS[k]: {"avg_us": round(avg[k] * 1e3, 2), "step_order_us": round(ordered[k] * 1e3, 2),
+                            "launches_per_step": int(launches[k]),
                             "weight_bytes": int(wbytes[k]),
                             "GB_s": round(wbytes[k] / (avg[k] * 1e-3) / 1e9, 1) if avg[k] > 0 and wbytes[k] else None}
                 for k in range(8)}
-        log("per-kernel (back-to-back launches): " + json.dumps(prof))
+        log("per-kernel (back-to-back; step order with its event pairs beside): " + json.dumps(prof))
         log(f"sum of kernel time per step: {sum(per_step.values()):.3f} ms vs {wall / K * 1e3:.3f} ms per step")
 
     cpu = None
@@ -481,7 +530,7 @@ def main():
         log(f"cpu baseline: {args.cpu_steps} faithful oracle step(s) at ctx {args.ctx}, 1 thread ...")
         med, toks = cpu_baseline(path, kv_k, kv_v, args.ctx, start_tok, args.cpu_steps)
         cpu = {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-               "sample": f"{args.cpu_steps} decode step(s) of the same 8B model from the same {args.ctx}-row KV "
+               "sample": f"{args.cpu_steps} decode step(s) of the same {args.model.upper()} model from the same {args.ctx}-row KV "
                          f"state, faithful CPU restatement (per-step full dequant, AVX2 matmul_t), median "
                          f"{med:.2f} s/step; greedy picks {toks} vs GPU {[int(v) for v in out[:len(toks)]]}",
                "host": host_cpu()}
@@ -489,16 +538,19 @@ def main():
 
     L.ifx_session_destroy(sess)
     other_kv = None
-    if not args.no_profile:
+    if not args.no_profile and not args.lite:
         other_kv = measure_other_kv(L, model, spec, 0 if args.kv == "f16" else 1, args.ctx, K, W)
         log(f"decode with the {other_kv['kv_cache']} KV cache: {other_kv['tok_s']} tok/s")
-    prefill = None if args.no_profile else measure_prefill(
+    prefill = None if (args.no_profile or args.lite) else measure_prefill(
         L, model, spec, [int(x) for x in args.prefill_sizes.split(",")], 1)
     L.ifx_model_close(model)
     micro = tiny = None
     if not args.no_micro and args.model == "8b":
         micro = gemv_microbench(L)
         tiny = tiny_run(L, args.model_dir, cpu=do_cpu)
+    model_70b = None
+    if args.model == "8b" and not args.no_70b and not args.no_profile:
+        model_70b = run_70b(args)
 
     line = {
         "metric": METRIC if args.model == "8b" else METRIC.replace("8B", "70B"), "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -519,6 +571,7 @@ def main():
         "kernels": prof or None,
         "gemv_microbench": micro,
         "tiny": tiny,
+        "model_70b": model_70b,
     }
     print(json.dumps(line), flush=True)
 

@@ -235,6 +235,14 @@ int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms);
 int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms,
                         uint64_t* launches, uint64_t* bytes);
 
+/* Measurement hook (no reference counterpart): n_steps greedy decode steps
+ * from `token`, each launched kernel by kernel with a HIP event pair around
+ * every launch, so each kernel is timed in the order and cache state of a real
+ * step (the captured step replays the same launches with no events between
+ * them).  avg_ms[8]: the mean duration of one launch of each kernel class of
+ * ifx_session_profile (class 7, finalize, is timed too).  len grows by n_steps. */
+int ifx_session_profile_ordered(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms);
+
 /* ---------------------------------------------------------------------------
  * Device memory and streams (plumbing for the kernel-level entry points)
  * ------------------------------------------------------------------------- */

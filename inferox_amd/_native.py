@@ -66,6 +66,7 @@ SIGNATURES = {
     "ifx_session_last_elapsed_ms": (i32, [vp, P(f32)]),
     "ifx_session_last_token": (i32, [vp, P(u32)]),
     "ifx_session_profile": (i32, [vp, u32, u64, P(f32), P(u64), P(u64)]),
+    "ifx_session_profile_ordered": (i32, [vp, u32, u64, P(f32)]),
     "ifx_device_info": (i32, [cp, u64, P(i32), P(u64)]),
     "ifx_malloc": (i32, [P(vp), u64]),
     "ifx_free": (i32, [vp]),

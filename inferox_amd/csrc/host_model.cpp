@@ -1154,6 +1154,53 @@ int ifx_session_profile(ifx_session* s, uint32_t token, uint64_t n_steps, float*
   return IFX_OK;
 }
 
+int ifx_session_profile_ordered(ifx_session* s, uint32_t token, uint64_t n_steps, float* avg_ms) {
+  clear_error();
+  if (!s || !avg_ms || n_steps == 0) return set_error(IFX_E_INVALID_ARG, "bad arguments");
+  ifx_model* m = s->m;
+  if (token >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "token");
+  IFX_TRY(check_vocab(m));
+  if (s->len + n_steps > s->max_seq) return set_error(IFX_E_KV_FULL, "profile steps overflow the KV cache");
+  const size_t NL = m->layers.size();
+  // the launches of one step, in step order: class 0, classes 1..5 per layer, 6, 7
+  std::vector<std::pair<int, size_t>> seq;
+  seq.emplace_back(0, 0);
+  for (size_t l = 0; l < NL; l++)
+    for (int k = 1; k <= 5; k++) seq.emplace_back(k, l);
+  seq.emplace_back(6, 0);
+  seq.emplace_back(7, 0);
+  std::vector<hipEvent_t> ev(2 * seq.size(), nullptr);
+  int rc = IFX_OK;
+  for (hipEvent_t& e : ev)
+    if (rc == IFX_OK && hipEventCreate(&e) != hipSuccess) rc = set_error(IFX_E_HIP, "hipEventCreate failed");
+  double sum[kClasses] = {};
+  uint64_t cnt[kClasses] = {};
+  if (rc == IFX_OK) rc = state_op(s, STATE_DECODE, token, 0);
+  for (uint64_t i = 0; i < n_steps && rc == IFX_OK; i++) {
+    choose_merge(s, s->len + i + 1);  // the bound the step graph would take for this token
+    for (size_t j = 0; j < seq.size() && rc == IFX_OK; j++) {
+      if (hipEventRecord(ev[2 * j], s->stream) != hipSuccess) rc = set_error(IFX_E_HIP, "hipEventRecord failed");
+      if (rc == IFX_OK) rc = enqueue_class(s, seq[j].first, seq[j].second);
+      if (rc == IFX_OK && hipEventRecord(ev[2 * j + 1], s->stream) != hipSuccess)
+        rc = set_error(IFX_E_HIP, "hipEventRecord failed");
+    }
+    if (rc == IFX_OK && hipStreamSynchronize(s->stream) != hipSuccess) rc = set_error(IFX_E_HIP, "sync failed");
+    for (size_t j = 0; j < seq.size() && rc == IFX_OK; j++) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, ev[2 * j], ev[2 * j + 1]) != hipSuccess) rc = set_error(IFX_E_HIP, "event time");
+      sum[seq[j].first] += ms;
+      cnt[seq[j].first] += 1;
+    }
+    s->steps++;
+  }
+  if (rc == IFX_OK) s->len += n_steps;
+  for (hipEvent_t e : ev)
+    if (e) (void)hipEventDestroy(e);
+  if (rc != IFX_OK) return rc;
+  for (int k = 0; k < kClasses; k++) avg_ms[k] = cnt[k] ? (float)(sum[k] / (double)cnt[k]) : 0.f;
+  return IFX_OK;
+}
+
 int ifx_session_last_token(ifx_session* s, uint32_t* token) {
   if (!s || !token) return set_error(IFX_E_INVALID_ARG, "null argument");
   IFX_HIP(hipStreamSynchronize(s->stream));
