@@ -71,6 +71,9 @@ constexpr size_t kMaxDynLds = 156 * 1024;
 struct MArgs {
   GemvSeg seg[3];      // paired: seg[0] gate, seg[1] up
   uint32_t ntiles[3];  // 16-row tiles per logical segment
+  // Items per segment: items below half0 are whole tiles; item half0 + 2i + h
+  // is half h (8 rows) of tile half0 + i, up to nitems (= ntiles: no halves)
+  uint32_t half0[3], nitems[3];
   uint32_t rot[3];     // first-group rotation per segment (balances small segments)
   uint32_t use_b;      // bit s: segment s has the kernel's second type
   uint32_t split;      // waves per item: 1, 2, 4 or 8
@@ -394,15 +397,38 @@ struct NtLoads<EpiQkv> {
   static constexpr bool value = false;
 };
 
+// Item v of segment s: its tile, and hl = 0 (the whole tile) or 1 + h (rows
+// 8h..8h+7 of it).  A half item runs the whole tile's code with lane n + 16g
+// reading row 8h + (n & 7): lanes n and n + 8 load the same bytes and compute
+// the same sum, lanes 0..7 emit it.  Half items split the last round of a
+// launch whose items do not fill it, so that every workgroup streams in it.
+struct Item {
+  uint32_t tile, hl;
+  __device__ __forceinline__ Item(const MArgs& a, int s, uint32_t v) {
+    const uint32_t h0 = a.half0[s];
+    tile = v < h0 ? v : h0 + ((v - h0) >> 1);
+    hl = v < h0 ? 0u : 1u + ((v - h0) & 1u);
+  }
+  // the lane index the unit loads use
+  __device__ __forceinline__ uint32_t lane_of(uint32_t lane) const {
+    return hl ? (lane & 0x37u) + 8u * (hl - 1u) : lane;
+  }
+  // the row lane (< 16) emits, and whether it emits
+  __device__ __forceinline__ uint32_t row(uint32_t lane) const {
+    return tile * (uint32_t)kTileRows + lane_of(lane & 15u);
+  }
+  __device__ __forceinline__ bool emits(uint32_t lane) const { return lane < (hl ? 8u : 16u); }
+};
+
 template <class Epi, int NT>
-__device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, const MArgs& a, int s, uint32_t tile,
+__device__ __forceinline__ void emit(const Epi& epi, typename Epi::Wave& ws, const MArgs& a, int s, const Item& it,
                                      const float* acc, const typename Epi::Pre& pre, int lane) {
   const float v = acc[0];
   float partner = 0.f;
   if (Epi::kPaired) partner = acc[NT - 1];
   else if (Epi::kNeighbor) partner = lane_xor1(v);
-  const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
-  if (lane < 16 && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner, pre);
+  const uint32_t r = it.row((uint32_t)lane);
+  if (it.emits((uint32_t)lane) && r < a.seg[s].rows) epi.row(ws, Epi::kPaired ? 0 : s, r, v, partner, pre);
 }
 
 // The items of segment s owned by this wave's group (a.split waves of one
@@ -415,17 +441,18 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
                                         KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t TG, uint32_t iters,
                                         uint32_t j, const uint8_t* lds, uint32_t a_base, uint32_t a_step,
                                         float* part, float nscale, int lane, int wave) {
-  const uint32_t S = a.split, NB = a.steps, nbr = a.nbr, nt = a.ntiles[s];
+  const uint32_t S = a.split, NB = a.steps, nbr = a.nbr, nt = a.nitems[s];
   const int g = lane >> 4;
   const float4* xsum = (const float4*)(lds + a.xs_off) + g;
   for (uint32_t k = 0; k < iters; k++) {
-    const uint32_t tile = first + k * TG;
-    const bool live = tile < nt;  // uniform over the wave
+    const uint32_t item = first + k * TG;
+    const bool live = item < nt;  // uniform over the wave
+    const Item it(a, s, item);
     // the epilogue's global reads, in flight while the item is decoded
     typename Epi::Pre pre{};
     {
-      const uint32_t r = tile * (uint32_t)kTileRows + (uint32_t)(lane & 15);
-      if (live && lane < 16 && r < a.seg[s].rows) pre = epi.pre(ws, Epi::kPaired ? 0 : s, r);
+      const uint32_t r = it.row((uint32_t)lane);
+      if (live && it.emits((uint32_t)lane) && r < a.seg[s].rows) pre = epi.pre(ws, Epi::kPaired ? 0 : s, r);
     }
     float acc[NT];
 #pragma unroll
@@ -449,18 +476,18 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
         // Past the wave's last item the (unused) refill reads the segment's
         // first unit, which every such refill on the XCD shares: an L2 hit,
         // so the wave does not wait an HBM round trip for it before it ends.
-        uint32_t nm = m + D, ntl = tile;
+        uint32_t nm = m + D, nit = item;
         if (nm >= NB) {
           nm -= NB;
-          ntl += TG;
+          nit += TG;
         }
-        const bool past = ntl >= nt;
+        const bool past = nit >= nt;
         const uint32_t nb = past ? 0u : min(j + S * nm, nbr - 1);
-        ntl = past ? 0u : ntl;
+        const Item nx(a, s, past ? 0u : nit);
 #pragma unroll
         for (int t = 0; t < NT; t++)
-          buf[i][t].template load<NtLoads<Epi>::value>(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, ntl, nb), lane,
-                                                       a.seg[NT == 2 ? t : s].q6_signed);
+          buf[i][t].template load<NtLoads<Epi>::value>(unit_ptr<T>(a.seg[NT == 2 ? t : s], nbr, nx.tile, nb),
+                                                       nx.lane_of((uint32_t)lane), a.seg[NT == 2 ? t : s].q6_signed);
         // keep the ring order: the next block's decode may not be hoisted above
         // these loads (it would wait for every buffer at once)
         __builtin_amdgcn_sched_barrier(0);
@@ -486,12 +513,12 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
           for (uint32_t q = 0; q < S; q++) v += pb[((wave + q) * NT + t) * 16 + (lane & 15)];
           acc[t] = v * nscale;
         }
-        emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
+        emit<Epi, NT>(epi, ws, a, s, it, acc, pre, lane);
       }
     } else if (live) {
 #pragma unroll
       for (int t = 0; t < NT; t++) acc[t] *= nscale;
-      emit<Epi, NT>(epi, ws, a, s, tile, acc, pre, lane);
+      emit<Epi, NT>(epi, ws, a, s, it, acc, pre, lane);
     }
   }
 }
@@ -500,14 +527,14 @@ __device__ __forceinline__ void run_seg(const MArgs& a, const Epi& epi, typename
 template <int T, int NT, int D, bool NTL>
 __device__ __forceinline__ void prefetch(const MArgs& a, int s, KBuf<T> (&buf)[D][NT], uint32_t first, uint32_t j,
                                          int lane, int i0 = 0, int i1 = D) {
-  const uint32_t tile = min(first, a.ntiles[s] - 1);
+  const Item it(a, s, min(first, a.nitems[s] - 1));
 #pragma unroll
   for (int i = 0; i < D; i++) {
     if (i < i0 || i >= i1) continue;
     const uint32_t b = min(j + a.split * i, a.nbr - 1);
 #pragma unroll
     for (int t = 0; t < NT; t++)
-      buf[i][t].template load<NTL>(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, tile, b), lane,
+      buf[i][t].template load<NTL>(unit_ptr<T>(a.seg[NT == 2 ? t : s], a.nbr, it.tile, b), it.lane_of((uint32_t)lane),
                                    a.seg[NT == 2 ? t : s].q6_signed);
     // issue the slots in ring order: the loop's waits assume slot i is older
     // than slot i + 1 on every path into it (reordered prefetches made each
@@ -560,7 +587,7 @@ __global__ void __launch_bounds__(kThreads, kWavesPerSimd) k_gemv_mfma(MArgs a, 
     uint32_t n = 0;
     for (uint32_t q = 0; q < GPB; q++) {
       const uint32_t f0 = (blockIdx.x * GPB + q + TG - a.rot[s]) % TG;
-      if (f0 < a.ntiles[s]) n = max(n, (a.ntiles[s] - 1 - f0) / TG + 1);
+      if (f0 < a.nitems[s]) n = max(n, (a.nitems[s] - 1 - f0) / TG + 1);
     }
     return n;
   };
@@ -1163,6 +1190,20 @@ hipError_t launch_mfma(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
   for (int s = 0; s < a.nseg; s++) {
     a.rot[s] = acc % TG;
     acc += a.ntiles[s];
+  }
+  // Half items in the last round of a one-segment launch whose tiles leave
+  // it at most half full (8B gate/up: 896 tile pairs on 256 groups, so that
+  // 128 workgroups streamed a fourth pair while the other CUs idled; now
+  // every workgroup takes three pairs and a half.  The head: 8016 tiles,
+  // 31 rounds and 160 halves).  IFX_GEMV_HALVES=0 keeps whole tiles.
+  for (int s = 0; s < 3; s++) a.half0[s] = a.nitems[s] = a.ntiles[s];
+  const char* hv = getenv("IFX_GEMV_HALVES");
+  if (!(hv && hv[0] == '0' && hv[1] == 0) && a.nseg == 1) {
+    const uint32_t nt = a.ntiles[0], rounds = nt / TG, rest = nt % TG;
+    if (rounds >= 1 && rest > 0 && 2 * rest <= TG) {
+      a.half0[0] = rounds * TG;
+      a.nitems[0] = rounds * TG + 2 * rest;
+    }
   }
   // One tile per workgroup on more workgroups than CUs (the mixed QKV launch:
   // 384 on 256): workgroup i shares a CU with workgroup i + CUs, and those

@@ -234,12 +234,13 @@ def test_deterministic_mode_reruns_bit_identical(tmpdir_session):
 
 @pytest.mark.parametrize("env", [{"IFX_KS_LOCK": "0"}, {"IFX_QKV_KS": "0"}, {"IFX_QKV_KS": "0", "IFX_QKV_PLACE": "0"},
                                  {"IFX_ATTN_HKF": "0"}, {"IFX_ATTN_HKF": "1"}, {"IFX_MERGE_O": "0"},
-                                 {"IFX_MERGE_O": "1"}])
+                                 {"IFX_MERGE_O": "1"}, {"IFX_GEMV_HALVES": "0"}])
 def test_centred_launch_variants(tmpdir_session, monkeypatch, env):
     """The launch variants the IFX_* switches select: each wave of the K-split
     residual launch on its own, the tiled q/k/v launch on the f32 cache (with
     and without its placement of the Q6_K tiles), both attention grid orders,
-    and each merge form forced."""
+    each merge form forced, and the gate/up and head launches on whole tiles
+    only (no half tiles in their last round)."""
     for key, val in env.items():
         monkeypatch.setenv(key, val)
     p = _model(tmpdir_session, "c8b_2l.gguf", C8B, 88)

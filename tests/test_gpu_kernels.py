@@ -148,6 +148,30 @@ def test_gemv_microbench_shapes(rows, cols, t):
     assert rel_l2(y, ref) < 1e-5
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_gemv_half_tiles_in_last_round(t, monkeypatch):
+    """5691 rows (356 tiles, the last with 11 rows) on 256 workgroups: one
+    round of whole tiles, then 200 half tiles. Every row within the oracle's
+    bound, and the same bits as the launch on whole tiles only
+    (IFX_GEMV_HALVES=0): a half tile computes each row from the same unit
+    data and x digits in the same order."""
+    rows, cols = 16 * 356 - 5, 4096
+    rng = np.random.default_rng(356 + t)
+    raw = _raw(t, rows * cols, rng)
+    w = Tensor(t, raw, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    dx, y1, y0 = Dev.of(x), Dev(4 * rows), Dev(4 * rows)
+    assert _native.lib().ifx_gemv(w.h, dx.ptr, y1.ptr, None) == 0
+    monkeypatch.setenv("IFX_GEMV_HALVES", "0")
+    assert _native.lib().ifx_gemv(w.h, dx.ptr, y0.ptr, None) == 0
+    got, whole = y1.get(np.float32, rows), y0.get(np.float32, rows)
+    assert np.array_equal(got.view(np.uint32), whole.view(np.uint32))
+    _, wf = orc.dequantize(t, raw, rows * cols)
+    ref = orc.matmul_t(x, wf, 1, rows, cols)
+    bound = np.abs(wf.reshape(rows, cols)).astype(np.float64) @ np.abs(x).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= 1e-5 * bound + 1e-30)
+
+
 def test_gemv_lm_head_q6k_rows():
     """[128256 x 4096] Q6_K: all rows computed, a seeded sample of 8192 rows checked."""
     rows, cols = 128256, 4096
