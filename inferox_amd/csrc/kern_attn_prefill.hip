@@ -388,21 +388,32 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
     m = mn;
     vref = vnew;
     if (more) load_v(kb + 1);
-    // ---- O^T = V^T P^T: dims 16t + 4fg + r x query fi (one key tile at a time) ----
+    // ---- O^T = V^T P^T: dims 16t + 4fg + r x query fi, 32 keys per MFMA ----
+    // The K = 32 step over keys 32c..32c+31 takes, in lane group fg, the keys
+    // this lane's weights already hold: 32c + 4fg + r (tile 2c) and
+    // 32c + 16 + 4fg + r (tile 2c + 1).  V^T's columns are read in the same
+    // order, so the sum over k is the sum over the 32 keys.
 #pragma unroll
     for (int t = 0; t < NT; t++) o[t] *= oscale;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int c = 0; c < 2; c++) {
+      const h8 p8h = __builtin_shufflevector(ph[2 * c], ph[2 * c + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const h8 p8l = __builtin_shufflevector(pl[2 * c], pl[2 * c + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const int va = 32 * c + 4 * fg, vb = va + 16;
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const int vr = 16 * t + fi, vc = 16 * j + 4 * fg;
-        const h4 vh4 = *(const h4*)&Vh[swzv(vr, vc >> 3) + (vc & 7)];
-        const h4 vl4 = *(const h4*)&Vl[swzv(vr, vc >> 3) + (vc & 7)];
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh4, ph[j], o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh4, pl[j], o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vl4, ph[j], o[t], 0, 0, 0);
+        const int vr = 16 * t + fi;
+        const h4 vha = *(const h4*)&Vh[swzv(vr, va >> 3) + (va & 7)];
+        const h4 vhb = *(const h4*)&Vh[swzv(vr, vb >> 3) + (vb & 7)];
+        const h4 vla = *(const h4*)&Vl[swzv(vr, va >> 3) + (va & 7)];
+        const h4 vlb = *(const h4*)&Vl[swzv(vr, vb >> 3) + (vb & 7)];
+        const h8 vh8 = __builtin_shufflevector(vha, vhb, 0, 1, 2, 3, 4, 5, 6, 7);
+        const h8 vl8 = __builtin_shufflevector(vla, vlb, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh8, p8h, o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh8, p8l, o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl8, p8h, o[t], 0, 0, 0);
+        if (t % 4 == 3) __builtin_amdgcn_sched_barrier(0);  // V fragments of four tiles live at once
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
   if (qt < a.n) {

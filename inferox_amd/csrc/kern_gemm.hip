@@ -479,9 +479,11 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm(GemmArgs a, Ep ep) {
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(dj[j], cs[i][j][r], acc[i][j][r]);
     if constexpr (Q::kMins) {
-      // K = 16: lanes of group g take S_hi (g < 2) or S_lo (g >= 2) of
-      // groups 4 (g & 1) .. + 3 against the hi parts; the second MFMA adds
-      // S_hi against the lo parts
+      // Two K = 16 products: lanes of group g take S_hi (g < 2) or S_lo
+      // (g >= 2) of groups 4 (g & 1) .. + 3 against the hi parts; the second
+      // adds S_hi against the lo parts.  They run as one K = 32 MFMA (a1 a2
+      // against b1 b2 in each lane's 8 k slots: the same sum of products), at
+      // the cost of one K = 16 one on gfx950.
       const h4 z = {0, 0, 0, 0};
       h4 a1[4], a2[4], b1[4], b2[4];
 #pragma unroll
@@ -499,8 +501,9 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm(GemmArgs a, Ep ep) {
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1[i], b1[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2[i], b2[j], acc[i][j], 0, 0, 0);
+          const h8 a = __builtin_shufflevector(a1[i], a2[i], 0, 1, 2, 3, 4, 5, 6, 7);
+          const h8 b = __builtin_shufflevector(b1[j], b2[j], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i][j], 0, 0, 0);
         }
     }
   };
