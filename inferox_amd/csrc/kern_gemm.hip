@@ -603,14 +603,46 @@ __global__ void k_gemm_reduce(GemmArgs a, Ep ep) {
   ep(t, n, v, partner);
 }
 
+// The same sums four outputs (t, 4i .. 4i + 3) per thread, as 16-byte loads
+// (n % 4 == 0): each output's partials are added in the same order, so the
+// bits are those of k_gemm_reduce.  The RoPE partner n ^ 1 is in the same four.
+template <class Ep>
+__global__ void k_gemm_reduce4(GemmArgs a, Ep ep) {
+  const uint32_t n4 = a.n / 4;
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (uint64_t)a.m * n4) return;
+  const uint32_t t = (uint32_t)(idx / n4), n = 4 * (uint32_t)(idx % n4);
+  const uint32_t ncols = EpTraits<Ep>::kPaired ? 2 * a.n : a.n;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f), u = v;
+  for (uint32_t z = 0; z < a.ksplit; z++) {
+    const float* pr = a.part + ((uint64_t)z * a.m + t) * ncols;
+    const float4 x = *(const float4*)(pr + n);
+    v.x += x.x; v.y += x.y; v.z += x.z; v.w += x.w;
+    if (EpTraits<Ep>::kPaired) {
+      const float4 y = *(const float4*)(pr + n + a.n);
+      u.x += y.x; u.y += y.y; u.z += y.z; u.w += y.w;
+    }
+  }
+  if (!EpTraits<Ep>::kPaired && EpTraits<Ep>::kNeighbor) u = make_float4(v.y, v.x, v.w, v.z);
+  ep(t, n, v.x, u.x);
+  ep(t, n + 1, v.y, u.y);
+  ep(t, n + 2, v.z, u.z);
+  ep(t, n + 3, v.w, u.w);
+}
+
 template <int T, class Ep>
 hipError_t go(const GemmArgs& a, const Ep& ep, hipStream_t st) {
   const uint32_t bn = EpTraits<Ep>::kPaired ? kBN / 2 : kBN;
   dim3 grid((a.n + bn - 1) / bn, (a.m + kBM - 1) / kBM, a.ksplit);
   hipLaunchKernelGGL((k_gemm<T, Ep>), grid, dim3(kThreads), 0, st, a, ep);
   if (a.ksplit > 1) {
-    const uint64_t total = (uint64_t)a.m * a.n;
-    hipLaunchKernelGGL((k_gemm_reduce<Ep>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, ep);
+    if (a.n % 4 == 0) {
+      const uint64_t total = (uint64_t)a.m * (a.n / 4);
+      hipLaunchKernelGGL((k_gemm_reduce4<Ep>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, ep);
+    } else {
+      const uint64_t total = (uint64_t)a.m * a.n;
+      hipLaunchKernelGGL((k_gemm_reduce<Ep>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a, ep);
+    }
   }
   return hipGetLastError();
 }
