@@ -25,14 +25,15 @@
 //     registers.  Per 64-key block it copies K and V^T into LDS (the next
 //     block's copies wait in registers meanwhile) and computes the scores
 //     transposed, S^T = K Q^T (16x16x32 MFMAs): lane i + 16g then holds the
-//     scores of query i against keys 16j + 4g + r, which is exactly the
-//     B operand of O^T = V^T P^T on v_mfma_f32_16x16x16_f16 (B[4g + r][i]),
-//     so the softmax weights never leave registers, and the row max and sum
-//     take two shuffles.  64 KB of LDS and one workgroup per CU (two waves
-//     per SIMD): each staged block serves 128 queries.
-// MFMA lane layouts: 16x16x32: lane i + 16g holds A[i][8g..8g+7],
-// B[8g..8g+7][i]; 16x16x16: A[i][4g..4g+3], B[4g..4g+3][i]; both give C[4g + r][i]
-// in lane i + 16g, register r.
+//     scores of query i against keys 16j + 4g + r.  O^T = V^T P^T runs on
+//     the same 16x16x32 MFMA with each 32-key step's k slots 8g..8g+7 taken
+//     as keys 32c + 4g + r and 32c + 16 + 4g + r, the weights lane i + 16g
+//     already holds (V^T's columns read in that order), so the softmax
+//     weights never leave registers, and the row max and sum take two
+//     shuffles.  64 KB of LDS and one workgroup per CU (two waves per SIMD):
+//     each staged block serves 128 queries.
+// MFMA lane layout (16x16x32): lane i + 16g holds A[i][8g..8g+7] and
+// B[8g..8g+7][i], and receives C[4g + r][i] in register r.
 #include "kernels.h"
 
 namespace ifx {

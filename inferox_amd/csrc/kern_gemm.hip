@@ -41,7 +41,6 @@
 // Block scales and the Q4_K min operands go to a per-block side area.
 // MFMA v_mfma_f32_16x16x32_f16: lane i + 16g holds A[i][8g..8g+7] and
 // B[8g..8g+7][i]; C[4g + r][i] arrives in lane i + 16g, register r
-// (16x16x16: A[i][4g..4g+3], B[4g..4g+3][i], the same C).
 #include <algorithm>
 #include <type_traits>
 
