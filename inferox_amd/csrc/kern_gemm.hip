@@ -15,8 +15,9 @@
 //   Q4_0: p = q - 8, s = delta (dequant.rs:62-84).
 // p is an exact fp16 integer, so the MFMAs run on the integers and the block
 // scale is applied in f32 once per block: C = sum_b s[n][b] (sum_{k in b} p[n][k] A[t][k]) - sum_g c[n][g] S[t][g],
-// S[t][g] the group sums of A.  The Q4_K min term is itself a K = 16 MFMA per
-// super-block (8 groups x the hi/lo parts of S against dmin mn, an exact fp16 pair).
+// S[t][g] the group sums of A.  The Q4_K min term is itself one K = 32 MFMA
+// per super-block and tile (8 groups x the hi/lo parts of S against dmin mn,
+// an exact fp16 pair).
 // The activations are carried as fp16 pairs: k_prep_rows scales row t by
 // 2^(14 - e_t) (e_t the exponent of its largest magnitude, |A s| < 2^15) and
 // splits a = a_hi + a_lo; each 16x16x32 step runs a_hi p + a_lo p (Q6_K:
