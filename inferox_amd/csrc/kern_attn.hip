@@ -522,14 +522,14 @@ __global__ void __launch_bounds__(kThreads) k_attn_merge(AttnArgs a) {
 
 // compute units of the current device (looked up once)
 int attn_cu_count() {
-  static int n = 0;
-  if (n == 0) {
+  // initialised once, thread-safe (sessions may run on several threads)
+  static const int n = [] {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      n = v;
-    if (n <= 0) n = 256;
-  }
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      return v;
+    return 256;
+  }();
   return n;
 }
 

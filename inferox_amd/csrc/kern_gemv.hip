@@ -544,31 +544,32 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(KArgs a, Epi epi) {
 }
 
 int device_cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0;
-    hipDeviceProp_t p;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
-    if (n <= 0) n = 256;
-  }
+  // initialised once, thread-safe (sessions may run on several threads)
+  static const int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      return v;
+    return 256;
+  }();
   return n;
 }
 
+// Rows of >16K columns need more than 64 KiB of LDS: each kernel instance
+// opts in once, through a block-scope static of a function instantiated per
+// kernel (initialised the first time a launch gets there, once even when
+// sessions run on several threads).
 template <class K>
-hipError_t lds_opt_in(K kernel, size_t lds, bool& done) {
-  if (lds > 64 * 1024 && !done) {  // rows of >16K columns need more than 64 KiB of LDS
-    hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
-    if (e != hipSuccess) return e;
-    done = true;
-  }
-  return hipSuccess;
+hipError_t allow_lds(K kernel) {
+  return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
 }
 
 template <class Epi, class F>
 hipError_t dispatch(const KArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
-  static bool done = false;
-  hipError_t e = lds_opt_in(k_gemv<Epi, F>, lds, done);
-  if (e != hipSuccess) return e;
+  if (lds > 64 * 1024) {
+    static const hipError_t opted = allow_lds(k_gemv<Epi, F>);
+    if (opted != hipSuccess) return opted;
+  }
   hipLaunchKernelGGL((k_gemv<Epi, F>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
   return hipGetLastError();
 }
@@ -627,9 +628,10 @@ hipError_t launch(const GemvLaunch& L, const Epi& epi, hipStream_t st) {
     acc += a.ntiles[s];
   }
   if (generic) {
-    static bool done = false;
-    hipError_t e = lds_opt_in(k_gemv_generic<Epi>, lds, done);
-    if (e != hipSuccess) return e;
+    if (lds > 64 * 1024) {
+      static const hipError_t opted = allow_lds(k_gemv_generic<Epi>);
+      if (opted != hipSuccess) return opted;
+    }
     hipLaunchKernelGGL(k_gemv_generic<Epi>, dim3(blocks), dim3(kThreads), lds, st, a, epi);
     return hipGetLastError();
   }

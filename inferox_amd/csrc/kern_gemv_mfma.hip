@@ -1073,24 +1073,25 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemv_ks_merge(KsArgs a) {
 }
 
 int cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0;
-    hipDeviceProp_t p;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
-    if (n <= 0) n = 256;
-  }
+  // initialised once, thread-safe (sessions may run on several threads)
+  static const int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      return v;
+    return 256;
+  }();
   return n;
 }
 
 template <class Epi, int TA, int TB, int D, bool NORM, int KB>
 hipError_t go_one(const MArgs& a, const Epi& epi, uint32_t blocks, size_t lds, hipStream_t st) {
-  static bool opted = false;
-  if (lds > 64 * 1024 && !opted) {  // rows of more than ~18K columns (the 70B down projection: 28672)
-    hipError_t e = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM, KB>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
-    if (e != hipSuccess) return e;
-    opted = true;
+  if (lds > 64 * 1024) {  // rows of more than ~18K columns (the 70B down projection: 28672)
+    // the instance opts in once; a block-scope static is initialised the first
+    // time a launch gets here, once even when sessions run on several threads
+    static const hipError_t opted = hipFuncSetAttribute((const void*)k_gemv_mfma<Epi, TA, TB, D, NORM, KB>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
+    if (opted != hipSuccess) return opted;
   }
   hipLaunchKernelGGL((k_gemv_mfma<Epi, TA, TB, D, NORM, KB>), dim3(blocks), dim3(kThreads), lds, st, a, epi);
   return hipGetLastError();
