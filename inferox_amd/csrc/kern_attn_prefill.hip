@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
   constexpr int UV = HP * 8 * 2 / kThreads;     // V^T chunks per thread
   __shared__ __attribute__((aligned(16))) _Float16 Kh[kKB * HP], Kl[kKB * HP];
   __shared__ __attribute__((aligned(16))) _Float16 Vh[HP * kKB], Vl[HP * kKB];
-  __shared__ int kexp_s[kKB];
+  __shared__ __attribute__((aligned(16))) float kfac_s[kKB];  // per key of the block: 2^(e_k - 14) log2(e) / sqrt(hd)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fi = lane & 15, fg = lane >> 4;
@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
   const uint32_t q0 = qb * kQ, group = a.n_heads / a.n_kv_heads, hk = h / group;
   const uint32_t qd = a.n_heads * HD;
   const uint32_t nkb_all = (a.n + kKB - 1) / kKB, npad = nkb_all * kKB;
-  const float rsq = 1.0f / sqrtf((float)HD);
+  const float kc = 1.44269504088896341f / sqrtf((float)HD);  // log2(e) / sqrt(hd)
 
   // ---- this lane's query (fi) as the B operand of S^T = K Q^T, in registers ----
   const uint32_t qt = q0 + 16 * wave + fi;
@@ -312,7 +312,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
       const int c = tid + kThreads * u, pl = c / (HP * 8), rem = c % (HP * 8);
       *(u4*)((pl ? Vl : Vh) + swzv(rem >> 3, rem & 7)) = rv[u];
     }
-    if (tid < kKB) kexp_s[tid] = rke;
+    if (tid < kKB) kfac_s[tid] = ldexpf(kc, rke - 14);
   };
 
   f4 o[NT];
@@ -351,33 +351,50 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // scale, mask, running max / sum over the block's keys for query qt
+    // Scores in the log2 domain (src/ops.rs:223-239 takes exp(s - max); here
+    // 2^(log2(e) (s - max))): t = S^T * kf, kf = 2^(e_k - 14) log2(e) /
+    // sqrt(hd) per key, staged with the block, so that qinv t (qinv = 2^(e_q - 14),
+    // exact) is the score times log2(e).  The weights are 2^(qinv (t - m)),
+    // from one fma and v_exp_f32.  Masks only where the block crosses the
+    // wave's diagonal or the chunk's end (a uniform branch).
     float bm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 kf = *(const float4*)&kfac_s[16 * j + 4 * fg];
+      s[j][0] *= kf.x;
+      s[j][1] *= kf.y;
+      s[j][2] *= kf.z;
+      s[j][3] *= kf.w;
+    }
+    const bool full = k0 + kKB <= kend && (!a.causal || k0 + kKB - 1 <= q0 + 16 * (uint32_t)wave);
+    if (!full) {
+      // key k0 + 4 fg + 16 j + r is attended iff 16 j + r <= lim
+      const int lim = (int)(a.causal ? min(qt, kend - 1) : kend - 1) - (int)(k0 + 4 * (uint32_t)fg);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) s[j][r] = 16 * j + r <= lim ? s[j][r] : -INFINITY;
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int kr = 16 * j + 4 * fg + r;
-        const uint32_t key = k0 + (uint32_t)kr;
-        const bool ok = key < kend && (!a.causal || key <= qt);
-        const float kinv = ldexpf(1.f, kexp_s[kr] - 14);
-        s[j][r] = ok ? (s[j][r] * (qinv * kinv)) * rsq : -INFINITY;
-        bm = fmaxf(bm, s[j][r]);
-      }
+      for (int r = 0; r < 4; r++) bm = fmaxf(bm, s[j][r]);
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
-    const float alpha = mn == -INFINITY ? 1.f : expf(m - mn);
+    const bool none = mn == -INFINITY;  // no attended key yet (m and every t are -inf)
+    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(qinv * (m - mn));
     const int vnew = ve > vref ? ve : vref;
     const float oscale = alpha * ldexpf(1.f, vref - vnew);  // the output's rescale
     const float pscale = ldexpf(1.f, ve - vnew);            // this block's weights, <= 1
+    const float c = none ? 0.f : -(qinv * mn);              // exact: qinv is a power of 2
     float ps = 0.f;
     h4 ph[4], pl[4];
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const float p = mn == -INFINITY ? 0.f : expf(s[j][r] - mn);
+        const float p = __builtin_amdgcn_exp2f(fmaf(qinv, s[j][r], c));
         ps += p;
         const float pw = p * pscale;
         ph[j][r] = (_Float16)pw;
@@ -394,8 +411,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_attn_prefill(AttnPrefillArgs a,
     // this lane's weights already hold: 32c + 4fg + r (tile 2c) and
     // 32c + 16 + 4fg + r (tile 2c + 1).  V^T's columns are read in the same
     // order, so the sum over k is the sum over the 32 keys.
+    if (__any(oscale != 1.f)) {  // a new running max or V scale on some lane
 #pragma unroll
-    for (int t = 0; t < NT; t++) o[t] *= oscale;
+      for (int t = 0; t < NT; t++) o[t] *= oscale;
+    }
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const h8 p8h = __builtin_shufflevector(ph[2 * c], ph[2 * c + 1], 0, 1, 2, 3, 4, 5, 6, 7);
