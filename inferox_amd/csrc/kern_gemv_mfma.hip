@@ -186,7 +186,6 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
 // top bits of bytes s - 4 / s (dequant.rs:141-149).
 template <>
 struct KBuf<T_Q4K> {
-  static constexpr uint64_t kUnit = kUnitQ4K;
   uint4 h, q0, q1;
   // u: wave-uniform unit base; 32-bit unsigned lane offsets keep the
   // scalar-base addressing form (no 64-bit address per lane)
@@ -217,7 +216,6 @@ struct KBuf<T_Q4K> {
 // sc u8, or int8 for a tensor read in ggml's layout (sgn).
 template <>
 struct KBuf<T_Q6K> {
-  static constexpr uint64_t kUnit = kUnitQ6K;
   uint4 l0, l1, hq;
   uint32_t sc, d, xm;
   float off;  // int8 scales: each byte's top bit flipped (xm) and 128 taken off at use
