@@ -316,7 +316,7 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
   ifx_model* m = s->m;
   const ifx_config& c = m->cfg;
   hipStream_t st = s->stream;
-  const uint32_t D = (uint32_t)c.hidden_size, F = (uint32_t)c.intermediate_size;
+  const uint32_t D = (uint32_t)c.hidden_size;
   const uint32_t kvd = (uint32_t)(c.n_kv_heads * c.head_dim);
   switch (k) {
     case 0:
