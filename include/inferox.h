@@ -176,12 +176,13 @@ int ifx_decode_greedy(ifx_session* s, uint32_t token, uint64_t n_steps, uint32_t
 int ifx_session_set_sampler(ifx_session* s, float temperature, uint32_t top_k, float top_p, uint64_t seed);
 
 /* ifx_generate with every generated token drawn by the session's sampler on
- * the device (k_sample between the logits and the state update). */
+ * the device (three sampler launches between the logits and the state
+ * update). */
 int ifx_generate_sampled(ifx_session* s, const uint32_t* prompt, uint64_t n, uint64_t max_tokens,
                          uint32_t* out_tokens);
 
 /* One-off draws from host logits[vocab] (tests): n_draws draws, draw i with
- * counter i, as generate step i would. */
+ * counter i, as generate step i would.  IFX_E_NAN_LOGIT if a logit is NaN. */
 int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, uint32_t top_k, float top_p,
                       uint64_t seed, uint32_t n_draws, uint32_t* out);
 

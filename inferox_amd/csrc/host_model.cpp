@@ -67,7 +67,7 @@ struct ifx_session {
   uint32_t *out_tokens = nullptr, *feed_ids = nullptr;
   uint32_t attn_chunk = 64, max_chunks = 0;
   // captured steps: [sampling][merge bound / 8] (the greedy step, the step
-  // with k_sample before finalize; each with the attention merge in its own
+  // with the sampler before finalize; each with the attention merge in its own
   // launch (bound 0) or in the O projection's prologue, which loads the first
   // `merge_bound` chunk records up front)
   static constexpr int kMergeGraphs = 7;
@@ -78,7 +78,8 @@ struct ifx_session {
   // through the tiled launches, the attention merge in its own launch
   bool deterministic = false;
   uint32_t merge_bound = 0;              // of the step being enqueued: 0, or a multiple of 8 up to 48
-  float* probs = nullptr;                // k_sample scratch [vocab]
+  float* probs = nullptr;                // sampler weights [vocab]
+  void* sample_ws = nullptr;             // sampler histogram, sums and candidates (sample_ws_bytes)
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
   std::vector<void*> allocs;
@@ -335,7 +336,8 @@ int enqueue_class(ifx_session* s, int k, size_t l) {
       return IFX_OK;
     }
     case 7:
-      if (s->sampling) IFX_HIP(launch_sample(s->logits, s->probs, (uint32_t)c.vocab_size, s->state, st));
+      if (s->sampling)
+        IFX_HIP(launch_sample(s->logits, s->probs, sample_ws(s->sample_ws), (uint32_t)c.vocab_size, s->state, st));
       IFX_HIP(launch_finalize(s->state, st));
       return IFX_OK;
     default:
@@ -560,7 +562,8 @@ int batched_prefill(ifx_session* s, uint64_t n, uint64_t start, bool causal, flo
   gh.norm_w = m->out_norm;
   gh.eps = c.norm_eps;
   IFX_HIP(gemv_logits(gh, s->logits, s->state, st));
-  if (s->sampling) IFX_HIP(launch_sample(s->logits, s->probs, (uint32_t)c.vocab_size, s->state, st));
+  if (s->sampling)
+    IFX_HIP(launch_sample(s->logits, s->probs, sample_ws(s->sample_ws), (uint32_t)c.vocab_size, s->state, st));
   IFX_HIP(launch_finalize(s->state, st));
   if (logits_out) {
     const uint64_t V = c.vocab_size, rows = std::min<uint64_t>(n, 512);
@@ -745,6 +748,7 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
   A((void**)&s->mid, F * 4);
   A((void**)&s->logits, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
   A((void**)&s->probs, (uint64_t)std::max<uint32_t>(c.vocab_size, 1) * 4);
+  A(&s->sample_ws, sample_ws_bytes());
   A((void**)&s->partial, (uint64_t)c.n_kv_heads * s->max_chunks * attn_partial_floats(G, c.head_dim) * 4);
   A((void**)&s->qkv_q, (uint64_t)std::max<size_t>(m->layers.size(), 1) * D * 4);
   A((void**)&s->rope_cs, max_seq_len * std::max<uint64_t>(c.rope_dim / 2, 1) * 8);
@@ -768,7 +772,7 @@ int ifx_session_create_kv(ifx_model* m, uint64_t max_seq_len, int kv_type, ifx_s
   if (hipMemcpy(s->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(s->state, &init, sizeof init, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemset(s->kc, 0, kv_bytes) != hipSuccess || hipMemset(s->vc, 0, kv_bytes) != hipSuccess ||
-      hipDeviceSynchronize() != hipSuccess) {
+      hipMemset(s->sample_ws, 0, sample_ws_bytes()) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     session_free(s);
     return set_error(IFX_E_HIP, "session initialisation failed");
   }
@@ -974,13 +978,16 @@ int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, ui
     return set_error(IFX_E_INVALID_ARG, "sample needs temperature > 0 and 0 <= top_p <= 1");
   hipStream_t st = nullptr;
   float *dl = nullptr, *dp = nullptr;
+  void* dw = nullptr;
   DevState* ds = nullptr;
   uint32_t* dt = nullptr;
   hipError_t e = hipMalloc(&dl, (size_t)vocab * 4);
   if (e == hipSuccess) e = hipMalloc(&dp, (size_t)vocab * 4);
+  if (e == hipSuccess) e = hipMalloc(&dw, sample_ws_bytes());
   if (e == hipSuccess) e = hipMalloc(&ds, sizeof(DevState));
   if (e == hipSuccess) e = hipMalloc(&dt, (size_t)std::max<uint32_t>(n_draws, 1) * 4);
   if (e == hipSuccess) e = hipMemcpy(dl, logits, (size_t)vocab * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(dw, 0, sample_ws_bytes());
   DevState init{};
   init.out_tokens = dt;
   init.out_cap = n_draws;
@@ -989,16 +996,20 @@ int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, ui
   init.top_p = top_p;
   init.seed = seed;
   if (e == hipSuccess) e = hipMemcpy(ds, &init, sizeof init, hipMemcpyHostToDevice);
-  // draw i uses step i, as generate step i would; finalize stores it and advances
+  // draw i uses step i, as generate step i would; the maximum first, as the
+  // head leaves it; finalize stores the draw and advances
+  const SampleWs ws = sample_ws(dw);
   for (uint32_t i = 0; i < n_draws && e == hipSuccess; i++) {
-    e = launch_sample(dl, dp, vocab, ds, st);
+    e = launch_logits_max(dl, vocab, ds, st);
+    if (e == hipSuccess) e = launch_sample(dl, dp, ws, vocab, ds, st);
     if (e == hipSuccess) e = launch_finalize(ds, st);
   }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e == hipSuccess && n_draws) e = hipMemcpy(out, dt, (size_t)n_draws * 4, hipMemcpyDeviceToHost);
-  for (void* p : {(void*)dl, (void*)dp, (void*)ds, (void*)dt}) if (p) (void)hipFree(p);
+  for (void* p : {(void*)dl, (void*)dp, dw, (void*)ds, (void*)dt}) if (p) (void)hipFree(p);
   if (e != hipSuccess) return set_error(IFX_E_HIP, "sample: %s", hipGetErrorString(e));
-  for (uint32_t i = 0; i < n_draws; i++) out[i] &= 0x7fffffffu;
+  for (uint32_t i = 0; i < n_draws; i++)
+    if (out[i] & 0x80000000u) return set_error(IFX_E_NAN_LOGIT, "sample: NaN among the logits");
   return IFX_OK;
 }
 

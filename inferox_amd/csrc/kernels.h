@@ -28,7 +28,7 @@ struct DevState {
   uint32_t* out_tokens;           // greedy picks (device)
   uint32_t out_cap;
   uint32_t attn_end;     // 0: attend rows [attn_lo, len]; else rows [attn_lo, attn_end)
-  // sampler (k_sample; temperature 0: the greedy argmax)
+  // sampler (kern_sample.hip; temperature 0: the greedy argmax)
   float temperature;
   uint32_t top_k;
   float top_p;
@@ -235,9 +235,32 @@ hipError_t launch_finalize(DevState* state, hipStream_t st);
 enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL, STATE_TOKEN_AT, STATE_BATCH,
                             STATE_SAMPLER };
 // ---- sampling (kern_sample.hip) ----
+// The sampler's device scratch: a histogram of the probabilities (counts and
+// masses packed per bin), each sweeping workgroup's sum, the candidate list
+// and the draw's plan.  Zeroed once when allocated; every draw leaves the
+// histogram and the candidate count zero again for the next.
+struct SampleCtl {
+  uint32_t count;  // candidates appended by the gather
+  uint32_t mode;   // the plan: 1 draw over all, 2 candidates, 3 one-workgroup fallback
+  uint32_t lo_bin, n_cand;
+};
+struct SampleWs {
+  unsigned long long* hist;
+  float* part;
+  uint2* cand;  // (index, probability bits)
+  SampleCtl* ctl;
+};
+size_t sample_ws_bytes();
+SampleWs sample_ws(void* base);  // the scratch carved from sample_ws_bytes() zeroed bytes
 // Overrides state->argmax_key with a temperature / top-k / top-p draw from
 // logits[vocab] when state->temperature > 0 (probs: vocab floats of scratch).
-hipError_t launch_sample(const float* logits, float* probs, uint32_t vocab, DevState* state, hipStream_t st);
+// state->argmax_key must hold the maximum logit's key on entry (the head's
+// greedy argmax, or launch_logits_max).
+hipError_t launch_sample(const float* logits, float* probs, const SampleWs& ws, uint32_t vocab, DevState* state,
+                         hipStream_t st);
+// state->argmax_key and state->status from logits[vocab], as the head's
+// argmax leaves them (for draws from logits the host supplies).
+hipError_t launch_logits_max(const float* logits, uint32_t vocab, DevState* state, hipStream_t st);
 struct StateOp {
   uint32_t kind;
   uint32_t value;

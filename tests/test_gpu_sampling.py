@@ -1,9 +1,15 @@
-"""Device sampling (k_sample) against the oracle's restatement of
+"""Device sampling (kern_sample.hip) against the oracle's restatement of
 Sampler::sample (src/sampler.rs:28-76, max-shifted): every draw inside the
 kept set, draw frequencies within a total-variation bound of the kept
 distribution, reproducible from the seed; generate with the sampler on the
 tiny model (token replay and batched prefill), where top_k = 1 must give the
 greedy tokens.
+
+The sampler takes one of three paths per draw, each covered here: the draw
+over the whole vocabulary in index order (neither filter), the sorted
+candidate list (top-k / top-p with at most 4096 candidates), and the
+one-workgroup radix selection (more candidates).  Which inputs take which path
+follows from the histogram plan; the cases below name theirs.
 
 Bars: support exact; TV distance < 0.04 over 20000 draws of a 32-token
 vocabulary (the sampling noise is ~0.016); equal seeds give equal tokens."""
@@ -30,7 +36,8 @@ def _draw(logits, T, k, p, seed, n):
     return out
 
 
-@pytest.mark.parametrize("T,k,p", [(1.0, 0, 1.0), (0.7, 8, 1.0), (1.3, 0, 0.8), (1.0, 12, 0.7), (2.0, 3, 0.95)])
+@pytest.mark.parametrize("T,k,p", [(1.0, 0, 1.0), (0.7, 8, 1.0), (1.3, 0, 0.8), (1.0, 12, 0.7), (2.0, 3, 0.95),
+                                   (1.0, 50, 1.0), (0.9, 0, 0.0)])
 def test_sample_distribution(T, k, p):
     rng = np.random.default_rng(int(T * 10) + k)
     z = (rng.standard_normal(32) * 2.0).astype(np.float32)
@@ -48,6 +55,71 @@ def test_sample_support_full_vocab():
         want = numpy_ref.sampler_probs(z, 0.8, k, p)
         got = _draw(z, 0.8, k, p, seed=7, n=400)
         assert set(np.unique(got)) <= set(np.flatnonzero(want))
+
+
+def _peaked(seed=21):
+    """An 8B-sized vocabulary whose mass sits on 30 entries 25 above the rest."""
+    r = np.random.default_rng(seed)
+    z = (r.standard_normal(synth.LLAMA3_8B.vocab) * 3.0).astype(np.float32)
+    top = r.choice(z.size, 30, replace=False)
+    z[top] += 25.0
+    return z, np.sort(top)
+
+
+@pytest.mark.parametrize("k,p", [(0, 1.0), (40, 0.9), (0, 0.9)])
+def test_sample_distribution_full_vocab(k, p):
+    """128256 entries: neither filter (the whole-vocabulary draw), top-k 40
+    with top-p 0.9, top-p 0.9 alone (five candidates).  TV < 0.04 over 20000
+    draws, with the entries outside the 30 peaks as one bucket."""
+    z, top = _peaked()
+    want = numpy_ref.sampler_probs(z, 1.0, k, p)
+    got = _draw(z, 1.0, k, p, seed=77, n=20000)
+    assert set(np.unique(got)) <= set(np.flatnonzero(want)), "draw outside the kept set"
+    freq = np.bincount(got, minlength=z.size) / got.size
+    fb = np.append(freq[top], 1.0 - freq[top].sum())
+    wb = np.append(want[top], 1.0 - want[top].sum())
+    assert 0.5 * np.abs(fb - wb).sum() < 0.04
+
+
+@pytest.mark.parametrize("V", [1000, 32000])
+def test_sample_top_k_ties_take_the_lowest_indices(V):
+    """All logits equal: the reference's stable sort keeps indices 0..9 for
+    top-k 10.  1000 entries: the candidate sort; 32000: more candidates than
+    it holds, the one-workgroup path."""
+    got = _draw(np.zeros(V, np.float32), 1.0, 10, 1.0, seed=3, n=2000)
+    assert set(np.unique(got)) == set(range(10))
+
+
+def test_sample_top_p_zero_keeps_the_first_maximum():
+    """top_p 0 keeps the head of the sorted list: of two equal maxima, the
+    lower index (the greedy argmax takes the higher one)."""
+    r = np.random.default_rng(8)
+    z = r.uniform(-4, 4, 1000).astype(np.float32)
+    z[[100, 700]] = 5.0
+    assert set(np.unique(_draw(z, 1.0, 0, 0.0, seed=4, n=200))) == {100}
+    assert set(np.unique(_draw(z, 1.0, 1, 1.0, seed=4, n=200))) == {100}
+
+
+@pytest.mark.parametrize("T,k,p", [(2.0, 0, 0.99), (1.0, 5000, 1.0)])
+def test_sample_many_candidates(T, k, p):
+    """A flat 32000-entry vocabulary, where the kept set exceeds the candidate
+    sort (the one-workgroup path): every draw inside the oracle's kept set,
+    and the draws spread over it."""
+    r = np.random.default_rng(21)
+    z = (r.standard_normal(32000) * 0.5).astype(np.float32)
+    want = numpy_ref.sampler_probs(z, T, k, p)
+    got = _draw(z, T, k, p, seed=5, n=3000)
+    assert set(np.unique(got)) <= set(np.flatnonzero(want))
+    assert np.unique(got).size > 1500
+
+
+def test_sample_nan_logit_is_an_error():
+    z = np.zeros(64, np.float32)
+    z[9] = np.nan
+    out = np.zeros(4, np.uint32)
+    rc = _native.lib().ifx_sample_logits(z.ctypes.data_as(C.c_void_p), z.size, 1.0, 0, 1.0, 1, 4,
+                                         out.ctypes.data_as(C.c_void_p))
+    assert rc == 24  # IFX_E_NAN_LOGIT
 
 
 def test_sample_reproducible_and_seeded():
