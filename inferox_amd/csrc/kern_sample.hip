@@ -31,13 +31,14 @@
 //   k_sample_select (one workgroup): the candidates sorted by decreasing p,
 //     ties in index order, in LDS; top-k, top-p, and the draw walking the kept
 //     list in that order, as the reference walks its sorted list.  With more
-//     candidates than the sort holds, the single-workgroup draw below
-//     (sample_one_wg) runs instead, from the logits: thread t owns the index
-//     range [t per, (t + 1) per) so that index order is thread order, the
+//     candidates than the sort holds (draw_many), only the bins that can hold
+//     the last kept entry are gathered and sorted, and the draw walks the kept
+//     set in index order (the same distribution in another order).  When
+//     those bins alone exceed the sort (equal logits), the single-workgroup
+//     draw below (sample_one_wg) runs from the logits: thread t owns the index
+//     range [t per, (t + 1) per) so that index order is thread order, and the
 //     k-th largest probability and the top-p threshold come from a 4-pass
-//     radix select on the float bits (non-negative floats order as integers),
-//     and the draw walks the kept entries in index order (the same
-//     distribution in another order).
+//     radix select on the float bits (non-negative floats order as integers).
 // One workgroup swept the vocabulary by itself for every draw before: 1.14 ms
 // of a sampled 8B step at 128256 entries.
 #include "kernels.h"
@@ -210,7 +211,8 @@ __device__ void keep_top(float* p, uint32_t i0, uint32_t i1, uint32_t key, uint3
 }
 
 // The whole draw in one workgroup of kT threads, from the logits: the
-// fallback of k_sample_select when the candidates exceed kCap.
+// last resort of k_sample_select, when the bins that can hold the last kept
+// entry alone hold more than kCap entries.
 __device__ void sample_one_wg(const float* logits, float* p, uint32_t V, DevState* s) {
   __shared__ Blk b;
   __shared__ uint32_t pick;
@@ -688,50 +690,25 @@ __device__ __forceinline__ void share(uint32_t n, uint32_t& a0, uint32_t& a1) {
   a1 = min(n, a0 + q);
 }
 
-// The draw from the candidates: sorted by decreasing p, ties by index (the
-// reference's stable sort); top-k; top-p, the first position whose running sum
-// reaches top_p S; the draw over the kept prefix in that order.  With more
-// candidates than kCap, the one-workgroup draw from the logits.  Leaves the
-// histogram and the candidate count zero for the next draw.
-__global__ void __launch_bounds__(kT) k_sample_select(const float* __restrict__ logits, float* __restrict__ p,
-                                                      SampleWs ws, uint32_t V, DevState* s) {
-  __shared__ unsigned long long key[kCap];
+// The draw from a sorted candidate list key[0, n) (keys (~p bits) << 32 |
+// index, ascending: p descending, ties by index, the reference's stable
+// sort): top-k, then top-p, the first position whose running sum reaches
+// top_p S; the draw over the kept prefix in that order, as the reference's
+// WeightedIndex walks its sorted, truncated list.
+__device__ void draw_sorted(const unsigned long long* key, uint32_t n, float S, DevState* s) {
   __shared__ float wt_f[kWaves];
-  __shared__ uint32_t sh_mode, sh_n, cut, found;
-  __shared__ float sh_S;
-  const float T = s->temperature;
-  if (!(T > 0.f) || s->status != IFX_OK) return;
+  __shared__ uint32_t cut, found;
   if (threadIdx.x == 0) {
-    sh_mode = ws.ctl->mode;
-    sh_n = min(ws.ctl->count, kCap);
     cut = kNone;
     found = kNone;
   }
-  if (threadIdx.x < 64) {
-    const float S = part_total(ws.part);
-    if (threadIdx.x == 0) sh_S = S;
-  }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < kBins; i += kT) ws.hist[i] = 0ull;
-  if (threadIdx.x == 0) ws.ctl->count = 0;
-  const uint32_t mode = sh_mode, n = sh_n;
-  if (mode == kModeOneWg) {
-    sample_one_wg(logits, p, V, s);
-    return;
-  }
-  if (mode != kModeCand || n == 0) return;
-  for (uint32_t j = threadIdx.x; j < n; j += kT) {
-    const uint2 c = ws.cand[j];
-    key[j] = ((unsigned long long)(~c.y) << 32) | c.x;
-  }
-  __syncthreads();
-  sort_keys(key, n);
   uint32_t kept = n;
   const uint32_t top_k = s->top_k;
   if (top_k > 0 && top_k < kept) kept = top_k;
   const float top_p = s->top_p;
   if (top_p < 1.0f) {
-    const float R = top_p * sh_S;
+    const float R = top_p * S;
     uint32_t a0, a1;
     share(kept, a0, a1);
     float sum = 0.f;
@@ -750,8 +727,6 @@ __global__ void __launch_bounds__(kT) k_sample_select(const float* __restrict__ 
     __syncthreads();
     if (cut != kNone) kept = cut + 1;
   }
-  // the draw walks the kept list in its sorted order, as the reference's
-  // WeightedIndex walks its sorted, truncated list
   uint32_t a0, a1;
   share(kept, a0, a1);
   float sum = 0.f;
@@ -774,6 +749,324 @@ __global__ void __launch_bounds__(kT) k_sample_select(const float* __restrict__ 
   if (lowest_lane(hit != kNone)) atomicMin(&found, hit);
   __syncthreads();
   if (threadIdx.x == 0) s->argmax_key = key[found != kNone ? found : kept - 1] & 0xffffffffull;
+}
+
+constexpr uint32_t kRow = 4096;  // entries of one row of the index-order draw (16 float4 per lane of a wave)
+static_assert(((1u << 24) / kRow) * 4 <= kCap * 8, "the row sums fit where the candidate keys were");
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ unsigned long long sample_key(uint32_t bits, uint32_t i) {
+  return ((unsigned long long)(~bits) << 32) | i;
+}
+// the weight of entry i in the draw over the kept set {key <= kstar}
+__device__ __forceinline__ float kept_w(float v, uint32_t i, unsigned long long kstar) {
+  return (v > 0.f && sample_key(__float_as_uint(v), i) <= kstar) ? v : 0.f;
+}
+
+// More candidates than the sort holds (a flat distribution with top-p near 1,
+// a large top-k): the kept set is every entry whose key is at most the last
+// kept one's, K*, and only the entries of the bins that can hold that one are
+// sorted.  From the histogram: the top-k bin (exact counts) and the bins
+// between which the top-p boundary lies (the mass lower bounds, and those plus
+// one significand unit per entry).  One sweep over p gathers those bins'
+// entries and sums in double the mass of every entry above them; the gathered
+// ones are sorted and cut (top-k by count, top-p by the running sum from that
+// mass).  The draw walks the kept set in index order: each wave sums whole
+// 4096-entry rows, the workgroup finds the row holding u W, and one wave walks
+// that row.  The reference walks its sorted list instead: the same
+// distribution.  Returns false when the boundary bins alone hold more than
+// kCap entries.
+__device__ bool draw_many(const float* p, const SampleWs& ws, uint32_t V, float S, DevState* s,
+                          unsigned long long* key) {
+  __shared__ uint32_t wt_u[kWaves];
+  __shared__ double wt_d[kWaves];
+  __shared__ float wt_f[kWaves];
+  __shared__ uint32_t fj[4];
+  __shared__ uint32_t c_above, c_incl, n_g;
+  __shared__ double m_above;
+  __shared__ uint32_t cut;
+  __shared__ unsigned long long kstar, rowpick;
+  __shared__ uint32_t found, lastpos;
+  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t top_k = s->top_k;
+  const float top_p = s->top_p;
+  const bool kon = top_k > 0 && top_k < V, pon = top_p < 1.0f;
+  const double R = (double)(top_p * S);
+  // bins in descending positions j = tid (bin kBins - 1 - j)
+  const uint32_t j = (uint32_t)tid;
+  const bool in = j < kBins;
+  uint32_t c = 0;
+  double lm = 0.0, um = 0.0;
+  if (in) {
+    const uint32_t b = kBins - 1 - j;
+    const unsigned long long h = ws.hist[b];
+    c = (uint32_t)(h >> kCountShift);
+    lm = bin_mass(b, h);
+    um = lm + (double)c * (b == 0 ? ldexp(1.0, -32) : ldexp(1.0, 95 + (int)((b - 1) >> 4) - 142));
+  }
+  uint32_t ctot;
+  double ltot, utot;
+  const uint32_t cex = wg_scan<kWaves>(c, wt_u, ctot);
+  const double lex = wg_scan<kWaves>(lm, wt_d, ltot);
+  const double uex = wg_scan<kWaves>(um, wt_d, utot);
+  if (tid < 4) fj[tid] = kNone;
+  if (tid == 0) {
+    n_g = 0;
+    cut = kNone;
+    found = kNone;
+    lastpos = 0;
+    rowpick = ~0ull;
+  }
+  __syncthreads();
+  if (lowest_lane(in && kon && cex + c >= top_k)) atomicMin(&fj[0], j);
+  if (lowest_lane(in && pon && lex + lm >= R * (1.0 + 1e-9))) atomicMin(&fj[1], j);
+  if (lowest_lane(in && pon && uex + um >= R * (1.0 - 1e-9))) atomicMin(&fj[2], j);
+  if (lowest_lane(in && cex + c >= 1)) atomicMin(&fj[3], j);
+  __syncthreads();
+  const uint32_t last = kBins - 1, j1 = min(fj[3], last);
+  const uint32_t jk = kon ? min(fj[0], last) : last;
+  const uint32_t jl = pon ? max(min(fj[1], last), j1) : last;  // the top-p boundary lies at or above it
+  const uint32_t ju = pon ? max(min(fj[2], last), j1) : last;  // ... and at or below this one
+  const uint32_t ja = min(jk, ju), jb = min(jk, jl);
+  if (in && j == ja) c_above = cex;
+  if (in && j == jb) c_incl = cex + c;
+  __syncthreads();
+  const uint32_t n = c_incl - c_above;
+  if (n == 0 || n > kCap) return false;
+  const uint32_t blo = last - jb, bhi = last - ja;
+
+  // gather bins [blo, bhi]; the mass above them.  A wave covers 256
+  // consecutive entries per load, kBatch loads in flight per lane.
+  constexpr uint32_t kBatch = 8;
+  double above = 0.0;
+  for (uint32_t w0 = 4u * (uint32_t)(tid & ~63); w0 < V; w0 += 4u * kT * kBatch) {  // uniform in the wave
+    float4 q[kBatch];
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; u++) {
+      const uint32_t i0 = w0 + 4u * kT * u + 4u * (uint32_t)lane;
+      if (i0 + 3 < V) {
+        q[u] = *(const float4*)(p + i0);
+      } else {
+        q[u].x = i0 < V ? p[i0] : 0.f;
+        q[u].y = i0 + 1 < V ? p[i0 + 1] : 0.f;
+        q[u].z = i0 + 2 < V ? p[i0 + 2] : 0.f;
+        q[u].w = 0.f;
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; u++) {
+      const uint32_t i0 = w0 + 4u * kT * u + 4u * (uint32_t)lane;
+      const float v[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+      uint32_t mine = 0;
+      bool take[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t b = bin_of(__float_as_uint(v[e]));
+        take[e] = v[e] > 0.f && b >= blo && b <= bhi;
+        if (v[e] > 0.f && b > bhi) above += (double)v[e];
+        mine += take[e] ? 1u : 0u;
+      }
+      if (!__any(mine != 0)) continue;
+      uint32_t x = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+      }
+      uint32_t base = 0;
+      if (lane == 63) base = atomicAdd(&n_g, x);
+      base = __shfl(base, 63, 64);
+      uint32_t at = base + x - mine;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        if (take[e]) {
+          if (at < kCap) key[at] = sample_key(__float_as_uint(v[e]), i0 + (uint32_t)e);
+          at++;
+        }
+      }
+    }
+  }
+  above = wave_sum_d(above);
+  if (lane == 0) wt_d[wave] = above;
+  __syncthreads();
+  if (tid == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kWaves; w++) t += wt_d[w];
+    m_above = t;
+  }
+  const uint32_t ng = min(n_g, kCap);
+  if (ng == 0) return false;
+  sort_keys(key, ng);  // ends with a barrier
+  // top-k by count, then top-p by the running sum from the mass above
+  uint32_t kept = ng;
+  if (kon) kept = c_above < top_k ? min(kept, top_k - c_above) : 1u;
+  if (pon) {
+    uint32_t a0, a1;
+    share(kept, a0, a1);
+    double sum = 0.0;
+    for (uint32_t q = a0; q < a1; q++) sum += (double)__uint_as_float(~(uint32_t)(key[q] >> 32));
+    double unused;
+    double acc = m_above + wg_scan<kWaves>(sum, wt_d, unused);
+    uint32_t hit = kNone;
+    for (uint32_t q = a0; q < a1; q++) {
+      acc += (double)__uint_as_float(~(uint32_t)(key[q] >> 32));
+      if (acc >= R) {
+        hit = q;
+        break;
+      }
+    }
+    if (lowest_lane(hit != kNone)) atomicMin(&cut, hit);
+    __syncthreads();
+    if (cut != kNone) kept = min(kept, cut + 1);
+  }
+  if (tid == 0) kstar = key[kept - 1];
+  __syncthreads();
+  const unsigned long long ks = kstar;
+
+  // row sums of the kept weights (rows of kRow entries, one wave per row)
+  float* rowsum = (float*)key;
+  const uint32_t rows = (V + kRow - 1) / kRow;
+  for (uint32_t r = (uint32_t)wave; r < rows; r += kWaves) {
+    float sum = 0.f;
+#pragma unroll
+    for (uint32_t q = 0; q < kRow / 256; q++) {
+      const uint32_t i0 = r * kRow + 256 * q + 4 * (uint32_t)lane;
+      if (i0 + 3 < V) {
+        const float4 v = *(const float4*)(p + i0);
+        sum += kept_w(v.x, i0, ks) + kept_w(v.y, i0 + 1, ks) + kept_w(v.z, i0 + 2, ks) + kept_w(v.w, i0 + 3, ks);
+      } else {
+        for (uint32_t e = 0; e < 4; e++)
+          if (i0 + e < V) sum += kept_w(p[i0 + e], i0 + e, ks);
+      }
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) rowsum[r] = sum;
+  }
+  __syncthreads();
+  // the row holding target = u W (thread t: rows [t q, (t + 1) q))
+  uint32_t r0, r1;
+  share(rows, r0, r1);
+  float rs = 0.f;
+  uint32_t lastrow = 0;
+  for (uint32_t r = r0; r < r1; r++) {
+    rs += rowsum[r];
+    if (rowsum[r] > 0.f) lastrow = r + 1;
+  }
+  float W;
+  const float rb = wg_scan<kWaves>(rs, wt_f, W);
+  const float target = uniform01(s->seed, s->step) * W;
+  unsigned long long pickrow = ~0ull;
+  if (rs > 0.f && rb <= target && target < rb + rs) {
+    float acc = rb;
+    for (uint32_t r = r0; r < r1; r++) {
+      if (rowsum[r] > 0.f && target < acc + rowsum[r]) {
+        pickrow = ((unsigned long long)r << 32) | __float_as_uint(target - acc);
+        break;
+      }
+      acc += rowsum[r];
+    }
+  }
+  if (lowest_lane(pickrow != ~0ull)) atomicMin(&rowpick, pickrow);
+  if (highest_lane(lastrow != 0)) atomicMax(&lastpos, lastrow);
+  __syncthreads();
+  if (rowpick == ~0ull && lastpos == 0) return true;  // no kept weight (not reached: K* is kept)
+  // the walk: wave 0 over the row, lane l its entries [64 l, 64 l + 64)
+  const bool fallback = rowpick == ~0ull;
+  const uint32_t prow = fallback ? lastpos - 1 : (uint32_t)(rowpick >> 32);
+  const float tl = fallback ? INFINITY : __uint_as_float((uint32_t)rowpick);
+  if (wave == 0) {
+    const uint32_t a0 = min(V, prow * kRow + 64 * (uint32_t)lane), a1 = min(V, a0 + 64);
+    float ls = 0.f;
+    uint32_t lp = 0;
+    if (a1 - a0 == 64) {
+      float4 q[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) q[u] = *(const float4*)(p + a0 + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        const float v[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t i = a0 + 4 * u + e;
+          const float w = kept_w(v[e], i, ks);
+          ls += w;
+          if (w > 0.f) lp = i + 1;
+        }
+      }
+    } else {
+      for (uint32_t i = a0; i < a1; i++) {
+        const float w = kept_w(p[i], i, ks);
+        ls += w;
+        if (w > 0.f) lp = i + 1;
+      }
+    }
+    float x = ls;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    const float ex = x - ls;
+    uint32_t hit = kNone;
+    if (ls > 0.f && ex <= tl && tl < ex + ls) {
+      float acc = ex;
+      for (uint32_t i = a0; i < a1; i++) {
+        const float w = kept_w(p[i], i, ks);
+        acc += w;
+        if (w > 0.f && tl < acc) {
+          hit = i;
+          break;
+        }
+      }
+    }
+    const unsigned long long hb = __ballot(hit != kNone), lb = __ballot(lp != 0);
+    const uint32_t pick_lane = hb ? (uint32_t)(__ffsll((long long)hb) - 1) : (lb ? (uint32_t)(63 - __clzll((long long)lb)) : 64u);
+    const uint32_t pick = hb ? __shfl(hit, (int)pick_lane, 64) : (lb ? __shfl(lp, (int)pick_lane, 64) - 1 : kNone);
+    if (lane == 0 && pick != kNone) s->argmax_key = pick;
+  }
+  return true;
+}
+
+// The draw: from the sorted candidates (at most kCap), from the boundary bins
+// (draw_many) when there are more, and from the logits by one workgroup
+// (sample_one_wg) when the boundary bins alone hold more than kCap.  Leaves
+// the histogram and the candidate count zero for the next draw.
+__global__ void __launch_bounds__(kT) k_sample_select(const float* __restrict__ logits, float* __restrict__ p,
+                                                      SampleWs ws, uint32_t V, DevState* s) {
+  __shared__ unsigned long long key[kCap];
+  __shared__ uint32_t sh_mode, sh_n;
+  __shared__ float sh_S;
+  const float T = s->temperature;
+  if (!(T > 0.f) || s->status != IFX_OK) return;
+  if (threadIdx.x == 0) {
+    sh_mode = ws.ctl->mode;
+    sh_n = min(ws.ctl->count, kCap);
+  }
+  if (threadIdx.x < 64) {
+    const float S = part_total(ws.part);
+    if (threadIdx.x == 0) sh_S = S;
+  }
+  __syncthreads();
+  const uint32_t mode = sh_mode, n = sh_n;
+  const float S = sh_S;
+  if (mode == kModeCand && n > 0) {
+    for (uint32_t j = threadIdx.x; j < n; j += kT) {
+      const uint2 c = ws.cand[j];
+      key[j] = sample_key(c.y, c.x);
+    }
+    __syncthreads();
+    sort_keys(key, n);
+    draw_sorted(key, n, S, s);
+  } else if (mode == kModeOneWg) {
+    if (!draw_many(p, ws, V, S, s, key)) sample_one_wg(logits, p, V, s);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < kBins; i += kT) ws.hist[i] = 0ull;
+  if (threadIdx.x == 0) ws.ctl->count = 0;
 }
 
 // The maximum logit's key and the NaN flag, as the head's argmax leaves them.

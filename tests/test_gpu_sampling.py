@@ -5,11 +5,13 @@ distribution, reproducible from the seed; generate with the sampler on the
 tiny model (token replay and batched prefill), where top_k = 1 must give the
 greedy tokens.
 
-The sampler takes one of three paths per draw, each covered here: the draw
+The sampler takes one of four paths per draw, each covered here: the draw
 over the whole vocabulary in index order (neither filter), the sorted
-candidate list (top-k / top-p with at most 4096 candidates), and the
-one-workgroup radix selection (more candidates).  Which inputs take which path
-follows from the histogram plan; the cases below name theirs.
+candidate list (top-k / top-p with at most 4096 candidates), the sorted
+boundary bins with an index-order draw over the kept set (more candidates),
+and the one-workgroup radix selection (boundary bins beyond 4096 entries:
+equal logits).  Which inputs take which path follows from the histogram plan;
+the cases below name theirs.
 
 Bars: support exact; TV distance < 0.04 over 20000 draws of a 32-token
 vocabulary (the sampling noise is ~0.016); equal seeds give equal tokens."""
@@ -103,14 +105,36 @@ def test_sample_top_p_zero_keeps_the_first_maximum():
 @pytest.mark.parametrize("T,k,p", [(2.0, 0, 0.99), (1.0, 5000, 1.0)])
 def test_sample_many_candidates(T, k, p):
     """A flat 32000-entry vocabulary, where the kept set exceeds the candidate
-    sort (the one-workgroup path): every draw inside the oracle's kept set,
-    and the draws spread over it."""
+    sort (the boundary-bin path): every draw inside the oracle's kept set, and
+    the draws spread over it."""
     r = np.random.default_rng(21)
     z = (r.standard_normal(32000) * 0.5).astype(np.float32)
     want = numpy_ref.sampler_probs(z, T, k, p)
     got = _draw(z, T, k, p, seed=5, n=3000)
     assert set(np.unique(got)) <= set(np.flatnonzero(want))
     assert np.unique(got).size > 1500
+
+
+@pytest.mark.parametrize("T,k,p", [(1.0, 0, 0.95), (1.0, 20000, 1.0)])
+def test_sample_many_kept_distribution(T, k, p):
+    """128256 entries with logits ~ N(0, 1): the kept set (95011 entries for
+    top-p 0.95, 20000 for top-k) is past the candidate sort, so the boundary
+    bins are sorted and the draw walks the kept set in index order by rows.
+    Every draw inside the oracle's kept set; frequencies against the oracle's
+    kept distribution summed over 16 index ranges (the row walk) and over 8
+    ranges of probability rank (the cut): TV < 0.04 over 20000 draws (the
+    sampling noise is ~0.015)."""
+    r = np.random.default_rng(21)
+    z = r.standard_normal(synth.LLAMA3_8B.vocab).astype(np.float32)
+    want = numpy_ref.sampler_probs(z, T, k, p)
+    got = _draw(z, T, k, p, seed=13, n=20000)
+    assert set(np.unique(got)) <= set(np.flatnonzero(want)), "draw outside the kept set"
+    freq = np.bincount(got, minlength=z.size) / got.size
+    edges = np.linspace(0, z.size, 17).astype(int)[:-1]
+    assert 0.5 * np.abs(np.add.reduceat(freq, edges) - np.add.reduceat(want, edges)).sum() < 0.04
+    order = np.argsort(-want, kind="stable")[: np.count_nonzero(want)]
+    redges = np.linspace(0, order.size, 9).astype(int)[:-1]
+    assert 0.5 * np.abs(np.add.reduceat(freq[order], redges) - np.add.reduceat(want[order], redges)).sum() < 0.04
 
 
 def test_sample_nan_logit_is_an_error():
