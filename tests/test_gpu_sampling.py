@@ -137,6 +137,23 @@ def test_sample_many_kept_distribution(T, k, p):
     assert 0.5 * np.abs(np.add.reduceat(freq[order], redges) - np.add.reduceat(want[order], redges)).sum() < 0.04
 
 
+@pytest.mark.parametrize("V", [37, 32003])
+def test_sample_vocab_not_a_multiple_of_four(V):
+    """Vocabulary sizes that are not a multiple of 4: the sweeps load float4
+    and finish the tail entry by entry.  The last entry is made likely and
+    must be drawn, and every draw must be inside the oracle's kept set, with
+    no filter, with top-k 8 and top-p 0.9 (candidates), and with top-p 0.99
+    at T 2 (for 32003 entries, a kept set past the candidate sort)."""
+    r = np.random.default_rng(31)
+    z = (r.standard_normal(V) * 0.5).astype(np.float32)
+    z[-1] = 10.0 if V > 100 else 2.0
+    for T, k, p in ((1.0, 0, 1.0), (0.7, 8, 0.9), (2.0, 0, 0.99)):
+        want = numpy_ref.sampler_probs(z, T, k, p)
+        got = _draw(z, T, k, p, seed=17, n=3000)
+        assert set(np.unique(got)) <= set(np.flatnonzero(want)), (T, k, p)
+        assert (got == V - 1).any(), (T, k, p)
+
+
 def test_sample_nan_logit_is_an_error():
     z = np.zeros(64, np.float32)
     z[9] = np.nan
