@@ -241,7 +241,7 @@ enum StateKind : uint32_t { STATE_RESET, STATE_MODE, STATE_DECODE, STATE_PREFILL
 // histogram and the candidate count zero again for the next.
 struct SampleCtl {
   uint32_t count;  // candidates appended by the gather
-  uint32_t mode;   // the plan: 1 draw over all, 2 candidates, 3 one-workgroup fallback
+  uint32_t mode;   // the plan: 1 draw over all, 2 candidates, 3 more candidates than the select sorts
   uint32_t lo_bin, n_cand;
 };
 struct SampleWs {
