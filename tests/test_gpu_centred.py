@@ -76,11 +76,13 @@ def _rows_of(x, c, rows, r0, r1):
     return x.reshape(c.n_layers, rows, -1)[:, r0:r1]
 
 
-def decode_parity(g, o, rows, steps, tok, seed, kv_f16=False, rope_mode=0, deterministic=False, guard=True):
+def decode_parity(g, o, rows, steps, tok, seed, kv_f16=False, rope_mode=0, deterministic=False, guard=True,
+                  spare=8):
     """Seeded rows imported into both, `steps` decode steps compared (logits,
-    picks), then the rows the steps wrote.  Returns (worst rel L2, picks)."""
+    picks), then the rows the steps wrote; the session holds `spare` rows
+    more.  Returns (worst rel L2, picks)."""
     c = o.cfg
-    max_seq = rows + steps + 8
+    max_seq = rows + steps + spare
     k, v = _kv_rows(o, rows, seed, kv_f16)
     if guard:
         # the oracle's first step sees the imported V rows
@@ -108,6 +110,8 @@ def decode_parity(g, o, rows, steps, tok, seed, kv_f16=False, rope_mode=0, deter
         assert last_argmax(lg) == tok, step
         picks.append(tok)
     assert worst < tol, worst
+    if spare == 0:  # the cache is full: the next step is refused (src/model/forward.rs:376)
+        assert s.decode_step(tok)[0] == 21
     # the K/V rows the steps appended (src/model/forward.rs:374-378)
     kg, vg = s.kv_export(rows + steps)
     kr, vr = kv.export(rows + steps)
@@ -125,6 +129,18 @@ def test_centred_8b_decode_over_2048_rows(tmpdir_session):
     g, o = GpuModel(p), orc.Model(p)
     decode_parity(g, o, 2048, 4, 1000, seed=41)
     decode_parity(g, o, 2048, 2, 77, seed=43, kv_f16=True)
+    g.close()
+    o.close()
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_centred_8b_decode_fills_the_cache(tmpdir_session, kv_f16):
+    """A session of exactly 2048 rows, 2045 imported and 3 decoded: the last
+    step writes row 2047 and attends all 32 chunks of the chunk grid, which
+    ends there; a further step is refused."""
+    p = _model(tmpdir_session, "c8b_2l.gguf", C8B, 88)
+    g, o = GpuModel(p), orc.Model(p)
+    decode_parity(g, o, 2045, 3, 321, seed=47, kv_f16=kv_f16, spare=0)
     g.close()
     o.close()
 

@@ -137,6 +137,21 @@ def test_tiny_rope_absolute(tiny, tiny_prompt):
         assert rc == 0 and rel_l2(lg, ref) < TOL
 
 
+def test_tiny_decode_to_the_last_row(tiny, tiny_prompt):
+    """130 decode steps in a session of 130 rows (two 64-row chunks and a
+    2-row one), every step against the oracle; the last attends every row of
+    the cache, and a further step is refused."""
+    g, o = tiny
+    s, kv = g.session(130), o.kv(130)
+    tok = int(tiny_prompt[0])
+    for step in range(130):
+        rc, lg = s.decode_step(tok)
+        _, ref = o.decode_step(kv, tok)
+        assert rc == 0 and rel_l2(lg, ref) < TOL, step
+        tok = int(tiny_prompt[(step + 1) % len(tiny_prompt)])
+    assert len(s) == 130 and s.decode_step(tok)[0] == 21
+
+
 def test_errors(tiny):
     g, _ = tiny
     s = g.session(2)
