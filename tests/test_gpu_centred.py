@@ -209,6 +209,50 @@ def test_centred_8b_batched_prefill(tmpdir_session, n):
     o.close()
 
 
+def test_centred_8b_two_prefill_chunks_then_decode(tmpdir_session):
+    """Two batched prefill chunks, 300 ids and then 200 at cache row 300
+    (RoPE positions relative to the chunk, attention within it:
+    src/model/forward.rs:496-538), neither a whole number of 128-row query
+    blocks; then 3 decode steps over all 500 rows.  Sampled rows' logits,
+    every K/V row, and the decode logits and picks against the oracle."""
+    p = _model(tmpdir_session, "c8b_2l.gguf", C8B, 88)
+    g, o = GpuModel(p), orc.Model(p)
+    assert g.batched_prefill()
+    # the guard: the second chunk at absolute positions 300.. stores other K
+    # rows (its own logits hardly move: a common shift of q and k positions
+    # leaves q . k as it is)
+    ids1, ids2 = synth.token_ids(300, C8B.vocab, seed=1300), synth.token_ids(200, C8B.vocab, seed=1301)
+    kv_a, kv_b = o.kv(512), o.kv(512)
+    for kv_x, mode in ((kv_a, orc.ROPE_REFERENCE), (kv_b, orc.ROPE_ABSOLUTE)):
+        assert o.prefill_rows(kv_x, ids1, [299])[0] == 0
+        assert o.prefill_rows(kv_x, ids2, [199], rope_mode=mode)[0] == 0
+    ka, kb = kv_a.export(500)[0], kv_b.export(500)[0]
+    assert rel_l2(_rows_of(kb, o.cfg, 500, 300, 500), _rows_of(ka, o.cfg, 500, 300, 500)) >= SEEN * KV_TOL
+    kv, s = o.kv(512), g.session(512)
+    for n, seed in ((300, 1300), (200, 1301)):
+        ids = synth.token_ids(n, C8B.vocab, seed=seed)
+        rows = sorted({0, 1, n // 3, n // 2, n - 2, n - 1})
+        orc_rc, ref = o.prefill_rows(kv, ids, rows)
+        rc, lg = s.prefill(ids)
+        assert rc == 0 and orc_rc == 0
+        worst = max(rel_l2(lg[t], ref[i]) for i, t in enumerate(rows))
+        assert worst < TOL, (n, worst)
+    kg, vg = s.kv_export(500)
+    kr, vr = kv.export(500)
+    assert rel_l2(kg, kr) < KV_TOL and rel_l2(vg, vr) < KV_TOL
+    tok = 77
+    for step in range(3):
+        rc, lg = s.decode_step(tok)
+        orc_rc, ref = o.decode_step(kv, tok)
+        assert rc == 0 and orc_rc == 0
+        assert rel_l2(lg, ref) < TOL, step
+        tok = orc.argmax(ref)[1]
+        assert last_argmax(lg) == tok, step
+    s.close()
+    g.close()
+    o.close()
+
+
 def test_deterministic_mode_reruns_bit_identical(tmpdir_session):
     """ifx_session_set_deterministic: two sessions decoding the same steps give
     bit-identical logits; two sampled generates with one seed give the same
