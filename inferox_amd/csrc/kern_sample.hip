@@ -308,7 +308,7 @@ constexpr int kCountShift = 40;
 constexpr unsigned long long kMassMask = (1ull << kCountShift) - 1;
 constexpr uint32_t kCap = 4096;  // candidates k_sample_select sorts in LDS
 constexpr uint32_t kNone = 0xffffffffu;
-enum : uint32_t { kModeAll = 1, kModeCand = 2, kModeOneWg = 3 };
+enum : uint32_t { kModeAll = 1, kModeCand = 2, kModeMany = 3 };
 
 constexpr size_t kOffHist = 0;
 constexpr size_t kOffPart = (kOffHist + kBins * 8 + 255) & ~size_t(255);
@@ -455,7 +455,8 @@ __device__ Plan make_plan(const SampleWs& ws, uint32_t V, const DevState* s) {
   __shared__ float S_sh;
   const uint32_t top_k = s->top_k;
   const float top_p = s->top_p;
-  const bool kon = top_k > 0 && top_k < V, pon = top_p < 1.0f;
+  bool kon = top_k > 0 && top_k < V;
+  const bool pon = top_p < 1.0f;
   if (threadIdx.x < 64) {
     const float S = part_total(ws.part);
     if (threadIdx.x == 0) S_sh = S;
@@ -488,6 +489,10 @@ __device__ Plan make_plan(const SampleWs& ws, uint32_t V, const DevState* s) {
   double mtot;
   const uint32_t c0 = wg_scan<kSW>(ct, wt_u, ctot);
   const double m0 = wg_scan<kSW>(mt, wt_d, mtot);
+  // a top-k of at least every positive weight keeps them all (zero weights
+  // are never drawn): no filter
+  if (kon && top_k >= ctot) kon = false;
+  if (!kon && !pon) return pl;
   const double R = (double)top_p * (double)pl.S * (1.0 + 1.0 / 512);
   // each predicate's first position in this thread (they hold from there on);
   // positions ascend with the lane, so a wave's first is its lowest such lane
@@ -525,7 +530,7 @@ __device__ Plan make_plan(const SampleWs& ws, uint32_t V, const DevState* s) {
   __syncthreads();
   pl.lo_bin = last - lo;
   pl.n = n_at;
-  pl.mode = pl.n <= kCap ? kModeCand : kModeOneWg;
+  pl.mode = pl.n <= kCap ? kModeCand : kModeMany;
   return pl;
 }
 
@@ -1061,7 +1066,7 @@ __global__ void __launch_bounds__(kT) k_sample_select(const float* __restrict__ 
     __syncthreads();
     sort_keys(key, n);
     draw_sorted(key, n, S, s);
-  } else if (mode == kModeOneWg) {
+  } else if (mode == kModeMany) {
     if (!draw_many(p, ws, V, S, s, key)) sample_one_wg(logits, p, V, s);
   }
   __syncthreads();

@@ -50,6 +50,21 @@ def test_sample_distribution(T, k, p):
     assert 0.5 * np.abs(freq - want).sum() < 0.04
 
 
+def test_sample_top_k_past_the_positive_weights():
+    """12 of 32 logits so low that their weights underflow to 0: top-k 25
+    keeps every positive weight, so the draw is the unfiltered one (the
+    whole-vocabulary path) and never picks a zero weight."""
+    rng = np.random.default_rng(12)
+    z = (rng.standard_normal(32) * 2.0).astype(np.float32)
+    z[rng.choice(32, 12, replace=False)] = -1.0e4
+    want = numpy_ref.sampler_probs(z, 1.0, 25, 1.0)
+    assert np.count_nonzero(want) == 20
+    got = _draw(z, 1.0, 25, 1.0, seed=21, n=20000)
+    assert set(np.unique(got)) <= set(np.flatnonzero(want))
+    freq = np.bincount(got, minlength=z.size) / got.size
+    assert 0.5 * np.abs(freq - want).sum() < 0.04
+
+
 def test_sample_support_full_vocab():
     rng = np.random.default_rng(5)
     z = (rng.standard_normal(synth.LLAMA3_8B.vocab) * 4.0).astype(np.float32)
