@@ -156,6 +156,11 @@ int ifx_prefill(ifx_session* s, const uint32_t* ids, uint64_t n, float* logits_o
  * for every row into host logits_out [n x vocab]. */
 int ifx_forward(ifx_model* model, const uint32_t* ids, uint64_t n, float* logits_out);
 
+/* Model::forward_last_token_logits (src/model/forward.rs:484-489): the
+ * forward's last row into host logits_out [vocab].  The output head runs for
+ * that row only.  n == 0 is IFX_E_INVALID_ARG (the reference's slice panics). */
+int ifx_forward_last_token_logits(ifx_model* model, const uint32_t* ids, uint64_t n, float* logits_out);
+
 /* Model::generate (src/model/forward.rs:592-612): clear, prefill, then
  * max_tokens greedy steps (argmax ties -> last index, src/model/forward.rs:615-622).
  * The argmax runs on the device; the loop runs without host round trips. */

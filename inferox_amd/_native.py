@@ -56,6 +56,7 @@ SIGNATURES = {
     "ifx_decode_step": (i32, [vp, u32, vp]),
     "ifx_prefill": (i32, [vp, vp, u64, vp]),
     "ifx_forward": (i32, [vp, vp, u64, vp]),
+    "ifx_forward_last_token_logits": (i32, [vp, vp, u64, vp]),
     "ifx_generate": (i32, [vp, vp, u64, u64, vp]),
     "ifx_decode_greedy": (i32, [vp, u32, u64, vp]),
     "ifx_session_set_sampler": (i32, [vp, C.c_float, u32, C.c_float, u64]),

@@ -1228,8 +1228,10 @@ int ifx_session_last_elapsed_ms(const ifx_session* s, float* ms) {
 // Model::forward (src/model/forward.rs:448-482): non-causal attention over the
 // chunk, no cache carried over.  Layer-major: each layer runs its GEMVs for all
 // rows before the next layer, since every row attends to every other row.
-int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out) {
-  clear_error();
+// Model::forward: logits of every row into logits_out [n x vocab], or with
+// last_only those of the last row alone [vocab] (the output head runs for
+// that row only, on the decode head GEMV).
+static int forward_rows(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out, bool last_only) {
   if (!m || (n && (!ids || !logits_out))) return set_error(IFX_E_INVALID_ARG, "null argument");
   for (uint64_t i = 0; i < n; i++)
     if (ids[i] >= m->cfg.vocab_size) return set_error(IFX_E_INVALID_TENSOR_INDEX, "tensor index out of bounds: 0");
@@ -1241,7 +1243,12 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
     int rc = IFX_OK;
     if (hipMemcpyAsync(s->feed_ids, ids, n * 4, hipMemcpyHostToDevice, s->stream) != hipSuccess)
       rc = set_error(IFX_E_HIP, "forward: id upload failed");
-    if (rc == IFX_OK) rc = batched_prefill(s, n, 0, false, logits_out);
+    if (rc == IFX_OK) rc = batched_prefill(s, n, 0, false, last_only ? nullptr : logits_out);
+    // the last row's logits, from the head GEMV the batched prefill runs on it
+    if (rc == IFX_OK && last_only &&
+        hipMemcpyAsync(logits_out, s->logits, (size_t)m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, s->stream) !=
+            hipSuccess)
+      rc = set_error(IFX_E_HIP, "forward: logits copy failed");
     if (rc == IFX_OK && hipStreamSynchronize(s->stream) != hipSuccess) rc = set_error(IFX_E_HIP, "forward: sync failed");
     session_free(s);
     return rc;
@@ -1297,16 +1304,28 @@ int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out
       hip(gemv_residual(gd, X + t * D, st));
     }
   }
-  for (uint64_t t = 0; t < n && rc == IFX_OK; t++) {
+  for (uint64_t t = last_only ? n - 1 : 0; t < n && rc == IFX_OK; t++) {
     GemvLaunch gh;
     gh.seg[0] = seg_of(m->output); gh.nseg = 1; gh.cols = (uint32_t)D; gh.x = X + t * D;
     gh.norm_w = m->out_norm; gh.eps = c.norm_eps;
     hip(gemv_logits(gh, s->logits, s->state, st));
-    hip(hipMemcpyAsync(logits_out + t * V, s->logits, V * 4, hipMemcpyDeviceToHost, st));
+    hip(hipMemcpyAsync(logits_out + (last_only ? 0 : t) * V, s->logits, V * 4, hipMemcpyDeviceToHost, st));
   }
   hip(hipStreamSynchronize(st));
   session_free(s);
   return rc;
+}
+
+int ifx_forward(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out) {
+  clear_error();
+  return forward_rows(m, ids, n, logits_out, false);
+}
+
+int ifx_forward_last_token_logits(ifx_model* m, const uint32_t* ids, uint64_t n, float* logits_out) {
+  clear_error();
+  // the reference slices the last vocab_size logits, which an empty prompt does not have
+  if (n == 0) return set_error(IFX_E_INVALID_ARG, "forward_last_token_logits of an empty prompt");
+  return forward_rows(m, ids, n, logits_out, true);
 }
 
 }  // extern "C"

@@ -88,6 +88,13 @@ class GpuModel:
                                        out.ctypes.data_as(C.c_void_p))
         return rc, out[: ids.size * self.vocab].reshape(ids.size, self.vocab)
 
+    def forward_last_token_logits(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.zeros(self.vocab, np.float32)
+        rc = _native.lib().ifx_forward_last_token_logits(self.h, ids.ctypes.data_as(C.c_void_p), ids.size,
+                                                         out.ctypes.data_as(C.c_void_p))
+        return rc, out
+
 
 class GpuSession:
     def __init__(self, model: GpuModel, max_seq: int, kv_f16: bool = False):

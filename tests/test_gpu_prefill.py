@@ -154,6 +154,25 @@ def test_tiny_batched_forward(tiny):
     assert max(rel_l2(lg[t], ref[t]) for t in range(len(ids))) < TOL
 
 
+@pytest.mark.parametrize("n", [8, 80])
+def test_tiny_forward_last_token_logits(tiny, n):
+    """Model::forward_last_token_logits (src/model/forward.rs:484-489): the
+    forward's last row, with the output head run for that row alone (8 ids:
+    layer-major token replays; 80: the batched path), against the oracle's
+    forward and against ifx_forward's last row; an empty prompt and an id
+    past the vocabulary are refused."""
+    g, o = tiny
+    ids = synth.token_ids(n, synth.TINY.vocab, seed=40 + n)
+    rc, last = g.forward_last_token_logits(ids)
+    orc_rc, ref = o.forward(ids)
+    rc_all, lg = g.forward(ids)
+    assert rc == 0 and orc_rc == 0 and rc_all == 0
+    assert rel_l2(last, ref[-1]) < TOL
+    assert rel_l2(last, lg[-1]) < 1e-5
+    assert g.forward_last_token_logits(np.zeros(0, np.uint32))[0] == 20
+    assert g.forward_last_token_logits(np.array([1, synth.TINY.vocab], np.uint32))[0] == 10
+
+
 def test_8b_shape_batched_prefill(tmpdir_session):
     """Full-width Llama-3-8B shape, two layers: a 96-id chunk through the
     Q4_K/Q6_K GEMMs (default threshold), logits of every row and the KV rows."""
