@@ -17,7 +17,9 @@ reported apart from `value`.
 
 Profiling aids: --no-graph launches each step's kernels directly instead of
 replaying the captured step graph (for kernel tracers); --copy-probe only runs
-a device-to-device copy of known size, the calibration for HBM byte counters.
+a device-to-device copy of known size, the calibration for HBM byte counters;
+--sampler T,K,P,SIGMA only runs 200 device draws (temperature T, top-k K,
+top-p P) from 128256 seeded logits ~ N(0, SIGMA^2), for a kernel tracer.
 """
 from __future__ import annotations
 
@@ -73,6 +75,8 @@ def parse():
     ap.add_argument("--kv", choices=["f32", "f16"], default="f32",
                     help="KV cache element type: f32 (the reference's cache, the parity mode) or f16 (rounded rows)")
     ap.add_argument("--copy-probe", action="store_true", help="only a d2d copy of known size (counter calibration)")
+    ap.add_argument("--sampler", default=None, metavar="T,K,P,SIGMA",
+                    help="only 200 device draws from 128256 seeded logits (sampler kernel tracing)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
     ap.add_argument("--prefill-reps", type=int, default=3)
@@ -109,6 +113,27 @@ def copy_probe():
     L.ifx_free(out)
     L.ifx_tensor_free(t)
     print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "launches": 8, "kernel": "k_dequant_dev"}), flush=True)
+
+
+def sampler_probe(spec):
+    """200 draws of ifx_sample_logits (temperature, top-k, top-p) from 128256
+    logits ~ N(0, sigma^2) of a fixed seed: the sampler's launches (the logits'
+    maximum, weights, plan and gather, select, finalize) 200 times, for a
+    kernel tracer; the wall time includes the call's allocations and copies."""
+    from inferox_amd import _native, synth
+    T, K, P, sig = (float(v) for v in spec.split(","))
+    z = (np.random.default_rng(5).standard_normal(synth.LLAMA3_8B.vocab) * sig).astype(np.float32)
+    out = np.zeros(200, np.uint32)
+    L = _native.lib()
+    t0 = time.perf_counter()
+    rc = L.ifx_sample_logits(z.ctypes.data_as(C.c_void_p), z.size, T, int(K), P, 9, out.size,
+                             out.ctypes.data_as(C.c_void_p))
+    wall = time.perf_counter() - t0
+    if rc != 0:
+        raise SystemExit(f"ifx_sample_logits: {(L.ifx_last_error() or b'').decode()}")
+    print(json.dumps({"sampler": {"temperature": T, "top_k": int(K), "top_p": P, "sigma": sig},
+                      "vocab": int(z.size), "draws": int(out.size), "wall_ms": round(wall * 1e3, 2),
+                      "distinct_tokens": int(np.unique(out).size)}), flush=True)
 
 
 def traffic_for(kclass):
@@ -386,6 +411,9 @@ def main():
         os.environ["IFX_NO_GRAPH"] = "1"  # read by the library at the first step
     if args.copy_probe:
         copy_probe()
+        return
+    if args.sampler:
+        sampler_probe(args.sampler)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the token loop runs on a single MI355X; "
