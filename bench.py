@@ -416,7 +416,7 @@ def main():
         sampler_probe(args.sampler)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the token loop runs on a single MI355X; "
+        print(json.dumps({"error": "bench.py measures one GPU: the token loop runs on a single MI355X; "
                           "multi-GPU sharding (heads and FFN columns split per GPU) is not built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
