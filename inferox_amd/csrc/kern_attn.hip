@@ -561,6 +561,7 @@ void launch_typed(const AttnArgs& a0, hipStream_t st, bool merge) {
   else if (a.head_dim == 128 && G == 1) IFX_ATTN(128, 1);
   else if (a.head_dim == 64 && G == 4) IFX_ATTN(64, 4);
   else if (a.head_dim == 64 && G == 1) IFX_ATTN(64, 1);
+  else if (a.head_dim == 48 && G == 1) IFX_ATTN(48, 1);  // the tiny Llama shape (dim 288, 6 heads)
   else IFX_ATTN(0, 0);
 #undef IFX_ATTN
 }
