@@ -19,7 +19,9 @@ Profiling aids: --no-graph launches each step's kernels directly instead of
 replaying the captured step graph (for kernel tracers); --copy-probe only runs
 a device-to-device copy of known size, the calibration for HBM byte counters;
 --sampler T,K,P,SIGMA only runs 200 device draws (temperature T, top-k K,
-top-p P) from 128256 seeded logits ~ N(0, SIGMA^2), for a kernel tracer.
+top-p P) from 128256 seeded logits ~ N(0, SIGMA^2), for a kernel tracer;
+--sampled-generate T,K,P times 256 tokens after a 512-id prompt, greedy and
+drawn on the device, on the 8B model.
 """
 from __future__ import annotations
 
@@ -77,6 +79,8 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true", help="only a d2d copy of known size (counter calibration)")
     ap.add_argument("--sampler", default=None, metavar="T,K,P,SIGMA",
                     help="only 200 device draws from 128256 seeded logits (sampler kernel tracing)")
+    ap.add_argument("--sampled-generate", default=None, metavar="T,K,P",
+                    help="only 256 generated tokens after a 512-id prompt, greedy against sampled")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill workload (512- and 2048-id prompts): tok/s, time to first token")
     ap.add_argument("--prefill-reps", type=int, default=3)
@@ -184,6 +188,33 @@ def measure_other_kv(L, model, spec, kv_type, ctx, steps, warmup):
     L.ifx_session_destroy(sess)
     return {"kv_cache": "f16" if kv_type == 1 else "f32", "tok_s": round(steps / wall, 2),
             "ms_per_step": round(wall / steps * 1e3, 4), "first_tokens": [int(x) for x in out[:4]]}
+
+
+def measure_sampled_generate(L, model, spec, cfg):
+    """256 tokens generated after a 512-id prompt, greedy (ifx_generate)
+    against drawn by the device sampler (ifx_generate_sampled: temperature,
+    top-k, top-p, seed 7), alternated twice; the device-loop time of each call
+    (ifx_session_last_elapsed_ms)."""
+    from inferox_amd import synth
+    from inferox_amd._native import check
+    T, K, P = cfg.split(",")
+    T, K, P = float(T), int(K), float(P)
+    sess = C.c_void_p()
+    check(L.ifx_session_create(model, 1024, C.byref(sess)), "session_create")
+    ids = synth.token_ids(512, spec.vocab, seed=3)
+    out = np.zeros(256, np.uint32)
+    res = {"greedy": [], "sampled": []}
+    check(L.ifx_session_set_sampler(sess, T, K, P, 7), "set_sampler")
+    for mode in ("greedy", "sampled", "greedy", "sampled"):
+        f = L.ifx_generate_sampled if mode == "sampled" else L.ifx_generate
+        check(f(sess, ids.ctypes.data_as(C.c_void_p), ids.size, out.size, out.ctypes.data_as(C.c_void_p)), mode)
+        ms = C.c_float()
+        check(L.ifx_session_last_elapsed_ms(sess, C.byref(ms)), "elapsed")
+        res[mode].append(round(out.size / ms.value * 1e3, 1))
+    L.ifx_session_destroy(sess)
+    return {"sampled_generate": {"temperature": T, "top_k": K, "top_p": P, "seed": 7},
+            "workload": f"{spec.name}: 512-id prompt, 256 generated tokens, device loop",
+            "greedy_tok_s": res["greedy"], "sampled_tok_s": res["sampled"]}
 
 
 def measure_prefill(L, model, spec, sizes, reps):
@@ -447,6 +478,9 @@ def main():
     log(f"model uploaded in {time.time() - t0:.1f} s: {dev_b.value / 1e9:.3f} GB in HBM "
         f"({gguf_b.value / 1e9:.3f} GB stored)")
 
+    if args.sampled_generate:
+        print(json.dumps(measure_sampled_generate(L, model, spec, args.sampled_generate)), flush=True)
+        return
     if args.prefill_only:
         sizes = [int(x) for x in args.prefill_sizes.split(",")]
         res = measure_prefill(L, model, spec, sizes, args.prefill_reps)
