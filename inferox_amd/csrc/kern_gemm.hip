@@ -378,7 +378,9 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm(GemmArgs a, Ep ep) {
   __shared__ __attribute__((aligned(16))) _Float16 lw[2][kNw][kWPlane];  // [buffer][p hi, p lo]
   __shared__ __attribute__((aligned(16))) typename Q::Side side[2];
   __shared__ int rexp[kBM];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index as a scalar: the wave's fragment rows and columns are
+  // uniform over it and stay out of the vector registers
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const uint32_t m0 = blockIdx.y * kBM;
   // output columns of the tile (paired: gate rows n0.. in W rows 0..127, up in 128..255)
