@@ -974,6 +974,7 @@ int ifx_sample_logits(const float* logits, uint32_t vocab, float temperature, ui
   clear_error();
   if (!logits || (n_draws && !out) || vocab == 0 || vocab >= (1u << 24))
     return set_error(IFX_E_INVALID_ARG, "sample: bad arguments");
+  IFX_TRY(device_init());
   if (!(temperature > 0.f) || !isfinite(temperature) || !(top_p >= 0.f && top_p <= 1.f))
     return set_error(IFX_E_INVALID_ARG, "sample needs temperature > 0 and 0 <= top_p <= 1");
   hipStream_t st = nullptr;
