@@ -129,6 +129,11 @@ def test_device_required_after_parse(tmp_path):
     assert _open_product(p) == 25
     h = C.c_void_p()
     assert _native.lib().ifx_malloc(C.byref(h), 16) == 25
+    # the sampler entry point checks its arguments, then the device
+    logits = (C.c_float * 8)(*range(8))
+    out = (C.c_uint32 * 2)()
+    assert _native.lib().ifx_sample_logits(logits, 8, 1.0, 0, 1.0, 1, 2, out) == 25
+    assert _native.lib().ifx_sample_logits(logits, 0, 1.0, 0, 1.0, 1, 2, out) == 20
 
 
 def test_synth_is_deterministic(tmp_path):
