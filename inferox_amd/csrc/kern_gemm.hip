@@ -799,6 +799,116 @@ __global__ void __launch_bounds__(256) k_prep_rows(const float* x, uint32_t ld, 
   }
 }
 
+// The same with the thread's chunks of the row held in registers from one
+// load (up to NCT of them: rows of up to 2048 NCT columns), instead of
+// reading the row again for the maximum and the split.  Same arithmetic in
+// the same order: the same bits.
+template <int NCT>
+__global__ void __launch_bounds__(256) k_prep_rows_reg(const float* x, uint32_t ld, uint32_t cols, const float* nw,
+                                                       float eps, uint16_t* hi, uint16_t* lo, uint16_t* gsum,
+                                                       int* rexp) {
+  const uint32_t t = blockIdx.x, nch = cols / 8;
+  const float4* r4 = (const float4*)(x + (uint64_t)t * ld);
+  const float4* w4 = (const float4*)nw;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float red[4];
+  __shared__ float bcast;
+  // the thread's chunks tid + 256 j, loaded once (zeros past the row)
+  float4 ru[NCT][2];
+#pragma unroll
+  for (int j = 0; j < NCT; j++) {
+    const uint32_t c = tid + 256u * j;
+    ru[j][0] = c < nch ? r4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ru[j][1] = c < nch ? r4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  auto row8 = [&](int j, uint32_t c, float* v, float scale) {
+    const float4 u0 = ru[j][0], u1 = ru[j][1];
+    v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+    v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    if (nw) {
+      const float4 g0 = w4[2 * c], g1 = w4[2 * c + 1];
+      const float w[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = (v[k] * scale) * w[k];
+    }
+  };
+  float scale = 1.f;
+  if (nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCT; j++) {
+      if (tid + 256u * j >= nch) break;
+      const float4 u0 = ru[j][0], u1 = ru[j][1];
+      ss = fmaf(u0.x, u0.x, ss); ss = fmaf(u0.y, u0.y, ss); ss = fmaf(u0.z, u0.z, ss); ss = fmaf(u0.w, u0.w, ss);
+      ss = fmaf(u1.x, u1.x, ss); ss = fmaf(u1.y, u1.y, ss); ss = fmaf(u1.z, u1.z, ss); ss = fmaf(u1.w, u1.w, ss);
+    }
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (tid == 0) bcast = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
+    __syncthreads();
+    scale = bcast;
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCT; j++) {
+    const uint32_t c = tid + 256u * j;
+    if (c >= nch) break;
+    float v[8];
+    row8(j, c, v, scale);
+#pragma unroll
+    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  __syncthreads();
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = (int)((__float_as_uint(m) >> 23) & 255u) - 127;
+  e = e < -100 ? -100 : e;
+  if (tid == 0) rexp[t] = e;
+  const float s = ldexpf(1.0f, 14 - e);
+  const bool sums = gsum && cols % 256 == 0;
+  uint16_t* ho = hi + (uint64_t)t * cols;
+  uint16_t* lw = lo + (uint64_t)t * cols;
+#pragma unroll
+  for (int j = 0; j < NCT; j++) {
+    if (256u * j >= nch) break;
+    const uint32_t c = 256u * j + tid;
+    const bool ok = c < nch;  // nch is a multiple of 4: a group's threads agree
+    float v[8];
+    if (ok) row8(j, c, v, scale);
+    else
+      for (int k = 0; k < 8; k++) v[k] = 0.f;
+    h8 vh, vl;
+    float s8 = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const float y = v[(p >> 1) + 4 * (p & 1)] * s;
+      vh[p] = (_Float16)y;
+      vl[p] = (_Float16)(y - (float)vh[p]);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) s8 += v[k] * s;
+    if (ok) {
+      *(h8*)(ho + 8u * c) = vh;
+      *(h8*)(lw + 8u * c) = vl;
+    }
+    if (sums) {
+      s8 += __shfl_xor(s8, 1, 64);
+      s8 += __shfl_xor(s8, 2, 64);
+      if (ok && (c & 3u) == 0) {
+        const uint32_t g = c >> 2;
+        const float sg = s8 * 0.03125f;
+        const _Float16 sh = (_Float16)sg, sl = (_Float16)(sg - (float)sh);
+        _Float16* dst = (_Float16*)gsum + ((uint64_t)t * (cols >> 8) + (g >> 3)) * 16u + (g & 7u);
+        dst[0] = sh;
+        dst[8] = sl;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 bool gemm_type(uint32_t t) { return t == T_Q4K || t == T_Q6K || t == T_Q8_0 || t == T_Q4_0; }
@@ -838,8 +948,16 @@ hipError_t launch_prep_rows(const float* x, uint32_t rows, uint32_t ld, uint32_t
   if (cols == 0 || cols % 32 || ld % 4 || ld < cols || !out.hi || !out.lo || !out.rexp || out.k != cols ||
       rows > out.m)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_prep_rows, dim3(rows), dim3(256), 0, st, x, ld, cols, norm_w, eps, (uint16_t*)out.hi,
-                     (uint16_t*)out.lo, (uint16_t*)out.gsum, (int*)out.rexp);
+  const uint32_t nct = (cols / 8 + 255) / 256;  // chunks of 8 per thread
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, st, x, ld, cols, norm_w, eps, (uint16_t*)out.hi,
+                       (uint16_t*)out.lo, (uint16_t*)out.gsum, (int*)out.rexp);
+  };
+  if (nct <= 2) go(k_prep_rows_reg<2>);
+  else if (nct <= 4) go(k_prep_rows_reg<4>);
+  else if (nct <= 8) go(k_prep_rows_reg<8>);
+  else if (nct <= 16) go(k_prep_rows_reg<16>);
+  else go(k_prep_rows);
   return hipGetLastError();
 }
 
